@@ -1,0 +1,164 @@
+/*
+ * cacheblend_hip.h -- C ABI of the MI355X (gfx950) CacheBlend KV data-movement
+ * and selection kernels.
+ *
+ * Plain pointers and sizes only. Every pointer named *_dev is device memory;
+ * every entry point is stream-ordered on `stream` (a hipStream_t, NULL = the
+ * legacy default stream), never synchronises, never allocates, and returns
+ * CBK_OK or a negative CBK_ERR_* code (cbk_last_error() holds a message for
+ * the calling thread). Strides are in BYTES unless named *_elems.
+ *
+ * Each entry point cites the reference (zoudinghong2000/PIC-KVCache) function
+ * it replaces. The reference is a Python/torch package; its "FFI" for this
+ * path is the Python signature, which the ctypes binding in
+ * pic-kvcache_amd/cacheblend_vllm/_native.py maps onto these symbols.
+ */
+#ifndef CACHEBLEND_HIP_H_
+#define CACHEBLEND_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* cbk_stream_t; /* hipStream_t */
+
+enum {
+  CBK_OK = 0,
+  CBK_ERR_INVALID = -1,     /* bad argument: shape, stride, alignment, range */
+  CBK_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
+  CBK_ERR_LAUNCH = -3,      /* HIP launch/runtime failure */
+  CBK_ERR_WORKSPACE = -4    /* workspace too small */
+};
+
+enum { CBK_DTYPE_F32 = 0, CBK_DTYPE_BF16 = 1, CBK_DTYPE_F16 = 2 };
+
+/* ABI version, bumped on any signature change. */
+int cbk_abi_version(void);
+/* Static string for a CBK_* code. */
+const char* cbk_error_string(int code);
+/* Message of the last failed call on this thread ("" if none). */
+const char* cbk_last_error(void);
+
+/*
+ * One paged KV layer, any of vLLM's three layouts (reference
+ * cacheblend_vllm/kv_layout.py:12-20, 110-118):
+ *   merged_first [2, NB, bs, H, D]  k_base = &kv[0,0,0], v_base = &kv[1,0,0]
+ *   merged_block [NB, 2, bs, H, D]  k_base = &kv[0,0,0], v_base = &kv[0,1,0]
+ *   separate     K,V [NB, bs, H, D] k_base = K, v_base = V
+ * A token's [H, D] row must be contiguous (row_bytes bytes).
+ */
+typedef struct cbk_kv_desc {
+  void* k_base;
+  void* v_base;
+  int64_t num_blocks;
+  int64_t block_size;   /* tokens per block */
+  int64_t block_stride; /* bytes between blocks */
+  int64_t token_stride; /* bytes between tokens of one block */
+  int64_t row_bytes;    /* bytes of one token's [H, D] row */
+} cbk_kv_desc;
+
+/*
+ * Paged gather: out_{k,v}[t] = {K,V}[slot_t / bs][slot_t % bs].
+ * Replaces gather_paged_kv(kv_layer, slot_mapping, block_size, out)
+ * (cacheblend_vllm/kv_layout.py:90-122) and the native paged-cache load it
+ * dispatches to (kv_layout.py:27-87). slots_dev: int64 [num_tokens].
+ * A slot outside [0, num_blocks*block_size) writes a zero row and adds one
+ * to *bad_slots_dev when that pointer is non-NULL.
+ */
+int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                     void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
+                     int32_t* bad_slots_dev, cbk_stream_t stream);
+
+/*
+ * Paged scatter: {K,V}[slot_t / bs][slot_t % bs] = in_{k,v}[t].
+ * Replaces scatter_paged_kv(contiguous, kv_layer, slot_mapping, block_size)
+ * (cacheblend_vllm/kv_layout.py:125-161) and reshape_and_cache
+ * (kv_layout.py:137-146). Out-of-range slots are skipped and counted.
+ */
+int cbk_paged_scatter(const void* in_k_dev, const void* in_v_dev, int64_t in_token_stride,
+                      const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                      int32_t* bad_slots_dev, cbk_stream_t stream);
+
+/*
+ * Multi-layer gather in one launch per 64 layers: for layer l,
+ * out + l*out_layer_stride + c*out_plane_stride + t*out_token_stride
+ * receives plane c of kv[l] at slot t. All layers share the geometry of
+ * kv[0] (only k_base/v_base differ). This is the whole-prompt store path of
+ * CacheBlendConnectorV1.save_kv_layer/_enqueue_store_batch
+ * (cacheblend_vllm/connector.py:281-447) batched over layers.
+ */
+int cbk_paged_gather_layers(const cbk_kv_desc* kv, int32_t num_layers, const int64_t* slots_dev,
+                            int64_t num_tokens, void* out_dev, int64_t out_layer_stride,
+                            int64_t out_plane_stride, int64_t out_token_stride,
+                            int32_t* bad_slots_dev, cbk_stream_t stream);
+
+/* Inverse of cbk_paged_gather_layers (batched scatter_paged_kv). */
+int cbk_paged_scatter_layers(const void* in_dev, int64_t in_layer_stride, int64_t in_plane_stride,
+                             int64_t in_token_stride, const cbk_kv_desc* kv, int32_t num_layers,
+                             const int64_t* slots_dev, int64_t num_tokens, int32_t* bad_slots_dev,
+                             cbk_stream_t stream);
+
+/*
+ * K-deviation scores: scores[i] = sum_j (f32(fresh[i, j]) - f32(cached[r_i, j]))^2
+ * over `width` elements, r_i = cached_rows_dev ? cached_rows_dev[i] : cached_row0 + i.
+ * A row index outside [0, cached_num_rows) yields a NaN score (never read).
+ * Replaces the inline score of Qwen3BlendExecutor._compute_layer
+ * (cacheblend_vllm/ascend.py:534-538). Row strides are in elements.
+ */
+int cbk_kdev_scores(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
+                    int64_t cached_row_stride_elems, int64_t cached_num_rows,
+                    const int64_t* cached_rows_dev, int64_t cached_row0, int64_t n, int64_t width,
+                    int32_t dtype, float* scores_dev, cbk_stream_t stream);
+
+/* Workspace bytes cbk_select / cbk_kdev_select need for n tokens. */
+size_t cbk_select_workspace_bytes(int64_t n);
+
+/*
+ * Budgeted selection: sorted int64 indices of
+ *   base | top_k(scores.masked_fill(base, -inf)),
+ *   base = gap | forced | dilate(gap, radius),
+ *   k = budget(n, #gap, #base, ratio)   (int(cached * ratio), >= 1, <= available)
+ * with ties at the k-th score going to the lower index. Writes the indices to
+ * out_idx_dev[0 .. count) (capacity n) and count to *out_count_dev.
+ * forced_dev may be NULL; radius 0 disables dilation.
+ * Replaces Qwen3BlendExecutor._select (cacheblend_vllm/ascend.py:757-796) at
+ * TP1, composed with the overflow dilation of _sparse_q_scores
+ * (ascend.py:662-671) when radius > 0. Masks are uint8 (0/1).
+ */
+int cbk_select(const float* scores_dev, const uint8_t* gap_dev, const uint8_t* forced_dev,
+               int64_t n, int64_t radius, double ratio, int64_t* out_idx_dev,
+               int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+               cbk_stream_t stream);
+
+/*
+ * K-deviation selection in one call: cbk_kdev_scores (scores_dev receives
+ * the scores) followed by cbk_select on them, with no host round trip.
+ */
+int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
+                    int64_t cached_row_stride_elems, int64_t cached_num_rows,
+                    const int64_t* cached_rows_dev,
+                    int64_t cached_row0, int64_t n, int64_t width, int32_t dtype,
+                    const uint8_t* gap_dev, const uint8_t* forced_dev, int64_t radius,
+                    double ratio, float* scores_dev, int64_t* out_idx_dev,
+                    int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+                    cbk_stream_t stream);
+
+/* Largest dilation radius cbk_select / cbk_kdev_select accept. */
+#define CBK_MAX_DILATION_RADIUS 4096
+
+/*
+ * forced_dev[i] = any(gap_dev[max(0, i - radius) .. min(n, i + radius + 1)))
+ * Replaces the prefix-sum window of _sparse_q_scores
+ * (cacheblend_vllm/ascend.py:662-671).
+ */
+int cbk_dilate(const uint8_t* gap_dev, int64_t n, int64_t radius, uint8_t* forced_dev,
+               cbk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CACHEBLEND_HIP_H_ */

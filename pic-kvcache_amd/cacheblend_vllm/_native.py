@@ -1,0 +1,161 @@
+"""ctypes binding of libcacheblend_hip.so (the gfx950 kernels' C ABI).
+
+The declarations mirror include/cacheblend_hip.h one for one. Loading fails
+loudly: there is no CPU or torch fallback for any kernel in this package.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libcacheblend_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+CBK_OK = 0
+CBK_ERR_INVALID = -1
+CBK_ERR_UNSUPPORTED = -2
+CBK_ERR_LAUNCH = -3
+CBK_ERR_WORKSPACE = -4
+
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+MAX_DILATION_RADIUS = 4096
+
+c_i64 = ctypes.c_int64
+c_i32 = ctypes.c_int32
+c_vp = ctypes.c_void_p
+
+
+class KVDesc(ctypes.Structure):
+    """``cbk_kv_desc``: one paged KV layer (base pointers, geometry in bytes)."""
+
+    _fields_ = [
+        ("k_base", c_vp),
+        ("v_base", c_vp),
+        ("num_blocks", c_i64),
+        ("block_size", c_i64),
+        ("block_stride", c_i64),
+        ("token_stride", c_i64),
+        ("row_bytes", c_i64),
+    ]
+
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "cbk_abi_version": (ctypes.c_int, []),
+    "cbk_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "cbk_last_error": (ctypes.c_char_p, []),
+    "cbk_paged_gather": (
+        ctypes.c_int,
+        [ctypes.POINTER(KVDesc), c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp],
+    ),
+    "cbk_paged_scatter": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_i64, ctypes.POINTER(KVDesc), c_vp, c_i64, c_vp, c_vp],
+    ),
+    "cbk_paged_gather_layers": (
+        ctypes.c_int,
+        [ctypes.POINTER(KVDesc), c_i32, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp],
+    ),
+    "cbk_paged_scatter_layers": (
+        ctypes.c_int,
+        [c_vp, c_i64, c_i64, c_i64, ctypes.POINTER(KVDesc), c_i32, c_vp, c_i64, c_vp, c_vp],
+    ),
+    "cbk_kdev_scores": (
+        ctypes.c_int,
+        [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32, c_vp, c_vp],
+    ),
+    "cbk_select_workspace_bytes": (ctypes.c_size_t, [c_i64]),
+    "cbk_select": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp],
+    ),
+    "cbk_kdev_select": (
+        ctypes.c_int,
+        [
+            c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32,
+            c_vp, c_vp, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp,
+        ],
+    ),
+    "cbk_dilate": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it is missing or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_NAME} is not built at {LIB_PATH}; run `make -C pic-kvcache_amd/csrc` "
+                "(hipcc --offload-arch=gfx950). cacheblend_vllm has no CPU fallback."
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.cbk_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{LIB_NAME} ABI {version} != expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python exception matching a CBK_* return code."""
+    if rc == CBK_OK:
+        return
+    message = load().cbk_last_error().decode(errors="replace")
+    text = f"{what}: {message}" if message else what
+    if rc == CBK_ERR_INVALID:
+        raise ValueError(text)
+    if rc == CBK_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise RuntimeError(f"{text} ({load().cbk_error_string(rc).decode()})")
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(tensor: torch.Tensor, what: str) -> None:
+    if tensor.device.type != "cuda":
+        raise RuntimeError(
+            f"{what} must be a ROCm device tensor (got {tensor.device}); "
+            "cacheblend_vllm runs its kernels only on the GPU"
+        )
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A reusable uint8 device workspace of at least ``nbytes`` for the
+    current stream of ``device`` (kernels on one stream are ordered, so one
+    buffer per stream is never used by two calls at once)."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           stream_handle(device))
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf

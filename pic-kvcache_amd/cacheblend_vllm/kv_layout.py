@@ -1,0 +1,374 @@
+"""Paged KV gather/scatter for vLLM KV layouts on MI355X.
+
+Drop-in for the reference module of the same name
+(cacheblend_vllm/kv_layout.py): same functions, arguments, return values and
+exceptions, executed by the gfx950 bandwidth kernels of libcacheblend_hip.so
+(cbk_paged_gather / cbk_paged_scatter and their multi-layer forms).
+
+Layouts (reference kv_layout.py:12-20, 110-118):
+  separate      (K, V), each [num_blocks, block_size, *row]
+  merged_first  [2, num_blocks, block_size, *row]   (tested first)
+  merged_block  [num_blocks, 2, block_size, *row]
+The ``*row`` dims of one token (normally [kv_heads, head_dim]) must be
+contiguous. Slots index ``block * block_size + offset``.
+
+Differences from the reference torch path, on purpose:
+  * slots outside ``[0, num_blocks * block_size)`` raise ``IndexError`` when
+    the slot tensor is on the host (torch would wrap negative slots). Device
+    slot tensors are not read back (no sync); an out-of-range device slot
+    gathers a zero row / skips the write instead of faulting.
+  * results are always contiguous ``[2, T, *row]`` (the reference returns a
+    transposed view for merged_block).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from . import _native
+
+KVLayer = torch.Tensor | Sequence[torch.Tensor]
+
+
+def _separate(kv_layer: KVLayer) -> tuple[torch.Tensor, torch.Tensor] | None:
+    """Follows reference kv_layout.py:12-20."""
+    if isinstance(kv_layer, torch.Tensor):
+        return None
+    if len(kv_layer) != 2:
+        raise ValueError(f"separate KV layout requires two tensors, got {len(kv_layer)}")
+    key, value = kv_layer
+    if not isinstance(key, torch.Tensor) or not isinstance(value, torch.Tensor):
+        raise TypeError("separate KV layout must contain tensors")
+    return key, value
+
+
+def kv_planes(kv_layer: KVLayer) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(K, V)`` views shaped ``[num_blocks, block_size, *row]``."""
+    separate = _separate(kv_layer)
+    if separate is not None:
+        return separate
+    assert isinstance(kv_layer, torch.Tensor)
+    if kv_layer.shape[0] == 2:
+        return kv_layer[0], kv_layer[1]
+    if kv_layer.ndim >= 4 and kv_layer.shape[1] == 2:
+        return kv_layer[:, 0], kv_layer[:, 1]
+    raise ValueError(f"unsupported vLLM KV layout {tuple(kv_layer.shape)}")
+
+
+def _rows_contiguous(t: torch.Tensor, first_row_dim: int) -> bool:
+    expected = 1
+    for dim in range(t.ndim - 1, first_row_dim - 1, -1):
+        if t.shape[dim] != 1 and t.stride(dim) != expected:
+            return False
+        expected *= t.shape[dim]
+    return True
+
+
+def kv_desc(kv_layer: KVLayer, block_size: int) -> tuple[_native.KVDesc, torch.Tensor]:
+    """Describe one paged layer for the C ABI; returns (desc, K plane)."""
+    key, value = kv_planes(kv_layer)
+    if key.shape != value.shape or key.dtype != value.dtype or key.device != value.device:
+        raise ValueError("K and V planes must share shape, dtype and device")
+    if key.ndim < 3:
+        raise ValueError(f"unsupported vLLM KV layout {tuple(key.shape)}")
+    if block_size <= 0 or block_size > key.shape[1]:
+        raise ValueError(f"block_size {block_size} does not fit KV blocks of {key.shape[1]} tokens")
+    if key.stride() != value.stride():
+        raise ValueError("K and V planes must share strides")
+    if not _rows_contiguous(key, 2):
+        raise ValueError("each token's KV row must be contiguous in the paged cache")
+    _native.require_device(key, "paged KV cache")
+    es = key.element_size()
+    row_elems = 1
+    for d in key.shape[2:]:
+        row_elems *= d
+    desc = _native.KVDesc(
+        key.data_ptr(),
+        value.data_ptr(),
+        key.shape[0],
+        block_size,
+        key.stride(0) * es,
+        key.stride(1) * es,
+        row_elems * es,
+    )
+    return desc, key
+
+
+def _device_slots(slot_mapping: torch.Tensor, device: torch.device, num_slots: int) -> torch.Tensor:
+    """Reference kv_layout.py:23-24, plus a host-side range check."""
+    if slot_mapping.device.type == "cpu" and slot_mapping.numel():
+        lo = int(slot_mapping.min())
+        hi = int(slot_mapping.max())
+        if lo < 0 or hi >= num_slots:
+            raise IndexError(
+                f"slot_mapping holds slots in [{lo}, {hi}], outside [0, {num_slots})"
+            )
+    return slot_mapping.to(device=device, dtype=torch.long, non_blocking=True).contiguous()
+
+
+def _plane_rows_ok(plane: torch.Tensor) -> bool:
+    return _rows_contiguous(plane, 1)
+
+
+def gather_paged_kv(
+    kv_layer: KVLayer,
+    slot_mapping: torch.Tensor,
+    block_size: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Gather paged KV as contiguous ``[2, tokens, *row]``.
+
+    Drop-in for reference kv_layout.py:90-122; runs cbk_paged_gather.
+    """
+    desc, key = kv_desc(kv_layer, block_size)
+    tokens = int(slot_mapping.numel())
+    shape = (2, tokens, *key.shape[2:])
+    if out is not None:
+        if tuple(out.shape) != shape:
+            raise ValueError(f"gather output has shape {tuple(out.shape)}, expected {shape}")
+        if out.dtype != key.dtype or out.device != key.device:
+            raise ValueError("gather output must match the KV cache dtype and device")
+        target = out
+    else:
+        target = torch.empty(shape, dtype=key.dtype, device=key.device)
+    if tokens == 0:
+        return target
+    direct = (
+        _plane_rows_ok(target[0])
+        and _plane_rows_ok(target[1])
+        and target.stride(1) == target[0].stride(0)
+    )
+    dst = target if direct else torch.empty(shape, dtype=key.dtype, device=key.device)
+    slots = _device_slots(slot_mapping, key.device, desc.num_blocks * block_size)
+    es = key.element_size()
+    lib = _native.load()
+    rc = lib.cbk_paged_gather(
+        desc,
+        slots.data_ptr(),
+        tokens,
+        dst[0].data_ptr(),
+        dst[1].data_ptr(),
+        dst.stride(1) * es,
+        None,
+        _native.stream_handle(key.device),
+    )
+    _native.check(rc, "gather_paged_kv")
+    if dst is not target:
+        target.copy_(dst)
+    return target
+
+
+def scatter_paged_kv(
+    contiguous: torch.Tensor,
+    kv_layer: KVLayer,
+    slot_mapping: torch.Tensor,
+    block_size: int,
+) -> None:
+    """Scatter ``[2, tokens, *row]`` into a vLLM paged KV layer in place.
+
+    Drop-in for reference kv_layout.py:125-161; runs cbk_paged_scatter.
+    """
+    if contiguous.shape[0] != 2:
+        raise ValueError("contiguous KV must have K/V as its first dimension")
+    desc, key = kv_desc(kv_layer, block_size)
+    tokens = int(slot_mapping.numel())
+    shape = (2, tokens, *key.shape[2:])
+    if tuple(contiguous.shape) != shape:
+        raise ValueError(f"contiguous KV has shape {tuple(contiguous.shape)}, expected {shape}")
+    if contiguous.dtype != key.dtype:
+        raise RuntimeError(
+            "Index put requires the source and destination dtypes match, "
+            f"got {key.dtype} for the destination and {contiguous.dtype} for the source."
+        )
+    if tokens == 0:
+        return
+    src = contiguous.to(device=key.device)
+    if not (_plane_rows_ok(src[0]) and _plane_rows_ok(src[1]) and src.stride(1) == src[0].stride(0)):
+        src = src.contiguous()
+    slots = _device_slots(slot_mapping, key.device, desc.num_blocks * block_size)
+    es = key.element_size()
+    lib = _native.load()
+    rc = lib.cbk_paged_scatter(
+        src[0].data_ptr(),
+        src[1].data_ptr(),
+        src.stride(1) * es,
+        desc,
+        slots.data_ptr(),
+        tokens,
+        None,
+        _native.stream_handle(key.device),
+    )
+    _native.check(rc, "scatter_paged_kv")
+
+
+def _layer_descs(kv_layers: Sequence[KVLayer], block_size: int):
+    if len(kv_layers) == 0:
+        raise ValueError("at least one KV layer is required")
+    descs = (_native.KVDesc * len(kv_layers))()
+    first = None
+    for i, layer in enumerate(kv_layers):
+        desc, key = kv_desc(layer, block_size)
+        if first is None:
+            first = key
+        elif key.shape != first.shape or key.dtype != first.dtype or key.stride() != first.stride():
+            raise ValueError("every KV layer must share shape, dtype and strides")
+        descs[i] = desc
+    return descs, first
+
+
+def gather_paged_kv_layers(
+    kv_layers: Sequence[KVLayer],
+    slot_mapping: torch.Tensor,
+    block_size: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Gather the same slots of every layer into ``[L, 2, tokens, *row]``.
+
+    One kernel launch per 64 layers (cbk_paged_gather_layers); equals
+    ``stack([gather_paged_kv(l, slot_mapping, block_size) for l in kv_layers])``.
+    """
+    descs, key = _layer_descs(kv_layers, block_size)
+    tokens = int(slot_mapping.numel())
+    shape = (len(kv_layers), 2, tokens, *key.shape[2:])
+    if out is None:
+        out = torch.empty(shape, dtype=key.dtype, device=key.device)
+    elif tuple(out.shape) != shape or out.dtype != key.dtype or out.device != key.device:
+        raise ValueError(f"gather output has shape {tuple(out.shape)}, expected {shape}")
+    if tokens == 0:
+        return out
+    if not out[0, 0].is_contiguous() or not out[0, 1].is_contiguous():
+        raise ValueError("multi-layer gather output needs contiguous [tokens, *row] planes")
+    slots = _device_slots(slot_mapping, key.device, descs[0].num_blocks * block_size)
+    es = key.element_size()
+    rc = _native.load().cbk_paged_gather_layers(
+        descs,
+        len(kv_layers),
+        slots.data_ptr(),
+        tokens,
+        out.data_ptr(),
+        out.stride(0) * es,
+        out.stride(1) * es,
+        out.stride(2) * es,
+        None,
+        _native.stream_handle(key.device),
+    )
+    _native.check(rc, "gather_paged_kv_layers")
+    return out
+
+
+def scatter_paged_kv_layers(
+    contiguous: torch.Tensor,
+    kv_layers: Sequence[KVLayer],
+    slot_mapping: torch.Tensor,
+    block_size: int,
+) -> None:
+    """Inverse of :func:`gather_paged_kv_layers` (cbk_paged_scatter_layers)."""
+    descs, key = _layer_descs(kv_layers, block_size)
+    tokens = int(slot_mapping.numel())
+    shape = (len(kv_layers), 2, tokens, *key.shape[2:])
+    if tuple(contiguous.shape) != shape:
+        raise ValueError(f"contiguous KV has shape {tuple(contiguous.shape)}, expected {shape}")
+    if contiguous.dtype != key.dtype:
+        raise RuntimeError("source and destination dtypes must match")
+    if tokens == 0:
+        return
+    src = contiguous.to(device=key.device)
+    if not src[0, 0].is_contiguous() or not src[0, 1].is_contiguous():
+        src = src.contiguous()
+    slots = _device_slots(slot_mapping, key.device, descs[0].num_blocks * block_size)
+    es = key.element_size()
+    rc = _native.load().cbk_paged_scatter_layers(
+        src.data_ptr(),
+        src.stride(0) * es,
+        src.stride(1) * es,
+        src.stride(2) * es,
+        descs,
+        len(kv_layers),
+        slots.data_ptr(),
+        tokens,
+        None,
+        _native.stream_handle(key.device),
+    )
+    _native.check(rc, "scatter_paged_kv_layers")
+
+
+class PagedKVCache:
+    """A model's registered paged KV layers (one descriptor per layer, built
+    once, as the connector's ``register_kv_caches`` receives them, reference
+    connector.py:168-175), with batched gather/scatter over any subset.
+
+    Calls cost one C-ABI launch per 64 layers and no per-layer Python work.
+    """
+
+    def __init__(self, kv_layers: Sequence[KVLayer], block_size: int):
+        self.kv_layers = list(kv_layers)
+        self.block_size = int(block_size)
+        self._descs, self._key = _layer_descs(self.kv_layers, self.block_size)
+        self.num_layers = len(self.kv_layers)
+        self.row_shape = tuple(self._key.shape[2:])
+        self.dtype = self._key.dtype
+        self.device = self._key.device
+        self.num_slots = self._descs[0].num_blocks * self.block_size
+        self._es = self._key.element_size()
+
+    def _slots(self, slot_mapping: torch.Tensor) -> torch.Tensor:
+        if slot_mapping.device == self.device and slot_mapping.dtype == torch.long:
+            return slot_mapping if slot_mapping.is_contiguous() else slot_mapping.contiguous()
+        return _device_slots(slot_mapping, self.device, self.num_slots)
+
+    def layer_desc(self, layer: int) -> _native.KVDesc:
+        return self._descs[layer]
+
+    def gather(self, slot_mapping: torch.Tensor, out: torch.Tensor | None = None,
+               layers: tuple[int, int] | None = None) -> torch.Tensor:
+        """``out[l, c, t] = layer l plane c at slot t`` for layers ``[l0, l1)``."""
+        l0, l1 = layers or (0, self.num_layers)
+        tokens = int(slot_mapping.numel())
+        shape = (l1 - l0, 2, tokens, *self.row_shape)
+        if out is None:
+            out = torch.empty(shape, dtype=self.dtype, device=self.device)
+        elif tuple(out.shape) != shape or out.dtype != self.dtype:
+            raise ValueError(f"gather output has shape {tuple(out.shape)}, expected {shape}")
+        if tokens == 0:
+            return out
+        slots = self._slots(slot_mapping)
+        es = self._es
+        rc = _native.load().cbk_paged_gather_layers(
+            ctypes_addressof(self._descs, l0), l1 - l0, slots.data_ptr(), tokens, out.data_ptr(),
+            out.stride(0) * es, out.stride(1) * es, out.stride(2) * es, None,
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "PagedKVCache.gather")
+        return out
+
+    def scatter(self, contiguous: torch.Tensor, slot_mapping: torch.Tensor,
+                layers: tuple[int, int] | None = None) -> None:
+        """Inverse of :meth:`gather`."""
+        l0, l1 = layers or (0, self.num_layers)
+        tokens = int(slot_mapping.numel())
+        shape = (l1 - l0, 2, tokens, *self.row_shape)
+        if tuple(contiguous.shape) != shape or contiguous.dtype != self.dtype:
+            raise ValueError(f"contiguous KV has shape {tuple(contiguous.shape)}, expected {shape}")
+        if tokens == 0:
+            return
+        if not contiguous[0, 0].is_contiguous() or not contiguous[0, 1].is_contiguous():
+            contiguous = contiguous.contiguous()
+        slots = self._slots(slot_mapping)
+        es = self._es
+        rc = _native.load().cbk_paged_scatter_layers(
+            contiguous.data_ptr(), contiguous.stride(0) * es, contiguous.stride(1) * es,
+            contiguous.stride(2) * es, ctypes_addressof(self._descs, l0), l1 - l0,
+            slots.data_ptr(), tokens, None, _native.stream_handle(self.device),
+        )
+        _native.check(rc, "PagedKVCache.scatter")
+
+
+def ctypes_addressof(descs, index: int):
+    """Pointer to ``descs[index]`` inside a ctypes array of KVDesc."""
+    import ctypes
+
+    return ctypes.cast(
+        ctypes.byref(descs, index * ctypes.sizeof(_native.KVDesc)), ctypes.POINTER(_native.KVDesc)
+    )

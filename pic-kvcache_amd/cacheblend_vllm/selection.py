@@ -1,0 +1,245 @@
+"""Recompute-token selection on MI355X: K-deviation, budgeted top-k, Sparse-Q.
+
+Mirrors the selection half of the reference ``Qwen3BlendExecutor``
+(cacheblend_vllm/ascend.py:534-566, 638-711, 757-796): the K-deviation score,
+``_select`` and ``_sparse_q_scores`` keep their names, arguments and
+results. The work runs in libcacheblend_hip.so:
+
+* ``cbk_kdev_scores``  per-token sum of squared K differences (HBM-bound)
+* ``cbk_select``       gap/forced/dilation masks + radix top-k + ordered
+                       compaction, entirely on the GPU (the reference's
+                       ``torch.topk`` + ``torch.where`` + host budget syncs)
+* ``cbk_dilate``       overflow-block dilation of the gap mask
+
+Ties at the k-th score go to the lower index (deterministic on every run and
+every rank). The only host synchronisation is reading the selected count to
+size the returned tensor, as the reference's ``torch.where`` does;
+``select_async`` avoids even that.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+from .config import CacheBlendConfig
+
+
+def _mask_u8(mask: torch.Tensor, n: int, what: str) -> torch.Tensor:
+    if mask.shape != (n,):
+        raise ValueError(f"{what} must have shape ({n},), got {tuple(mask.shape)}")
+    if mask.dtype == torch.bool:
+        mask = mask.contiguous().view(torch.uint8)
+    else:
+        mask = (mask != 0).contiguous().view(torch.uint8)
+    return mask
+
+
+def _row_view(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.ndim != 2:
+        t = t.reshape(t.shape[0], -1)
+    if t.stride(1) != 1:
+        t = t.contiguous()
+    if t.dtype not in _native.DTYPE_CODES:
+        raise ValueError(f"{what} dtype {t.dtype} is not supported")
+    return t
+
+
+def kdev_scores(
+    fresh: torch.Tensor,
+    cached: torch.Tensor,
+    absolute_indices: torch.Tensor | None = None,
+    row0: int = 0,
+) -> torch.Tensor:
+    """``sum((fresh.float() - cached[idx].float())**2, dim=-1)`` as float32.
+
+    Reference ascend.py:534-538 (``cached`` is ``flat_old_k``, ``idx`` is
+    ``absolute_indices``, or ``row0 + arange(N)`` when it is None).
+    """
+    fresh = _row_view(fresh, "fresh K")
+    cached = _row_view(cached, "cached K")
+    _native.require_device(fresh, "fresh K")
+    if fresh.dtype != cached.dtype or fresh.device != cached.device:
+        raise ValueError("fresh and cached K must share dtype and device")
+    if fresh.shape[1] != cached.shape[1]:
+        raise ValueError(f"row widths differ: {fresh.shape[1]} vs {cached.shape[1]}")
+    n = fresh.shape[0]
+    scores = torch.empty(n, dtype=torch.float32, device=fresh.device)
+    idx = None
+    if absolute_indices is not None:
+        idx = absolute_indices.to(device=fresh.device, dtype=torch.long).contiguous()
+        if idx.shape != (n,):
+            raise ValueError("absolute_indices must have one entry per fresh row")
+    rc = _native.load().cbk_kdev_scores(
+        fresh.data_ptr(), fresh.stride(0), cached.data_ptr(), cached.stride(0), cached.shape[0],
+        _native.ptr(idx), row0, n, fresh.shape[1], _native.DTYPE_CODES[fresh.dtype],
+        scores.data_ptr(), _native.stream_handle(fresh.device),
+    )
+    _native.check(rc, "kdev_scores")
+    return scores
+
+
+def select_async(
+    scores: torch.Tensor,
+    gap_mask: torch.Tensor,
+    ratio: float,
+    forced_mask: torch.Tensor | None = None,
+    radius: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Selection without a host sync: ``(indices[N] int64, count[1] int64)``;
+    the first ``count`` entries of ``indices`` are the sorted selection."""
+    n = int(scores.shape[0])
+    _native.require_device(scores, "scores")
+    if scores.ndim != 1:
+        raise ValueError("scores must be one-dimensional")
+    if forced_mask is not None and forced_mask.shape != gap_mask.shape:
+        raise ValueError("forced selection mask must match the active token shape")
+    if scores.dtype != torch.float32:
+        scores = scores.float()
+    scores = scores.contiguous()
+    gap = _mask_u8(gap_mask.to(scores.device), n, "gap_mask")
+    forced = None if forced_mask is None else _mask_u8(forced_mask.to(scores.device), n, "forced_mask")
+    out = torch.empty(max(n, 1), dtype=torch.long, device=scores.device)
+    count = torch.empty(1, dtype=torch.long, device=scores.device)
+    lib = _native.load()
+    nbytes = lib.cbk_select_workspace_bytes(n)
+    ws = _native.workspace(scores.device, nbytes)
+    rc = lib.cbk_select(
+        scores.data_ptr(), gap.data_ptr(), _native.ptr(forced), n, int(radius), float(ratio),
+        out.data_ptr(), count.data_ptr(), ws.data_ptr(), ws.numel(),
+        _native.stream_handle(scores.device),
+    )
+    _native.check(rc, "select")
+    return out, count
+
+
+def select(
+    scores: torch.Tensor,
+    gap_mask: torch.Tensor,
+    ratio: float,
+    forced_mask: torch.Tensor | None = None,
+    radius: int = 0,
+) -> torch.Tensor:
+    """Sorted int64 indices of ``gap | forced | dilate(gap, radius) | top-k``.
+
+    Reference ``_select`` (ascend.py:757-796) at TP1, with the budget
+    ``int((N - #gap) * ratio)`` clamped to ``[1, available]``.
+    """
+    out, count = select_async(scores, gap_mask, ratio, forced_mask, radius)
+    return out[: int(count.item())]
+
+
+def kdev_select(
+    fresh: torch.Tensor,
+    cached: torch.Tensor,
+    absolute_indices: torch.Tensor | None,
+    gap_mask: torch.Tensor,
+    ratio: float,
+    radius: int = 0,
+    row0: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """K-deviation scores and their selection in one call (``cbk_kdev_select``).
+
+    Returns ``(selected, scores)``; ``radius`` > 0 also forces every token
+    within ``radius`` of a gap (overflow blocks).
+    """
+    fresh = _row_view(fresh, "fresh K")
+    cached = _row_view(cached, "cached K")
+    _native.require_device(fresh, "fresh K")
+    if fresh.dtype != cached.dtype or fresh.device != cached.device:
+        raise ValueError("fresh and cached K must share dtype and device")
+    n = fresh.shape[0]
+    idx = None
+    if absolute_indices is not None:
+        idx = absolute_indices.to(device=fresh.device, dtype=torch.long).contiguous()
+        if idx.shape != (n,):
+            raise ValueError("absolute_indices must have one entry per fresh row")
+    gap = _mask_u8(gap_mask.to(fresh.device), n, "gap_mask")
+    scores = torch.empty(n, dtype=torch.float32, device=fresh.device)
+    out = torch.empty(max(n, 1), dtype=torch.long, device=fresh.device)
+    count = torch.empty(1, dtype=torch.long, device=fresh.device)
+    lib = _native.load()
+    nbytes = lib.cbk_select_workspace_bytes(n)
+    ws = _native.workspace(fresh.device, nbytes)
+    rc = lib.cbk_kdev_select(
+        fresh.data_ptr(), fresh.stride(0), cached.data_ptr(), cached.stride(0), cached.shape[0],
+        _native.ptr(idx), row0, n, fresh.shape[1], _native.DTYPE_CODES[fresh.dtype],
+        gap.data_ptr(), None, int(radius), float(ratio), scores.data_ptr(), out.data_ptr(),
+        count.data_ptr(), ws.data_ptr(), ws.numel(), _native.stream_handle(fresh.device),
+    )
+    _native.check(rc, "kdev_select")
+    return out[: int(count.item())], scores
+
+
+def dilate(gap_mask: torch.Tensor, radius: int) -> torch.Tensor:
+    """``forced[i] = any(gap[i - radius : i + radius + 1])`` (ascend.py:662-671)."""
+    n = int(gap_mask.shape[0])
+    _native.require_device(gap_mask, "gap_mask")
+    gap = _mask_u8(gap_mask, n, "gap_mask")
+    out = torch.empty(n, dtype=torch.bool, device=gap_mask.device)
+    rc = _native.load().cbk_dilate(
+        gap.data_ptr(), n, int(radius), out.view(torch.uint8).data_ptr(),
+        _native.stream_handle(gap_mask.device),
+    )
+    _native.check(rc, "dilate")
+    return out
+
+
+class BlendSelector:
+    """The selection methods of the reference ``Qwen3BlendExecutor``.
+
+    ``_select`` and the K-deviation block keep the reference's signatures so
+    an executor can delegate to them unchanged. With a TP group of more than
+    one rank the scores are all-reduced first (reference ascend.py:768-769);
+    every rank then runs the same deterministic selection, which replaces the
+    reference's rank-0 top-k plus broadcast (ascend.py:787-796).
+    """
+
+    def __init__(self, config: CacheBlendConfig, block_size: int, tp_group=None):
+        if block_size <= 0:
+            raise ValueError("vLLM KV cache block_size must be positive")
+        self.config = config
+        self.block_size = block_size
+        self.tp_group = tp_group
+
+    def _reduce(self, scores: torch.Tensor) -> torch.Tensor:
+        tp = self.tp_group
+        if self.config.tp_global_selection and tp is not None and tp.world_size > 1:
+            return tp.all_reduce(scores)
+        return scores
+
+    def _select(
+        self,
+        scores: torch.Tensor,
+        gap_mask: torch.Tensor,
+        layer_id: int | None = None,
+        forced_mask: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Reference ascend.py:757-796."""
+        if forced_mask is not None and forced_mask.shape != gap_mask.shape:
+            raise ValueError("forced selection mask must match the active token shape")
+        scores = self._reduce(scores)
+        return select(scores, gap_mask, self.config.ratio_for(layer_id), forced_mask)
+
+    def kv_deviation_select(
+        self,
+        k: torch.Tensor,
+        flat_old_k: torch.Tensor,
+        absolute_indices: torch.Tensor,
+        gap_mask: torch.Tensor,
+        layer_id: int | None = None,
+        overflow_blocks: int = 0,
+    ) -> torch.Tensor:
+        """The check-layer K-deviation block (ascend.py:534-543).
+
+        ``overflow_blocks`` > 0 additionally forces tokens within that many
+        vLLM blocks of a gap (the dilation the reference applies to Sparse-Q
+        only); 0 is the reference's K-deviation path exactly.
+        """
+        radius = overflow_blocks * self.block_size
+        ratio = self.config.ratio_for(layer_id)
+        if self.tp_group is not None and self.tp_group.world_size > 1:
+            scores = self._reduce(kdev_scores(k, flat_old_k, absolute_indices))
+            return select(scores, gap_mask, ratio, None, radius)
+        selected, _ = kdev_select(k, flat_old_k, absolute_indices, gap_mask, ratio, radius)
+        return selected

@@ -1,0 +1,238 @@
+// Paged KV gather/scatter for gfx950: the bandwidth kernels behind
+// gather_paged_kv / scatter_paged_kv (reference cacheblend_vllm/kv_layout.py).
+//
+// Work decomposition. A "row" is one token's [H, D] slice of one plane (K or
+// V): row_bytes contiguous bytes on both the page side and the contiguous
+// side. Rows are split into VEC-byte vectors (16 B when every pointer and
+// stride allows it), and vector f of a launch is
+//     row = f / row_vecs, j = f % row_vecs, token = row >> 1, plane = row & 1
+// so consecutive lanes walk consecutive 16 B of one row (fully coalesced
+// 64-lane x 16 B = 1 KiB wavefront accesses) and a wavefront covers whole
+// (token, head) rows. Each thread issues kUnroll independent loads before
+// its stores to keep enough bytes in flight per CU to cover HBM latency.
+// blockIdx.y selects the layer, so one launch moves up to kMaxLayers layers.
+#include "cbk_common.hpp"
+
+namespace cbk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+constexpr int kMaxLayers = 64;
+
+struct PagedArgs {
+  const char* k_base[kMaxLayers];
+  const char* v_base[kMaxLayers];
+  char* c_base;             // contiguous side: layer 0, plane K, token 0
+  int64_t c_layer_stride;   // bytes
+  int64_t c_plane_stride;   // bytes (V minus K, may be negative)
+  int64_t c_token_stride;   // bytes
+  const int64_t* slots;
+  int64_t block_stride;     // page side, bytes
+  int64_t token_stride;     // page side, bytes
+  int32_t* bad;             // optional out-of-range slot counter
+  uint32_t num_tokens;
+  uint32_t row_vecs;
+  uint32_t num_slots;
+  FastDiv row_div;          // by row_vecs
+  FastDiv bs_div;           // by block_size
+};
+
+template <int VEC, bool GATHER>
+__global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a) {
+  using V = typename Vec<VEC>::T;
+  const uint32_t layer = blockIdx.y;
+  const char* kb = a.k_base[layer];
+  const char* vb = a.v_base[layer];
+  char* cb = a.c_base + int64_t(layer) * a.c_layer_stride;
+  const uint32_t total = a.num_tokens * 2u * a.row_vecs;
+  const uint32_t f0 = blockIdx.x * uint32_t(kThreads * kUnroll) + threadIdx.x;
+
+  const char* page[kUnroll];
+  char* cont[kUnroll];
+  bool valid[kUnroll];
+  bool live[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t f = f0 + uint32_t(u * kThreads);
+    live[u] = f < total;
+    valid[u] = false;
+    page[u] = nullptr;
+    cont[u] = nullptr;
+    if (live[u]) {
+      const uint32_t row = a.row_div.div(f);
+      const uint32_t j = f - row * a.row_vecs;
+      const uint32_t t = row >> 1;
+      const uint32_t c = row & 1u;
+      const int64_t slot = a.slots[t];
+      valid[u] = slot >= 0 && slot < int64_t(a.num_slots);
+      if (valid[u]) {
+        const uint32_t s32 = uint32_t(slot);
+        const uint32_t blk = a.bs_div.div(s32);
+        const uint32_t off = s32 - blk * a.bs_div.d;
+        page[u] = (c ? vb : kb) + int64_t(blk) * a.block_stride + int64_t(off) * a.token_stride +
+                  int64_t(j) * VEC;
+      } else if (a.bad != nullptr && c == 0 && j == 0) {
+        atomicAdd(a.bad, 1);
+      }
+      cont[u] = cb + int64_t(c) * a.c_plane_stride + int64_t(t) * a.c_token_stride + int64_t(j) * VEC;
+    }
+  }
+  V buf[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (GATHER) {
+      buf[u] = V(0);
+      if (valid[u]) buf[u] = *reinterpret_cast<const V*>(page[u]);
+    } else if (live[u]) {
+      buf[u] = *reinterpret_cast<const V*>(cont[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    if (GATHER) {
+      if (live[u]) *reinterpret_cast<V*>(cont[u]) = buf[u];
+    } else if (valid[u]) {
+      *reinterpret_cast<V*>(const_cast<char*>(page[u])) = buf[u];
+    }
+  }
+}
+
+int validate_desc(const cbk_kv_desc* kv) {
+  CBK_REQUIRE(kv != nullptr, "kv descriptor is NULL");
+  CBK_REQUIRE(kv->k_base != nullptr && kv->v_base != nullptr, "kv base pointer is NULL");
+  CBK_REQUIRE(kv->num_blocks > 0 && kv->block_size > 0, "num_blocks and block_size must be positive");
+  CBK_REQUIRE(kv->row_bytes > 0, "row_bytes must be positive");
+  CBK_REQUIRE(kv->num_blocks * kv->block_size < (int64_t(1) << 32),
+              "num_blocks * block_size must be below 2^32");
+  CBK_REQUIRE(kv->token_stride >= kv->row_bytes, "token_stride smaller than a row");
+  CBK_REQUIRE(kv->block_stride >= kv->token_stride * kv->block_size || kv->block_size == 1,
+              "block_stride smaller than a block");
+  return CBK_OK;
+}
+
+int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const int64_t* slots,
+                 int64_t num_tokens, char* c_base, int64_t c_layer_stride, int64_t c_plane_stride,
+                 int64_t c_token_stride, int32_t* bad, hipStream_t stream) {
+  clear_error();
+  if (int rc = validate_desc(kv)) return rc;
+  CBK_REQUIRE(num_layers >= 1, "num_layers must be >= 1");
+  CBK_REQUIRE(num_tokens >= 0, "num_tokens must be >= 0");
+  if (num_tokens == 0) return CBK_OK;
+  CBK_REQUIRE(slots != nullptr && c_base != nullptr, "slots/contiguous pointer is NULL");
+  CBK_REQUIRE(c_token_stride >= kv->row_bytes, "contiguous token stride smaller than a row");
+  for (int32_t l = 1; l < num_layers; ++l) {
+    CBK_REQUIRE(kv[l].num_blocks == kv[0].num_blocks && kv[l].block_size == kv[0].block_size &&
+                    kv[l].block_stride == kv[0].block_stride &&
+                    kv[l].token_stride == kv[0].token_stride && kv[l].row_bytes == kv[0].row_bytes,
+                "layer %d geometry differs from layer 0", int(l));
+    CBK_REQUIRE(kv[l].k_base != nullptr && kv[l].v_base != nullptr, "layer %d base is NULL", int(l));
+  }
+
+  // widest access that every address and stride allows
+  int64_t align_vals[8] = {kv->row_bytes, kv->block_stride, kv->token_stride, c_token_stride,
+                           c_plane_stride, c_layer_stride, int64_t(reinterpret_cast<uintptr_t>(c_base)),
+                           0};
+  int vec = common_vec_bytes(align_vals, 7);
+  for (int32_t l = 0; l < num_layers; ++l) {
+    int64_t p[2] = {int64_t(reinterpret_cast<uintptr_t>(kv[l].k_base)),
+                    int64_t(reinterpret_cast<uintptr_t>(kv[l].v_base))};
+    vec = std::min(vec, common_vec_bytes(p, 2));
+  }
+  const int64_t row_vecs = kv->row_bytes / vec;
+  CBK_REQUIRE(num_tokens * 2 * row_vecs < (int64_t(1) << 32),
+              "too many vectors in one launch (%lld tokens)", (long long)num_tokens);
+
+  PagedArgs a;
+  a.c_base = c_base;
+  a.c_layer_stride = c_layer_stride;
+  a.c_plane_stride = c_plane_stride;
+  a.c_token_stride = c_token_stride;
+  a.slots = slots;
+  a.block_stride = kv->block_stride;
+  a.token_stride = kv->token_stride;
+  a.bad = bad;
+  a.num_tokens = uint32_t(num_tokens);
+  a.row_vecs = uint32_t(row_vecs);
+  a.num_slots = uint32_t(kv->num_blocks * kv->block_size);
+  a.row_div = FastDiv::make(uint32_t(row_vecs));
+  a.bs_div = FastDiv::make(uint32_t(kv->block_size));
+
+  const uint64_t total = uint64_t(num_tokens) * 2 * uint64_t(row_vecs);
+  const uint32_t grid_x = uint32_t((total + kThreads * kUnroll - 1) / (kThreads * kUnroll));
+
+  for (int32_t l0 = 0; l0 < num_layers; l0 += kMaxLayers) {
+    const int32_t nl = std::min(kMaxLayers, num_layers - l0);
+    for (int32_t i = 0; i < kMaxLayers; ++i) {
+      const cbk_kv_desc& d = kv[l0 + (i < nl ? i : 0)];
+      a.k_base[i] = static_cast<const char*>(d.k_base);
+      a.v_base[i] = static_cast<const char*>(d.v_base);
+    }
+    PagedArgs al = a;
+    al.c_base = c_base + int64_t(l0) * c_layer_stride;
+    dim3 grid(grid_x, uint32_t(nl));
+#define CBK_LAUNCH_PAGED(V)                                                                   \
+  if (gather)                                                                                 \
+    hipLaunchKernelGGL((paged_copy_kernel<V, true>), grid, dim3(kThreads), 0, stream, al);    \
+  else                                                                                        \
+    hipLaunchKernelGGL((paged_copy_kernel<V, false>), grid, dim3(kThreads), 0, stream, al);
+    switch (vec) {
+      case 16: CBK_LAUNCH_PAGED(16); break;
+      case 8: CBK_LAUNCH_PAGED(8); break;
+      case 4: CBK_LAUNCH_PAGED(4); break;
+      case 2: CBK_LAUNCH_PAGED(2); break;
+      default: CBK_LAUNCH_PAGED(1); break;
+    }
+#undef CBK_LAUNCH_PAGED
+    if (int rc = launch_status(gather ? "paged gather" : "paged scatter")) return rc;
+  }
+  return CBK_OK;
+}
+
+}  // namespace
+}  // namespace cbk
+
+extern "C" {
+
+int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                     void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
+                     int32_t* bad_slots_dev, cbk_stream_t stream) {
+  if (num_tokens > 0 && (out_k_dev == nullptr || out_v_dev == nullptr))
+    return cbk::set_error(CBK_ERR_INVALID, "output pointer is NULL");
+  char* k = static_cast<char*>(out_k_dev);
+  const int64_t plane = static_cast<char*>(out_v_dev) - k;
+  return cbk::launch_paged(true, kv, 1, slots_dev, num_tokens, k, 0, plane, out_token_stride,
+                           bad_slots_dev, static_cast<hipStream_t>(stream));
+}
+
+int cbk_paged_scatter(const void* in_k_dev, const void* in_v_dev, int64_t in_token_stride,
+                      const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                      int32_t* bad_slots_dev, cbk_stream_t stream) {
+  if (num_tokens > 0 && (in_k_dev == nullptr || in_v_dev == nullptr))
+    return cbk::set_error(CBK_ERR_INVALID, "input pointer is NULL");
+  char* k = const_cast<char*>(static_cast<const char*>(in_k_dev));
+  const int64_t plane = static_cast<const char*>(in_v_dev) - k;
+  return cbk::launch_paged(false, kv, 1, slots_dev, num_tokens, k, 0, plane, in_token_stride,
+                           bad_slots_dev, static_cast<hipStream_t>(stream));
+}
+
+int cbk_paged_gather_layers(const cbk_kv_desc* kv, int32_t num_layers, const int64_t* slots_dev,
+                            int64_t num_tokens, void* out_dev, int64_t out_layer_stride,
+                            int64_t out_plane_stride, int64_t out_token_stride,
+                            int32_t* bad_slots_dev, cbk_stream_t stream) {
+  return cbk::launch_paged(true, kv, num_layers, slots_dev, num_tokens, static_cast<char*>(out_dev),
+                           out_layer_stride, out_plane_stride, out_token_stride, bad_slots_dev,
+                           static_cast<hipStream_t>(stream));
+}
+
+int cbk_paged_scatter_layers(const void* in_dev, int64_t in_layer_stride, int64_t in_plane_stride,
+                             int64_t in_token_stride, const cbk_kv_desc* kv, int32_t num_layers,
+                             const int64_t* slots_dev, int64_t num_tokens, int32_t* bad_slots_dev,
+                             cbk_stream_t stream) {
+  return cbk::launch_paged(false, kv, num_layers, slots_dev, num_tokens,
+                           const_cast<char*>(static_cast<const char*>(in_dev)), in_layer_stride,
+                           in_plane_stride, in_token_stride, bad_slots_dev,
+                           static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

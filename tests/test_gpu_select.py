@@ -1,0 +1,165 @@
+"""GPU parity: K-deviation scores and budgeted selection against the oracle.
+
+Index sets are bit-exact for identical scores (the selection is integer work
+on float keys). K-deviation scores match within 1e-5 relative (the float32
+summation order differs); the index set computed from GPU scores must equal
+the oracle's whenever the k-th-score boundary margin exceeds that noise.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from cacheblend_vllm import selection as S
+from cacheblend_vllm import synthetic
+from cacheblend_vllm.config import CacheBlendConfig
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+SCORE_RTOL = 1e-5
+
+
+def test_reference_known_answers(golden):
+    case = golden["select_keeps_gaps"]
+    got = S.select(torch.tensor(case["scores"], device=DEV), torch.tensor(case["gap"], device=DEV), case["ratio"])
+    assert got.tolist() == case["expected"]
+    case = golden["select_forced_not_budgeted"]
+    got = S.select(
+        torch.tensor(case["scores"], device=DEV),
+        torch.tensor(case["gap"], device=DEV),
+        case["ratio"],
+        torch.tensor(case["forced"], device=DEV),
+    )
+    assert got.tolist() == case["expected"]
+    sel = S.BlendSelector(CacheBlendConfig.from_extra_config({"recompute_ratios": [0.5]}), 16)
+    got = sel._select(torch.tensor(case["scores"], device=DEV), torch.tensor(case["gap"], device=DEV),
+                      forced_mask=torch.tensor(case["forced"], device=DEV))
+    assert got.tolist() == case["expected"]
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 1023, 1024, 1025, 4097, 65536, 200000])
+def test_select_bit_exact_vs_oracle_random(n):
+    rng = np.random.default_rng(n)
+    for trial in range(3):
+        print(f"n={n} trial={trial}", flush=True)
+        if trial == 0:
+            scores = rng.standard_normal(n).astype(np.float32) ** 2
+        elif trial == 1:
+            scores = rng.integers(0, 5, n).astype(np.float32)  # heavy ties
+        else:
+            scores = rng.standard_normal(n).astype(np.float32)
+            scores[rng.random(n) < 0.05] = 0.0
+            scores[rng.random(n) < 0.01] = -0.0
+        gap = rng.random(n) < 0.2
+        forced = (rng.random(n) < 0.05) if trial != 1 else None
+        ratio = [0.15, 0.5, 0.01][trial]
+        radius = [0, 16, 3][trial]
+        fc = forced
+        if radius:
+            fc = O.dilate(gap, radius) | (forced if forced is not None else False)
+        want = O.select(scores, gap, ratio, fc)
+        got = S.select(
+            torch.from_numpy(scores).to(DEV),
+            torch.from_numpy(gap).to(DEV),
+            ratio,
+            None if forced is None else torch.from_numpy(forced).to(DEV),
+            radius=radius,
+        )
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def test_select_dilation_equals_forced_mask_composition():
+    # cbk_select(radius=r) == _select(gap, forced=dilate(gap, r))
+    rng = np.random.default_rng(9)
+    n = 5000
+    scores = rng.random(n).astype(np.float32)
+    gap = synthetic.gap_layout(n, seed=4)
+    for r in (1, 16, 64, 4096):
+        forced = O.dilate(gap, r)
+        want = O.select(scores, gap, 0.15, forced)
+        got = S.select(torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV), 0.15, radius=r)
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+        dil = S.dilate(torch.from_numpy(gap).to(DEV), r)
+        np.testing.assert_array_equal(dil.cpu().numpy(), forced)
+
+
+def test_select_edge_cases():
+    # no cached tokens -> only gaps; nothing available -> only base; empty
+    all_gap = torch.ones(10, dtype=torch.bool, device=DEV)
+    assert S.select(torch.rand(10, device=DEV), all_gap, 0.5).tolist() == list(range(10))
+    gap = torch.zeros(10, dtype=torch.bool, device=DEV)
+    forced = torch.ones(10, dtype=torch.bool, device=DEV)
+    assert S.select(torch.rand(10, device=DEV), gap, 0.5, forced).tolist() == list(range(10))
+    empty = S.select(torch.empty(0, device=DEV), torch.empty(0, dtype=torch.bool, device=DEV), 0.5)
+    assert empty.numel() == 0
+    # NaN ranks highest, -inf never beats a finite score
+    s = torch.tensor([1.0, float("nan"), 3.0, float("-inf"), 2.0], device=DEV)
+    assert S.select(s, torch.zeros(5, dtype=torch.bool, device=DEV), 0.4).tolist() == [1, 2]
+    with pytest.raises(ValueError, match="forced selection mask"):
+        S.select(s, torch.zeros(5, dtype=torch.bool, device=DEV), 0.4, torch.zeros(4, dtype=torch.bool, device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_kdev_scores_vs_oracle(dtype):
+    fresh, cached, gap = synthetic.kdev_inputs(3000, 4, 128, dtype, DEV, seed=1)
+    got = S.kdev_scores(fresh, cached)
+    f = fresh.float().cpu().numpy()
+    c = cached.float().cpu().numpy()
+    want = O.kdev_scores(f, c)
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=SCORE_RTOL, atol=0)
+    # gathered cached rows through absolute indices (ascend.py:536)
+    idx = torch.randperm(3000)[:1000]
+    got = S.kdev_scores(fresh[:1000], cached, idx.to(DEV))
+    np.testing.assert_allclose(got.cpu().numpy(), O.kdev_scores(f[:1000], c[idx.numpy()]), rtol=SCORE_RTOL)
+
+
+def test_kdev_odd_width_and_strided_rows():
+    torch.manual_seed(5)
+    fresh = torch.randn(100, 77, device=DEV).to(torch.bfloat16)
+    cached = torch.randn(120, 80, device=DEV).to(torch.bfloat16)[:, :77]
+    got = S.kdev_scores(fresh, cached, None, row0=20)
+    want = O.kdev_scores(fresh.float().cpu().numpy(), cached[20:120].float().cpu().numpy())
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=SCORE_RTOL)
+
+
+@pytest.mark.parametrize("overflow_blocks", [0, 1])
+def test_kdev_select_full_size_index_set(overflow_blocks):
+    """K-deviation selection at its headline size: 65,536 tokens, 4 KV heads x
+    128 bf16, 20% gaps, ratio 0.15, 16-token blocks."""
+    n, bs = 65536, 16
+    fresh, cached, gap = synthetic.kdev_inputs(n, 4, 128, torch.bfloat16, DEV, seed=0)
+    radius = overflow_blocks * bs
+    selected, scores = S.kdev_select(fresh, cached, None, gap, 0.15, radius=radius)
+    gap_np = gap.cpu().numpy()
+    # selection is bit-exact on the GPU's own scores
+    forced = O.dilate(gap_np, radius) if radius else None
+    want_same = O.select(scores.cpu().numpy(), gap_np, 0.15, forced)
+    np.testing.assert_array_equal(selected.cpu().numpy(), want_same)
+    # oracle scores agree within tolerance ...
+    want_scores = O.kdev_scores(fresh.float().cpu().numpy(), cached.float().cpu().numpy())
+    np.testing.assert_allclose(scores.cpu().numpy(), want_scores, rtol=SCORE_RTOL)
+    # ... and, where the k-th boundary margin exceeds that noise, so do index sets
+    want = O.select(want_scores, gap_np, 0.15, forced)
+    base = gap_np | (forced if forced is not None else False)
+    cand = np.sort(want_scores[~base])[::-1]
+    k = O.select_budget(n, int(gap_np.sum()), int(base.sum()), 0.15)
+    margin = (cand[k - 1] - cand[k]) / cand[k - 1]
+    print(f"k={k} boundary margin={margin:.3e} selected={selected.numel()}", flush=True)
+    if margin > 4 * SCORE_RTOL:
+        np.testing.assert_array_equal(selected.cpu().numpy(), want)
+    # determinism run to run
+    again, _ = S.kdev_select(fresh, cached, None, gap, 0.15, radius=radius)
+    assert torch.equal(again, selected)
+
+
+def test_selector_kv_deviation_block_matches_reference_composition():
+    cfg = CacheBlendConfig.from_extra_config({"check_layers": [1], "recompute_ratios": [0.15]})
+    sel = S.BlendSelector(cfg, 16)
+    fresh, cached, gap = synthetic.kdev_inputs(5000, 4, 128, torch.bfloat16, DEV, seed=2)
+    absolute = torch.arange(100, 5100, device=DEV)
+    pool = torch.cat([torch.zeros(100, 512, dtype=torch.bfloat16, device=DEV), cached])
+    got = sel.kv_deviation_select(fresh, pool, absolute, gap, layer_id=1)
+    scores = S.kdev_scores(fresh, pool, absolute)
+    want = O.select(scores.cpu().numpy(), gap.cpu().numpy(), 0.15)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
