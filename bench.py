@@ -50,6 +50,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--skip-cpu-baseline", action="store_true")
     p.add_argument("--skip-extras", action="store_true", help="only the headline copy step")
+    p.add_argument("--profile", action="store_true",
+                   help="run each kernel --steps times and exit (for rocprofv3 runs)")
     return p.parse_args()
 
 
@@ -100,6 +102,9 @@ def main() -> int:
     def step():
         cache.gather(src_slots, out=staging)
         cache.scatter(staging, dst_slots)
+
+    if args.profile:
+        return profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev)
 
     # correctness guard on the real workload before timing: round trip
     step()
@@ -227,6 +232,25 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     return out
 
 
+def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev):
+    """Each kernel --steps times, nothing timed here: rocprofv3 measures.
+    The plain device copy of the staging (torch's copy kernel, 1,207,959,552 B
+    read + written) calibrates the HBM counters."""
+    copy_dst = torch.empty_like(staging)
+    fresh, cached, gap = synthetic.kdev_inputs(65536, 4, 128, torch.bfloat16, dev, seed=0)
+    for _ in range(args.steps):
+        cache.gather(src_slots, out=staging)
+    for _ in range(args.steps):
+        cache.scatter(staging, dst_slots)
+    for _ in range(args.steps):
+        copy_dst.copy_(staging)
+    for _ in range(args.steps):
+        _kdev_async(torch, S, fresh, cached, gap)
+    torch.cuda.synchronize()
+    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select)")
+    return 0
+
+
 def _kdev_async(torch, S, fresh, cached, gap):
     """cbk_kdev_select without the count readback (device time only)."""
     from cacheblend_vllm import _native
@@ -262,7 +286,9 @@ def cpu_baseline(torch, synthetic):
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
     NB, BS, H, D, T, LS = 4096, 16, 8, 128, 8192, 4
-    layers = [torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16) for _ in range(LS)]
+    # filled (not torch.zeros, whose untouched pages all map the shared zero
+    # page and would make gathers read from cache)
+    layers = [torch.full((2, NB, BS, H, D), float(i + 1), dtype=torch.bfloat16) for i in range(LS)]
     g = torch.Generator().manual_seed(0)
     perm = torch.randperm(NB, generator=g)
     src = synthetic.block_slots(perm[:512], BS, T)

@@ -146,6 +146,31 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                     int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                     cbk_stream_t stream);
 
+/*
+ * Blend-buffer assembly for one layer: out_{k,v}[p] for p in [0, num_tokens)
+ * from src_map_dev[p] (int32):
+ *   >= 0  hit staging row r = src_map[p]: hit_{k,v} + r * hit_token_stride;
+ *         with `relocate`, the K row is RoPE-relocated from position
+ *         old_pos_dev[r] to new_pos_dev[p] (new_pos_dev NULL: p) with the
+ *         [rows, head_dim] cos|sin table cos_sin_dev (key dtype; neox or
+ *         interleaved pairs), each op rounded to the key dtype
+ *   -1    zero row (gap)
+ *   -2    page row at slot slots_dev[p] of `kv` (APC prefix)
+ * out_v_dev NULL processes the K plane only (standalone relocation).
+ * Replaces PagedBlendLoader.prefetch's prefix gather, _zero_gaps and
+ * _load_segments_fused placement (cacheblend_vllm/ascend.py:230-253,
+ * 280-287, 313-370) fused with relocate_key (ascend.py:52-103).
+ * Rows whose source is out of range are zeroed and counted in *bad_dev.
+ */
+int cbk_blend_assemble(const cbk_kv_desc* kv, const int64_t* slots_dev, const int32_t* src_map_dev,
+                       int64_t num_tokens, const void* hit_k_dev, const void* hit_v_dev,
+                       int64_t hit_token_stride, int64_t hit_rows, const int32_t* old_pos_dev,
+                       const int32_t* new_pos_dev, const void* cos_sin_dev,
+                       int64_t cos_sin_row_stride_elems, int64_t cos_sin_rows, int64_t heads,
+                       int64_t head_dim, int32_t relocate, int32_t neox, int32_t dtype,
+                       void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
+                       int32_t* bad_dev, cbk_stream_t stream);
+
 /* Largest dilation radius cbk_select / cbk_kdev_select accept. */
 #define CBK_MAX_DILATION_RADIUS 4096
 

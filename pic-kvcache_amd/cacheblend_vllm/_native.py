@@ -82,6 +82,13 @@ _SIGNATURES = {
         ],
     ),
     "cbk_dilate": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "cbk_blend_assemble": (
+        ctypes.c_int,
+        [
+            ctypes.POINTER(KVDesc), c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp,
+            c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp,
+        ],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

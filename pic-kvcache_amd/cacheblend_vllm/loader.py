@@ -1,0 +1,329 @@
+"""Layerwise blend loader on MI355X: H2D of cached hits + one fused kernel.
+
+``PagedBlendLoader`` keeps the reference's constructor and its
+``prefetch`` / ``get`` / ``commit`` protocol (cacheblend_vllm/ascend.py:
+170-407), so a layerwise executor drives it unchanged:
+
+    loader.prefetch(0, rope)
+    for l in layers:
+        buf = loader.get(l)            # [2, allocation_end, H, D]
+        loader.prefetch(l + 1, rope)   # overlaps with layer l's compute
+        ... compute, writing recomputed K/V into buf ...
+        loader.commit(l, buf)          # scatter [apc:] into the vLLM pages
+
+Per layer, on the Load stream (a default-priority side stream):
+  1. hipMemcpyAsync of the pinned host hit chunks into a reusable hit
+     staging ``[2, hit_tokens, H, D]``; chunks adjacent in host memory are
+     coalesced into one copy per plane;
+  2. ``cbk_blend_assemble`` writes the layer buffer in one pass: APC prefix
+     from the pages, zeros for gaps, hit rows with their K RoPE-relocated
+     from source to target positions;
+  3. an event, waited on by ``get``.
+Two buffers alternate by layer parity; ``commit`` records a reuse event so
+buffer ``l % 2`` is not overwritten before layer ``l``'s scatter has run.
+All per-request tables (source map, old positions, slots) are built on the
+host once and uploaded once.
+"""
+
+from __future__ import annotations
+
+import time
+
+import numpy as np
+import torch
+
+from . import _native
+from .config import CacheBlendConfig
+from .kv_layout import kv_desc, kv_planes
+from .rope import cos_sin_table, rope_style
+from .trace import PipelineTracer
+from .types import BlendPlan
+
+SRC_ZERO = -1
+SRC_PAGE = -2
+
+
+def build_source_map(plan: BlendPlan) -> tuple[np.ndarray, np.ndarray, bool]:
+    """(src_map[allocation_end] int32, old_pos[hit_tokens] int32, relocate).
+
+    src_map: ``-2`` APC prefix (page), ``-1`` gap (zero), ``r >= 0`` hit row r
+    of the staging (segments concatenated in plan order, as the reference's
+    fused copy stacks them, ascend.py:333-342). ``relocate`` is False exactly
+    when every hit keeps its position (reference ``torch.equal`` shortcut,
+    ascend.py:64-65).
+    """
+    src = np.full(plan.allocation_end, SRC_ZERO, dtype=np.int32)
+    src[: plan.apc_prefix_tokens] = SRC_PAGE
+    old = np.empty(plan.hit_tokens, dtype=np.int32)
+    relocate = False
+    off = 0
+    for seg in plan.segments:
+        n = seg.length
+        src[seg.target_start : seg.target_end] = np.arange(off, off + n, dtype=np.int32)
+        old[off : off + n] = np.arange(seg.source_start, seg.source_start + n, dtype=np.int32)
+        relocate |= seg.source_start != seg.target_start
+        off += n
+    return src, old, relocate
+
+
+def coalesce_host_runs(hosts: list[torch.Tensor]) -> list[tuple[int, int, torch.Tensor, torch.Tensor]]:
+    """Group consecutive host chunks whose K planes (and V planes) are adjacent
+    in one pinned allocation into ``(dst_offset, tokens, k_run, v_run)``."""
+    runs: list[list] = []
+    off = 0
+    for host in hosts:
+        k, v = host[0], host[1]
+        n = k.shape[0]
+        if not (k.is_contiguous() and v.is_contiguous()):
+            k, v = k.contiguous(), v.contiguous()
+        if runs:
+            run = runs[-1]
+            rk, rv = run[2], run[3]
+            nbytes = rk.element_size() * rk[0].numel()
+            if (
+                k.untyped_storage().data_ptr() == rk.untyped_storage().data_ptr()
+                and v.untyped_storage().data_ptr() == rv.untyped_storage().data_ptr()
+                and k.data_ptr() == rk.data_ptr() + run[1] * nbytes
+                and v.data_ptr() == rv.data_ptr() + run[1] * nbytes
+                and k.dtype == rk.dtype
+            ):
+                run[1] += n
+                off += n
+                continue
+        runs.append([off, n, k, v])
+        off += n
+    out = []
+    for start, n, k, v in runs:
+        if k.shape[0] != n:
+            k = k.as_strided((n, *k.shape[1:]), k.stride(), k.storage_offset())
+            v = v.as_strided((n, *v.shape[1:]), v.stride(), v.storage_offset())
+        out.append((start, n, k, v))
+    return out
+
+
+class PagedBlendLoader:
+    """Double-buffered layerwise H2D load, fused assembly and paged scatter."""
+
+    def __init__(
+        self,
+        kv_caches: list,
+        store,
+        request_id: str,
+        plan: BlendPlan,
+        slot_mapping: torch.Tensor,
+        block_size: int,
+        config: CacheBlendConfig,
+        tracer: PipelineTracer | None = None,
+        load_stream: torch.cuda.Stream | None = None,
+    ):
+        self.kv_caches = kv_caches
+        self.store = store
+        self.request_id = request_id
+        self.plan = plan
+        self.slot_mapping = slot_mapping[: plan.allocation_end]
+        self.block_size = block_size
+        self.config = config
+        self.tracer = tracer
+        key, _ = kv_planes(kv_caches[0])
+        _native.require_device(key, "paged KV cache")
+        self.device = key.device
+        self.dtype = key.dtype
+        self.row_shape = tuple(key.shape[2:])
+        if self.slot_mapping.numel() < plan.allocation_end:
+            raise ValueError(
+                f"slot_mapping has {self.slot_mapping.numel()} slots for an allocation of "
+                f"{plan.allocation_end} tokens"
+            )
+        src, old, relocate = build_source_map(plan)
+        self._relocate = relocate
+        self._src_map = torch.from_numpy(src).to(self.device)
+        self._old_pos = torch.from_numpy(old).to(self.device) if old.size else None
+        num_slots = key.shape[0] * block_size
+        if self.slot_mapping.device.type == "cpu" and self.slot_mapping.numel():
+            lo, hi = int(self.slot_mapping.min()), int(self.slot_mapping.max())
+            if lo < 0 or hi >= num_slots:
+                raise IndexError(f"slot_mapping holds slots in [{lo}, {hi}], outside [0, {num_slots})")
+        self._slots = self.slot_mapping.to(device=self.device, dtype=torch.long).contiguous()
+        self._buffers: dict[int, torch.Tensor] = {}
+        self._events: dict[int, torch.cuda.Event] = {}
+        self._reuse_events: dict[int, torch.cuda.Event] = {}
+        self._staging: list[torch.Tensor] = []
+        self._hit_staging: torch.Tensor | None = None
+        self._descs: dict[int, _native.KVDesc] = {}
+        self._load_stream = None
+        if config.event_pipeline:
+            self._load_stream = load_stream or torch.cuda.Stream(self.device)
+            # tables made on the current stream are read on the Load stream
+            for table in (self._src_map, self._old_pos, self._slots):
+                if table is not None:
+                    table.record_stream(self._load_stream)
+        if tracer is not None and tracer.enabled:
+            tracer.emit(
+                "loader_initialized",
+                request_id=request_id,
+                apc_prefix_tokens=plan.apc_prefix_tokens,
+                allocation_tokens=plan.allocation_tokens,
+                hit_tokens=plan.hit_tokens,
+                gap_tokens=plan.gap_tokens,
+                segments=len(plan.segments),
+            )
+
+    # ------------------------------------------------------------ helpers
+
+    def _desc(self, layer_id: int) -> _native.KVDesc:
+        desc = self._descs.get(layer_id)
+        if desc is None:
+            desc, _ = kv_desc(self.kv_caches[layer_id], self.block_size)
+            self._descs[layer_id] = desc
+        return desc
+
+    def _load_hits(self, layer_id: int) -> None:
+        hosts = [self.store.get_layer(self.request_id, seg, layer_id) for seg in self.plan.segments]
+        if self._hit_staging is None:
+            self._hit_staging = torch.empty(
+                (2, self.plan.hit_tokens, *self.row_shape), dtype=self.dtype, device=self.device
+            )
+        hit = self._hit_staging
+        for off, n, k, v in coalesce_host_runs(hosts):
+            hit[0, off : off + n].copy_(k, non_blocking=True)
+            hit[1, off : off + n].copy_(v, non_blocking=True)
+
+    def _assemble(self, layer_id: int, buffer: torch.Tensor, rotary_emb) -> None:
+        es = buffer.element_size()
+        hit = self._hit_staging
+        heads = int(np.prod(self.row_shape[:-1])) if len(self.row_shape) > 1 else 1
+        head_dim = self.row_shape[-1]
+        table = None
+        neox = 0
+        if self._relocate:
+            head_size, neox_style = rope_style(rotary_emb)
+            if head_size != head_dim or int(getattr(rotary_emb, "rotary_dim", head_size)) != head_size:
+                raise ValueError("CacheBlend relocation requires rotary_dim == head_size == head_dim")
+            table = cos_sin_table(rotary_emb, self.dtype, self.device)
+            neox = int(neox_style)
+            limit = max(self.plan.allocation_end, max(
+                (s.source_start + s.length for s in self.plan.segments), default=0))
+            if limit > table.shape[0]:
+                raise IndexError(f"positions up to {limit} exceed the RoPE cache of {table.shape[0]}")
+        apc = self.plan.apc_prefix_tokens
+        rc = _native.load().cbk_blend_assemble(
+            self._desc(layer_id) if apc else None,
+            self._slots.data_ptr() if apc else None,
+            self._src_map.data_ptr(),
+            self.plan.allocation_end,
+            hit[0].data_ptr() if hit is not None else None,
+            hit[1].data_ptr() if hit is not None else None,
+            hit.stride(1) * es if hit is not None else 0,
+            self.plan.hit_tokens,
+            _native.ptr(self._old_pos),
+            None,
+            _native.ptr(table),
+            table.stride(0) if table is not None else 0,
+            table.shape[0] if table is not None else 0,
+            heads,
+            head_dim,
+            int(self._relocate),
+            neox,
+            _native.DTYPE_CODES[self.dtype],
+            buffer[0].data_ptr(),
+            buffer[1].data_ptr(),
+            buffer.stride(1) * es,
+            None,
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "blend assemble")
+
+    # ----------------------------------------------------------- protocol
+
+    def prefetch(self, layer_id: int, rotary_emb) -> None:
+        """Enqueue layer ``layer_id``'s load (reference ascend.py:224-278)."""
+        if layer_id in self._buffers or layer_id >= len(self.kv_caches):
+            return
+        trace = self.tracer is not None and self.tracer.enabled
+        started = time.monotonic_ns() if trace else 0
+
+        def load() -> None:
+            if not self._staging:
+                shape = (2, self.plan.allocation_end, *self.row_shape)
+                self._staging = [
+                    torch.empty(shape, dtype=self.dtype, device=self.device) for _ in range(2)
+                ]
+            index = layer_id % 2
+            reuse = self._reuse_events.pop(index, None)
+            if reuse is not None:
+                torch.cuda.current_stream(self.device).wait_event(reuse)
+            buffer = self._staging[index]
+            if self.plan.segments:
+                self._load_hits(layer_id)
+            self._assemble(layer_id, buffer, rotary_emb)
+            self._buffers[layer_id] = buffer
+
+        if self._load_stream is None:
+            load()
+        else:
+            with torch.cuda.stream(self._load_stream):
+                load()
+                event = torch.cuda.Event()
+                event.record(self._load_stream)
+                self._events[layer_id] = event
+        if trace:
+            self.tracer.emit(
+                "layer_prefetch_enqueued",
+                request_id=self.request_id,
+                layer_id=layer_id,
+                duration_us=(time.monotonic_ns() - started) / 1000,
+            )
+
+    def get(self, layer_id: int) -> torch.Tensor:
+        """The layer's buffer, ordered after its load (ascend.py:372-383)."""
+        event = self._events.pop(layer_id, None)
+        current = torch.cuda.current_stream(self.device)
+        if event is not None:
+            current.wait_event(event)
+            # the buffer was allocated on the Load stream; keep its memory
+            # until the consuming stream is done with it
+            self._buffers[layer_id].record_stream(current)
+        if self.tracer is not None and self.tracer.enabled:
+            self.tracer.emit(
+                "layer_prefetch_wait_enqueued",
+                request_id=self.request_id,
+                layer_id=layer_id,
+                had_event=event is not None,
+            )
+        return self._buffers.pop(layer_id)
+
+    def commit(self, layer_id: int, contiguous: torch.Tensor) -> None:
+        """Scatter ``contiguous[:, apc:]`` into the layer's vLLM pages through
+        ``slot_mapping[apc:]`` (ascend.py:385-407); APC pages are untouched."""
+        start = self.plan.apc_prefix_tokens
+        end = self.plan.allocation_end
+        if start >= end:
+            return
+        if tuple(contiguous.shape) != (2, end, *self.row_shape) or contiguous.dtype != self.dtype:
+            raise ValueError(
+                f"commit expects [2, {end}, {', '.join(map(str, self.row_shape))}] {self.dtype}"
+            )
+        src = contiguous if contiguous[0].is_contiguous() and contiguous[1].is_contiguous() else contiguous.contiguous()
+        es = src.element_size()
+        rc = _native.load().cbk_paged_scatter(
+            src[0, start].data_ptr(),
+            src[1, start].data_ptr(),
+            src.stride(1) * es,
+            self._desc(layer_id),
+            self._slots[start:].data_ptr(),
+            end - start,
+            None,
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "blend commit")
+        if self._load_stream is not None:
+            event = torch.cuda.Event()
+            event.record(torch.cuda.current_stream(self.device))
+            self._reuse_events[layer_id % 2] = event
+        if self.tracer is not None and self.tracer.enabled:
+            self.tracer.emit(
+                "layer_committed",
+                request_id=self.request_id,
+                layer_id=layer_id,
+                suffix_tokens=end - start,
+            )

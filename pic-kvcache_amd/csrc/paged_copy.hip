@@ -5,19 +5,27 @@
 // V): row_bytes contiguous bytes on both the page side and the contiguous
 // side. Rows are split into VEC-byte vectors (16 B when every pointer and
 // stride allows it), and vector f of a launch is
-//     row = f / row_vecs, j = f % row_vecs, token = row >> 1, plane = row & 1
+//     row = f / row_vecs, j = f % row_vecs,
+//     plane = row >= T, token = row - plane * T          (plane-major)
 // so consecutive lanes walk consecutive 16 B of one row (fully coalesced
-// 64-lane x 16 B = 1 KiB wavefront accesses) and a wavefront covers whole
-// (token, head) rows. Each thread issues kUnroll independent loads before
-// its stores to keep enough bytes in flight per CU to cover HBM latency.
+// 64-lane x 16 B = 1 KiB wavefront accesses), a wavefront covers whole
+// (token, head) rows, and neighbouring workgroups touch neighbouring tokens
+// of the same plane, i.e. the same 16-token page block (DRAM page locality;
+// token-major interleaving of K and V measured ~5% slower). Each thread
+// issues all its loads before its stores to keep bytes in flight per CU.
+// Loads and stores are non-temporal: nothing is re-read, so the copy stays
+// out of L2/MALL (+10% on gfx950 against plain accesses).
 // blockIdx.y selects the layer, so one launch moves up to kMaxLayers layers.
 #include "cbk_common.hpp"
 
 namespace cbk {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+// Launch shapes from a sweep on the 36-layer, 8 KV-head store workload:
+// gather 512 x 2 vectors per thread, scatter 256 x 2.
+constexpr int kGatherThreads = 512;
+constexpr int kScatterThreads = 256;
+constexpr int kUnroll = 2;
 constexpr int kMaxLayers = 64;
 
 struct PagedArgs {
@@ -38,7 +46,7 @@ struct PagedArgs {
   FastDiv bs_div;           // by block_size
 };
 
-template <int VEC, bool GATHER>
+template <int VEC, bool GATHER, int kThreads>
 __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a) {
   using V = typename Vec<VEC>::T;
   const uint32_t layer = blockIdx.y;
@@ -62,8 +70,8 @@ __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a)
     if (live[u]) {
       const uint32_t row = a.row_div.div(f);
       const uint32_t j = f - row * a.row_vecs;
-      const uint32_t t = row >> 1;
-      const uint32_t c = row & 1u;
+      const uint32_t c = row >= a.num_tokens ? 1u : 0u;
+      const uint32_t t = row - c * a.num_tokens;
       const int64_t slot = a.slots[t];
       valid[u] = slot >= 0 && slot < int64_t(a.num_slots);
       if (valid[u]) {
@@ -83,17 +91,17 @@ __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a)
   for (int u = 0; u < kUnroll; ++u) {
     if (GATHER) {
       buf[u] = V(0);
-      if (valid[u]) buf[u] = *reinterpret_cast<const V*>(page[u]);
+      if (valid[u]) buf[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(page[u]));
     } else if (live[u]) {
-      buf[u] = *reinterpret_cast<const V*>(cont[u]);
+      buf[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(cont[u]));
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     if (GATHER) {
-      if (live[u]) *reinterpret_cast<V*>(cont[u]) = buf[u];
+      if (live[u]) __builtin_nontemporal_store(buf[u], reinterpret_cast<V*>(cont[u]));
     } else if (valid[u]) {
-      *reinterpret_cast<V*>(const_cast<char*>(page[u])) = buf[u];
+      __builtin_nontemporal_store(buf[u], reinterpret_cast<V*>(const_cast<char*>(page[u])));
     }
   }
 }
@@ -159,7 +167,8 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
   a.bs_div = FastDiv::make(uint32_t(kv->block_size));
 
   const uint64_t total = uint64_t(num_tokens) * 2 * uint64_t(row_vecs);
-  const uint32_t grid_x = uint32_t((total + kThreads * kUnroll - 1) / (kThreads * kUnroll));
+  const int threads = gather ? kGatherThreads : kScatterThreads;
+  const uint32_t grid_x = uint32_t((total + threads * kUnroll - 1) / (threads * kUnroll));
 
   for (int32_t l0 = 0; l0 < num_layers; l0 += kMaxLayers) {
     const int32_t nl = std::min(kMaxLayers, num_layers - l0);
@@ -171,11 +180,13 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
     PagedArgs al = a;
     al.c_base = c_base + int64_t(l0) * c_layer_stride;
     dim3 grid(grid_x, uint32_t(nl));
-#define CBK_LAUNCH_PAGED(V)                                                                   \
-  if (gather)                                                                                 \
-    hipLaunchKernelGGL((paged_copy_kernel<V, true>), grid, dim3(kThreads), 0, stream, al);    \
-  else                                                                                        \
-    hipLaunchKernelGGL((paged_copy_kernel<V, false>), grid, dim3(kThreads), 0, stream, al);
+#define CBK_LAUNCH_PAGED(V)                                                              \
+  if (gather)                                                                            \
+    hipLaunchKernelGGL((paged_copy_kernel<V, true, kGatherThreads>), grid,               \
+                       dim3(kGatherThreads), 0, stream, al);                             \
+  else                                                                                   \
+    hipLaunchKernelGGL((paged_copy_kernel<V, false, kScatterThreads>), grid,             \
+                       dim3(kScatterThreads), 0, stream, al);
     switch (vec) {
       case 16: CBK_LAUNCH_PAGED(16); break;
       case 8: CBK_LAUNCH_PAGED(8); break;
