@@ -55,6 +55,22 @@ def parse_args():
     return p.parse_args()
 
 
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "paged_copy_qwen3_8b_store.md")
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per gather launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE x 2 + WRITE_SIZE, calibrated on a plain copy of known size)."""
+    try:
+        with open(PROFILE_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def event_time_ms(torch, fn, reps: int) -> float:
     """Average device time of fn() measured with HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -160,7 +176,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "traffic_source": "profiles/paged_copy_qwen3_8b_store.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
             "launch_us": round(gather_ms * 1e3, 2),
             "algorithmic_bytes": 2 * copy_bytes,
         },
@@ -229,7 +246,160 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
         "tokens": n, "ratio": 0.15, "overflow_radius": 16,
     }
     log(f"kdev select: {out['kdev_select']}")
+    del fresh, cached, gap
+
+    out["store_pipeline"] = store_pipeline(torch, layers, cache, src_slots, args)
+    log(f"store pipeline: {out['store_pipeline']}")
+    out["blend_load"] = blend_load(torch, synthetic, dev, args)
+    log(f"blend load: {out['blend_load']}")
     return out
+
+
+def store_pipeline(torch, layers, cache, src_slots, args):
+    """Qwen3-8B layerwise store: save_kv_layer for all 36 layers of the
+    8192-token prompt (32 chunks of 256) through the Store stream -- gather
+    into reused device staging, pinned D2H, publication into the host store
+    -- timed from the first save to the end of wait_for_save."""
+    from cacheblend_vllm.host_store import PinnedChunkStore
+    from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
+
+    L = len(layers)
+    T = src_slots.numel()
+    slots_cpu = src_slots.cpu()
+    row_bytes = cache.row_shape[0] * cache.row_shape[1] * 2
+    nbytes = L * 2 * T * row_bytes
+    times = []
+    for rep in range(3):
+        store = PinnedChunkStore(256, 1 << 40)
+        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2)
+        request = RequestMetadata(f"r{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None, True, T)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for l in range(L):
+            writer.save_layer(l, layers[l], [request])
+        writer.wait_for_save()
+        times.append(time.perf_counter() - t0)
+        committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
+        writer.close()
+        del store, writer
+    best = min(times)
+    return {"layers": L, "tokens": T, "chunks_committed": committed, "bytes_d2h": nbytes,
+            "ms": round(best * 1e3, 3), "d2h_GBps": round(nbytes / best / 1e9, 2),
+            "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+            "includes": "gather kernels + pinned D2H + host publication, first save to wait_for_save"}
+
+
+def blend_load(torch, synthetic, dev, args):
+    """Qwen3-30B-A3B blend load: 48 layers, 4 KV heads x 128 bf16, 16-token
+    blocks; 32768-token prompt, 2048-token APC prefix, 12 reused segments of
+    256-multiples separated by 1-511-token gaps (allocation_end 32767). Per
+    layer: H2D of the hit chunks (pinned, coalesced), fused assembly with RoPE
+    relocation, commit scatter into the pages; run alone and overlapped with
+    a synthetic per-layer compute (bf16 GEMMs) on the serving stream."""
+    import numpy as np
+
+    from cacheblend_vllm.config import CacheBlendConfig
+    from cacheblend_vllm.host_store import PinnedChunkStore
+    from cacheblend_vllm.loader import PagedBlendLoader
+    from cacheblend_vllm.types import BlendPlan, BlendSegment
+
+    L, BS, H, D, A, APC = 48, 16, 4, 128, 32767, 2048
+    rng = np.random.default_rng(0)
+    gaps = rng.integers(1, 512, 12)
+    chunks_total = (A - APC - int(gaps.sum())) // 256
+    lens = 1 + rng.multinomial(chunks_total - 12, np.full(12, 1 / 12))
+    segs, pos, src = [], APC, 0
+    for g, m in zip(gaps, lens):
+        pos += int(g)
+        segs.append((src, pos, 256 * int(m)))
+        src += 256 * int(m) + 512
+        pos += 256 * int(m)
+    hit = sum(n for _, _, n in segs)
+    nb = (A + BS - 1) // BS + 8
+    layers = [synthetic.paged_pool(nb, BS, H, D, torch.bfloat16, dev, seed=100 + l) for l in range(L)]
+    store = PinnedChunkStore(256, 1 << 40)
+    blend_segments = []
+    host_runs = []
+    for i, (s0, t0, n) in enumerate(segs):
+        runs = [torch.empty((2, n, H, D), dtype=torch.bfloat16, pin_memory=True) for _ in range(L)]
+        for r in runs:
+            r.copy_(torch.randn(r.shape, device=dev, dtype=torch.bfloat16))
+        host_runs.append(runs)
+        for c in range(0, n, 256):
+            sid = store.begin_put("bench", s0 + c, list(range(s0 + c + 7 * i, s0 + c + 7 * i + 256)), L)
+            for l in range(L):
+                store.put_layer_host(sid, l, runs[l][:, c : c + 256])
+            blend_segments.append(BlendSegment(sid, t0 + c))
+    store.pin("blend", blend_segments)
+    plan = BlendPlan(APC, A, hit, tuple(blend_segments))
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
+    slots = synthetic.block_slots(perm[: (A + BS - 1) // BS], BS, A)
+
+    class Rope:
+        head_size = rotary_dim = D
+        is_neox_style = True
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        cos_sin_cache = torch.cat([(torch.arange(65536, dtype=torch.float32)[:, None] * inv).cos(),
+                                   (torch.arange(65536, dtype=torch.float32)[:, None] * inv).sin()], -1).to(dev)
+
+    rope = Rope()
+    cfg = CacheBlendConfig.from_extra_config({})
+    load_stream = torch.cuda.Stream()
+    h2d_bytes = L * hit * 2 * H * D * 2
+
+    def run(compute=None):
+        loader = PagedBlendLoader(layers, store, "blend", plan, slots, BS, cfg, load_stream=load_stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loader.prefetch(0, rope)
+        for l in range(L):
+            buf = loader.get(l)
+            loader.prefetch(l + 1, rope)
+            if compute is not None:
+                compute()
+            loader.commit(l, buf)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    run()
+    load_only = min(run() for _ in range(2))
+    # per-layer compute of about 1.5x one layer's load time
+    a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
+    c = torch.empty(4096, 4096, device=dev, dtype=torch.bfloat16)
+    torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    gemm_s = (time.perf_counter() - t0) / 20
+    reps = max(1, int(round(1.5 * load_only / L / gemm_s)))
+
+    def compute():
+        for _ in range(reps):
+            torch.mm(a, b, out=c)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(L):
+        compute()
+    torch.cuda.synchronize()
+    compute_only = time.perf_counter() - t0
+    overlapped = min(run(compute) for _ in range(2))
+    hidden = 1.0 - max(0.0, overlapped - compute_only) / load_only
+    store.release("blend")
+    return {
+        "layers": L, "allocation_end": A, "apc_prefix": APC, "hit_tokens": hit,
+        "segments": len(segs), "h2d_bytes": h2d_bytes,
+        "load_only_ms": round(load_only * 1e3, 3),
+        "h2d_GBps_load_only": round(h2d_bytes / load_only / 1e9, 2),
+        "host_link_frac": round(h2d_bytes / load_only / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+        "compute_only_ms": round(compute_only * 1e3, 3),
+        "overlapped_ms": round(overlapped * 1e3, 3),
+        "load_hidden_frac": round(hidden, 4),
+        "compute_per_layer": f"{reps} x bf16 GEMM 4096^3",
+    }
 
 
 def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev):

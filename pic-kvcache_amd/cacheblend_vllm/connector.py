@@ -1,0 +1,219 @@
+"""CacheBlendConnectorV1, worker data path, on MI355X.
+
+Keeps the reference connector's class name, constructor and worker-side
+methods (cacheblend_vllm/connector.py:75-568) for the KV data path:
+
+  register_kv_caches   layer order, pinned chunk store, Store/Load streams
+  save_kv_layer        Store-stream gather + pinned D2H + async publication
+  wait_for_save        the Store-completion / publication boundary
+  start_load_kv        PagedBlendLoader + the registered layerwise executor,
+                       failure policy ``kv_load_failure_policy=recompute``
+  get_finished, get_block_ids_with_load_errors, close
+
+The scheduler half (lookup RPC, matcher, plan gating, metadata building)
+is the reference's control plane and is not part of this package: those
+methods raise NotImplementedError; ``_slot_mapping`` (the slot format the
+kernels consume) is provided in ``store_path``.
+"""
+
+from __future__ import annotations
+
+import re
+from typing import Any
+
+import torch
+
+from .config import CacheBlendConfig
+from .host_store import PinnedChunkStore
+from .loader import PagedBlendLoader
+from .store_path import (  # noqa: F401 - re-exported reference names
+    CacheBlendConnectorMetadata,
+    RequestMetadata,
+    StoreStreamWriter,
+    _slot_mapping,
+)
+from .trace import PipelineTracer
+
+try:  # vLLM's connector base when vLLM is installed
+    from vllm.distributed.kv_transfer.kv_connector.v1.base import (  # type: ignore
+        KVConnectorBase_V1 as _Base,
+        KVConnectorRole,
+    )
+except ImportError:  # vLLM absent: a minimal stand-in with the same role enum
+    import enum
+
+    class KVConnectorRole(enum.Enum):  # type: ignore[no-redef]
+        SCHEDULER = 0
+        WORKER = 1
+
+    class _Base:  # type: ignore[no-redef]
+        def __init__(self, vllm_config, role, kv_cache_config=None):
+            self._vllm_config = vllm_config
+            self._role = role
+            self._connector_metadata = None
+
+        @property
+        def role(self):
+            return self._role
+
+        def bind_connector_metadata(self, metadata) -> None:
+            self._connector_metadata = metadata
+
+        def clear_connector_metadata(self) -> None:
+            self._connector_metadata = None
+
+        def _get_connector_metadata(self):
+            return self._connector_metadata
+
+
+def _layer_sort_key(name: str) -> tuple[int, str]:
+    """Trailing layer index of a vLLM layer name (reference connector.py:48-50)."""
+    matches = re.findall(r"(?:layers?\.)?(\d+)", name)
+    return (int(matches[-1]) if matches else 1 << 30, name)
+
+
+class CacheBlendConnectorV1(_Base):
+    """CacheBlend KV connector (worker data path on MI355X)."""
+
+    def __init__(self, vllm_config, role, kv_cache_config=None):
+        super().__init__(vllm_config, role, kv_cache_config)
+        transfer = vllm_config.kv_transfer_config
+        self.config = CacheBlendConfig.from_extra_config(transfer.kv_connector_extra_config)
+        self._recompute_on_failure = getattr(transfer, "kv_load_failure_policy", None) == "recompute"
+        self.engine_id = str(transfer.engine_id)
+        self.block_size = int(vllm_config.cache_config.block_size)
+        if int(vllm_config.parallel_config.pipeline_parallel_size) != 1:
+            raise ValueError("CacheBlendConnectorV1 currently requires pipeline_parallel_size=1")
+        self.model_scope = self.config.model_scope or str(
+            getattr(vllm_config.model_config, "model", "unknown-model")
+        )
+        self._trace = PipelineTracer("scheduler" if role is KVConnectorRole.SCHEDULER else "worker")
+        self._store: PinnedChunkStore | None = None
+        self._writer: StoreStreamWriter | None = None
+        self._kv_caches: list = []
+        self._layer_ids: dict[str, int] = {}
+        self._executor = None
+        self._load_stream = None
+        self._load_errors: set[int] = set()
+
+    # ---------------------------------------------------------- worker
+
+    def register_kv_caches(self, kv_caches: dict[str, Any], executor=None) -> None:
+        """Reference connector.py:168-213 (``executor``: the layerwise model
+        executor whose ``run(request_id, tokens, plan, loader)`` drives the
+        loader; the model forward itself is outside this package)."""
+        if self.role is not KVConnectorRole.WORKER:
+            return
+        ordered = sorted(kv_caches.items(), key=lambda item: _layer_sort_key(item[0]))
+        self._layer_ids = {name: i for i, (name, _) in enumerate(ordered)}
+        self._kv_caches = [value for _, value in ordered]
+        if not self._kv_caches:
+            raise RuntimeError("CacheBlendConnectorV1 received no KV caches")
+        self._store = PinnedChunkStore(self.config.chunk_size, self.config.max_local_cpu_bytes)
+        self._load_stream = torch.cuda.Stream()
+        self._writer = StoreStreamWriter(
+            self._store, self.block_size, self.config.chunk_size, len(self._kv_caches),
+            self.model_scope, self.config.store_workers, self.config.max_inflight_store_batches,
+            tracer=self._trace,
+        )
+        self._executor = executor
+        self._trace.emit("worker_registered", rank=0, layers=len(self._kv_caches),
+                         cpu_cache_bytes=self.config.max_local_cpu_bytes)
+
+    def _layer_id(self, layer_name: str) -> int | None:
+        layer_id = self._layer_ids.get(layer_name)
+        if layer_id is None:
+            key = _layer_sort_key(layer_name)[0]
+            layer_id = next(
+                (i for name, i in self._layer_ids.items() if _layer_sort_key(name)[0] == key), None
+            )
+        return layer_id
+
+    def save_kv_layer(self, layer_name: str, kv_layer: Any, attn_metadata: Any, **kwargs: Any) -> None:
+        """Reference connector.py:281-361."""
+        if self._writer is None:
+            return
+        metadata = self._get_connector_metadata()
+        if not isinstance(metadata, CacheBlendConnectorMetadata):
+            return
+        layer_id = self._layer_id(layer_name)
+        if layer_id is None:
+            return
+        self._writer.save_layer(layer_id, kv_layer, metadata.requests)
+
+    def wait_for_save(self) -> None:
+        if self._writer is not None:
+            self._writer.wait_for_save()
+
+    def wait_for_layer_load(self, layer_name: str) -> None:
+        return
+
+    def start_load_kv(self, forward_context: Any, **kwargs: Any) -> None:
+        """Reference connector.py:215-276."""
+        metadata = self._get_connector_metadata()
+        if not isinstance(metadata, CacheBlendConnectorMetadata):
+            raise TypeError("unexpected CacheBlend connector metadata")
+        if self._store is None or self._executor is None:
+            if any(request.plan is not None for request in metadata.requests):
+                raise RuntimeError("CacheBlend worker was not initialized")
+            return
+        for request in metadata.requests:
+            if request.plan is None:
+                continue
+            loader = PagedBlendLoader(
+                self._kv_caches, self._store, request.request_id, request.plan,
+                request.slot_mapping, self.block_size, self.config, tracer=self._trace,
+                load_stream=self._load_stream,
+            )
+            try:
+                self._executor.run(request.request_id, request.token_ids, request.plan, loader)
+            except Exception:
+                self._record_load_error(request)
+                if not self._recompute_on_failure:
+                    raise
+            finally:
+                self._store.release(request.request_id)
+
+    def get_finished(self, finished_req_ids: set[str]):
+        if self._writer is not None:
+            self._writer.finished(finished_req_ids)
+        return None, None
+
+    def get_block_ids_with_load_errors(self) -> set[int]:
+        result, self._load_errors = self._load_errors, set()
+        return result
+
+    def _record_load_error(self, request: RequestMetadata) -> None:
+        """Block ids of the externally allocated span (reference connector.py:564-568)."""
+        if request.plan is None:
+            return
+        slots = request.slot_mapping[request.plan.apc_prefix_tokens : request.plan.allocation_end]
+        self._load_errors.update(int(v) for v in torch.unique(slots // self.block_size))
+
+    def close(self) -> None:
+        if self._writer is not None:
+            self._writer.close()
+            self._writer = None
+        if self._store is not None:
+            self._store.clear()
+        self._trace.close()
+
+    # ------------------------------------------------------- scheduler
+
+    def _control_plane(self, name: str):
+        raise NotImplementedError(
+            f"CacheBlendConnectorV1.{name} is the scheduler-side control plane (lookup RPC, "
+            "matcher, plan gating); this package implements the worker KV data path only"
+        )
+
+    def get_num_new_matched_tokens(self, request, num_computed_tokens):
+        return self._control_plane("get_num_new_matched_tokens")
+
+    def update_state_after_alloc(self, request, blocks, num_external_tokens):
+        return self._control_plane("update_state_after_alloc")
+
+    def build_connector_meta(self, scheduler_output):
+        return self._control_plane("build_connector_meta")
+
+    def request_finished(self, request, block_ids):
+        return self._control_plane("request_finished")

@@ -1,0 +1,323 @@
+"""Worker-side save pipeline of CacheBlendConnectorV1 on MI355X.
+
+Same protocol and method names as the reference connector's save half
+(cacheblend_vllm/connector.py:281-549), with the gather running in the
+gfx950 paged-gather kernel and the copies on a HIP side stream:
+
+  save_kv_layer(layer)      per request: complete chunk_size chunks up to
+                            save_end, one reservation per (chunk, layer),
+                            one fused slot list over every pending chunk
+  _enqueue_store_batch      Store stream: wait for the serving stream,
+                            gather into the request's reused device staging,
+                            pinned D2H, record an event, hand the batch to a
+                            publisher thread (backpressure semaphore)
+  _publish_after_event      publisher thread: event.synchronize(), then put
+                            per-chunk views of the pinned batch into the store;
+                            any failure aborts every chunk of the batch
+  wait_for_save             Store-stream sync + join publishers; staging freed
+
+Everything enqueued goes to one default-priority Store stream, so the D2H of
+layer l and the gather of layer l + 1 are ordered on it while the serving
+stream keeps computing.
+"""
+
+from __future__ import annotations
+
+import threading
+import time
+from concurrent.futures import Future, ThreadPoolExecutor
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+
+from .kv_layout import gather_paged_kv, kv_planes
+from .trace import PipelineTracer
+from .types import BlendPlan, SegmentId
+
+
+def _slot_mapping(block_ids: list[int], block_size: int, token_count: int) -> torch.Tensor:
+    """``block * bs + offset`` over ``block_ids``, first ``token_count`` slots
+    (reference connector.py:42-45)."""
+    blocks = torch.tensor(block_ids, dtype=torch.long)
+    offsets = torch.arange(block_size, dtype=torch.long)
+    return (blocks[:, None] * block_size + offsets[None, :]).flatten()[:token_count]
+
+
+@dataclass(slots=True)
+class RequestMetadata:
+    """Per-request worker metadata (reference connector.py:53-60)."""
+
+    request_id: str
+    token_ids: list[int]
+    slot_mapping: torch.Tensor
+    plan: BlendPlan | None
+    save: bool
+    save_end: int
+
+
+@dataclass(slots=True)
+class CacheBlendConnectorMetadata:
+    requests: list[RequestMetadata] = field(default_factory=list)
+
+
+class CudaStreams:
+    """torch.cuda stream/event factory (replaceable by fakes in tests)."""
+
+    @staticmethod
+    def current_stream():
+        return torch.cuda.current_stream()
+
+    @staticmethod
+    def stream(s):
+        return torch.cuda.stream(s)
+
+    @staticmethod
+    def Event():  # noqa: N802 - mirrors torch.cuda.Event
+        return torch.cuda.Event()
+
+    @staticmethod
+    def Stream():  # noqa: N802
+        return torch.cuda.Stream()
+
+
+class StoreStreamWriter:
+    """The save half of CacheBlendConnectorV1 (worker role)."""
+
+    def __init__(
+        self,
+        store,
+        block_size: int,
+        chunk_size: int,
+        num_layers: int,
+        model_scope: str,
+        store_workers: int = 1,
+        max_inflight_store_batches: int = 8,
+        tracer: PipelineTracer | None = None,
+        streams=CudaStreams,
+        store_stream=None,
+    ):
+        self._store = store
+        self.block_size = block_size
+        self.chunk_size = chunk_size
+        self.num_layers = num_layers
+        self.model_scope = model_scope
+        self._trace = tracer or PipelineTracer("worker")
+        self._streams = streams
+        self._store_stream = store_stream if store_stream is not None else streams.Stream()
+        self._save_pool = ThreadPoolExecutor(max_workers=store_workers,
+                                             thread_name_prefix="cacheblend-save")
+        self._save_slots = threading.Semaphore(max_inflight_store_batches)
+        self._save_lock = threading.Lock()
+        self._save_futures: set[Future] = set()
+        self._pending_store_counts: dict[str, int] = {}
+        self._save_segments: dict[str, list[tuple[int, SegmentId]]] = {}
+        self._store_staging_by_request: dict[str, torch.Tensor] = {}
+        self._retired_store_staging: list[torch.Tensor] = []
+        # per request: (host slot list, device copy); the fused slot list is
+        # normally identical for every layer, so it is uploaded once
+        self._device_slots: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    # ------------------------------------------------------------- save
+
+    def save_layer(self, layer_id: int, kv_layer: Any, requests: list[RequestMetadata]) -> None:
+        """The per-request body of save_kv_layer (reference connector.py:308-361)."""
+        for request in requests:
+            if not request.save:
+                continue
+            usable = min(request.save_end, len(request.token_ids), request.slot_mapping.numel())
+            usable = usable // self.chunk_size * self.chunk_size
+            pending: list[tuple[SegmentId, int, int]] = []
+            slot_parts: list[torch.Tensor] = []
+            for start, segment_id in self._request_save_segments(request, usable):
+                if not self._store.reserve_layer(segment_id, layer_id):
+                    continue
+                pending.append((segment_id, layer_id, self.chunk_size))
+                slot_parts.append(request.slot_mapping[start : start + self.chunk_size])
+            if not pending:
+                continue
+            trace = self._trace.enabled
+            started = time.monotonic_ns() if trace else 0
+            try:
+                self._enqueue_store_batch(
+                    pending, kv_layer, torch.cat(slot_parts), request_id=request.request_id,
+                    store_enqueued_ns=time.monotonic_ns() if trace else None,
+                )
+                if trace:
+                    self._trace.emit(
+                        "save_store_enqueued",
+                        request_id=request.request_id,
+                        layer_id=layer_id,
+                        chunks=len(pending),
+                        tokens=sum(n for _, _, n in pending),
+                        duration_us=(time.monotonic_ns() - started) / 1000,
+                    )
+            except Exception:
+                for segment_id, _, _ in pending:
+                    self._store.abort_put(segment_id)
+                raise
+
+    def _request_save_segments(self, request: RequestMetadata, usable: int) -> list[tuple[int, SegmentId]]:
+        """Chunk identities hashed once per request (reference connector.py:363-382)."""
+        segments = self._save_segments.setdefault(request.request_id, [])
+        start = len(segments) * self.chunk_size
+        while start < usable:
+            end = start + self.chunk_size
+            segment_id = self._store.begin_put(
+                self.model_scope, start, request.token_ids[start:end], self.num_layers
+            )
+            segments.append((start, segment_id))
+            start = end
+        return segments[: usable // self.chunk_size]
+
+    def _enqueue_store_batch(
+        self,
+        pending: list[tuple[Any, int, int]],
+        kv_layer: Any,
+        slots: torch.Tensor,
+        request_id: str,
+        store_enqueued_ns: int | None = None,
+    ) -> None:
+        """Gather + pinned D2H on the Store stream (reference connector.py:384-447)."""
+        self._save_slots.acquire()
+        try:
+            if self._store_stream is None:
+                raise RuntimeError("CacheBlend Store stream was not initialized")
+            current = self._streams.current_stream()
+            with self._streams.stream(self._store_stream):
+                self._store_stream.wait_stream(current)
+                slots = self._upload_slots(request_id, slots, kv_layer)
+                staging = self._store_staging_by_request.get(request_id)
+                if staging is None or staging.shape[1] != slots.numel():
+                    if staging is not None:
+                        # an earlier D2H may still read it: keep it until the
+                        # Store stream drains (wait_for_save)
+                        self._retired_store_staging.append(staging)
+                    staging = gather_paged_kv(kv_layer, slots, self.block_size).contiguous()
+                    self._store_staging_by_request[request_id] = staging
+                else:
+                    gather_paged_kv(kv_layer, slots, self.block_size, out=staging)
+                host = torch.empty(staging.shape, dtype=staging.dtype, device="cpu", pin_memory=True)
+                host.copy_(staging, non_blocking=True)
+                event = self._streams.Event()
+                event.record(self._store_stream)
+            future = self._save_pool.submit(
+                self._publish_after_event, event, pending, host, request_id, store_enqueued_ns
+            )
+        except Exception:
+            self._save_slots.release()
+            raise
+        with self._save_lock:
+            self._save_futures.add(future)
+            self._pending_store_counts[request_id] = self._pending_store_counts.get(request_id, 0) + 1
+        future.add_done_callback(self._save_done)
+
+    def _upload_slots(self, request_id: str, slots: torch.Tensor, kv_layer: Any) -> torch.Tensor:
+        """Device copy of a host slot list, reused while it does not change.
+        The upload is a pinned, non-blocking copy on the Store stream, so the
+        host never waits for earlier Store work here."""
+        if slots.device.type != "cpu" or not torch.cuda.is_available():
+            return slots
+        cached = self._device_slots.get(request_id)
+        if cached is not None and cached[0].shape == slots.shape and torch.equal(cached[0], slots):
+            return cached[1]
+        key, _ = kv_planes(kv_layer)
+        num_slots = key.shape[0] * self.block_size
+        if slots.numel() and (int(slots.min()) < 0 or int(slots.max()) >= num_slots):
+            raise IndexError(f"slot_mapping holds slots outside [0, {num_slots})")
+        host = slots.to(torch.long).contiguous().pin_memory()
+        device = host.to("cuda", non_blocking=True)
+        self._device_slots[request_id] = (host, device)
+        return device
+
+    def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host: torch.Tensor) -> bool:
+        """Per-chunk views of the pinned batch into the store (connector.py:449-466)."""
+        offset = 0
+        committed = False
+        for segment_id, layer_id, length in pending:
+            result = self._store.put_layer_host(segment_id, layer_id, host[:, offset : offset + length])
+            if result is not None:
+                committed |= result
+            offset += length
+        return committed
+
+    def _publish_after_event(
+        self,
+        event: Any,
+        pending: list[tuple[Any, int, int]],
+        host: torch.Tensor,
+        request_id: str | None = None,
+        store_enqueued_ns: int | None = None,
+    ) -> bool:
+        """Publisher thread body (reference connector.py:468-499)."""
+        try:
+            event.synchronize()
+            committed = self._publish_host_batch(pending, host)
+            if self._trace.enabled:
+                self._trace.emit(
+                    "save_store_finished",
+                    request_id=request_id,
+                    layer_id=pending[0][1] if pending else None,
+                    chunks=len(pending),
+                    tokens=sum(n for _, _, n in pending),
+                    duration_us=((time.monotonic_ns() - store_enqueued_ns) / 1000
+                                 if store_enqueued_ns is not None else None),
+                    committed_segment=committed,
+                )
+            return committed
+        except Exception:
+            for segment_id, _, _ in pending:
+                self._store.abort_put(segment_id)
+            return False
+
+    def _save_done(self, future: Future) -> None:
+        self._save_slots.release()
+
+    def wait_for_save(self) -> None:
+        """Store-stream sync, then join publishers (reference connector.py:504-534)."""
+        started = time.monotonic_ns() if self._trace.enabled else 0
+        futures: tuple[Future, ...] = ()
+        counts: dict[str, int] = {}
+        try:
+            if self._store_stream is not None:
+                self._store_stream.synchronize()
+            with self._save_lock:
+                futures = tuple(self._save_futures)
+                counts = dict(self._pending_store_counts)
+                self._pending_store_counts.clear()
+            for future in futures:
+                future.result()
+        finally:
+            with self._save_lock:
+                self._save_futures.difference_update(futures)
+            self._store_staging_by_request.clear()
+            self._retired_store_staging.clear()
+            self._device_slots.clear()
+        if self._trace.enabled:
+            duration = (time.monotonic_ns() - started) / 1000
+            for request_id, stores in counts.items():
+                self._trace.emit("save_store_wait_finished", request_id=request_id, stores=stores,
+                                 duration_us=duration)
+
+    def finished(self, request_ids) -> None:
+        """get_finished's store cleanup (reference connector.py:551-557)."""
+        for request_id in request_ids:
+            self._store.release(request_id)
+            for _, segment_id in self._save_segments.pop(request_id, ()):
+                self._store.abort_put(segment_id)
+
+    def close(self) -> None:
+        try:
+            while True:
+                with self._save_lock:
+                    futures = tuple(self._save_futures)
+                if not futures:
+                    break
+                for future in futures:
+                    future.result()
+                with self._save_lock:
+                    self._save_futures.difference_update(futures)
+        finally:
+            self._store_staging_by_request.clear()
+            self._retired_store_staging.clear()
+            self._save_pool.shutdown(wait=True, cancel_futures=False)
