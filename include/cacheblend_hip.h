@@ -171,6 +171,32 @@ int cbk_blend_assemble(const cbk_kv_desc* kv, const int64_t* slots_dev, const in
                        void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
                        int32_t* bad_dev, cbk_stream_t stream);
 
+/* Workspace bytes cbk_sparse_q_scores needs. */
+size_t cbk_sparse_q_workspace_bytes(int64_t nq, int64_t nk, int64_t hq, int64_t hkv);
+
+/*
+ * Sparse-Q attention mass per key:
+ *   full[k] = sum_{h < hq} sum_{i < nq, pos_i >= k}
+ *             softmax_k( r(q[row_i, h, :] . key[k, h / (hq/hkv), :]) * scale )
+ * with row_i = q_index_dev ? q_index_dev[i] : i, pos_i = positions_dev[row_i],
+ * the softmax over all nk keys with keys k > pos_i masked, and r rounding to
+ * bf16 (round_logits 1), f16 (2) or not at all (0). q is [*, hq, head_dim]
+ * (row stride q_row_stride_elems), key is [nk, hkv, head_dim]. Writes
+ * out_scores_dev[i] = full[out_index_dev[i]] (i < n_out; out_index NULL:
+ * identity) and, when non-NULL, full_scores_dev[0 .. nk).
+ * bf16/f16 run on MFMA (head_dim 64 or 128, up to 16 query heads per KV
+ * head); f32 runs exact float32 dots. Deterministic (no float atomics).
+ * Replaces Qwen3BlendExecutor._sparse_q_scores' score loop and its
+ * index_select (cacheblend_vllm/ascend.py:683-701).
+ */
+int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int64_t* q_index_dev,
+                        int64_t nq, const int64_t* positions_dev, const void* k_dev,
+                        int64_t k_row_stride_elems, int64_t nk, int64_t hq, int64_t hkv,
+                        int64_t head_dim, float scale, int32_t dtype, int32_t round_logits,
+                        const int64_t* out_index_dev, int64_t n_out, float* out_scores_dev,
+                        float* full_scores_dev, void* workspace_dev, size_t workspace_bytes,
+                        cbk_stream_t stream);
+
 /* Largest dilation radius cbk_select / cbk_kdev_select accept. */
 #define CBK_MAX_DILATION_RADIUS 4096
 

@@ -185,6 +185,90 @@ def dilate(gap_mask: torch.Tensor, radius: int) -> torch.Tensor:
     return out
 
 
+_ROUND_MODES = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 0}
+
+
+def sparse_q_full_scores(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    query_rows: torch.Tensor | None,
+    positions: torch.Tensor,
+    scale: float,
+    out_index: torch.Tensor | None = None,
+    want_full: bool = False,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """Per-key causal attention mass (``cbk_sparse_q_scores``).
+
+    ``query`` is ``[N, Hq, D]``, ``key`` ``[K, Hkv, D]``; the sparse queries
+    are ``query[query_rows]`` (all rows when None) at ``positions[row]``.
+    Returns ``(full[out_index], full)`` (each None when not requested).
+    Reference ascend.py:683-701.
+    """
+    _native.require_device(query, "query")
+    if query.ndim != 3 or key.ndim != 3:
+        raise ValueError("query must be [N, Hq, D] and key [K, Hkv, D]")
+    n, hq, d = query.shape
+    nk, hkv, dk = key.shape
+    if hq % hkv:
+        raise ValueError(
+            "Sparse-Q requires query heads to be divisible by KV heads; "
+            f"got {hq} and {hkv}"
+        )
+    if d != dk or query.dtype != key.dtype or query.device != key.device:
+        raise ValueError("query and key must share head_dim, dtype and device")
+    if query.dtype not in _ROUND_MODES:
+        raise ValueError(f"Sparse-Q dtype {query.dtype} is not supported")
+    if query.stride(2) != 1 or query.stride(1) != d:
+        query = query.contiguous()
+    if key.stride(2) != 1 or key.stride(1) != d:
+        key = key.contiguous()
+    dev = query.device
+    rows = None
+    nq = n
+    if query_rows is not None:
+        rows = query_rows.to(device=dev, dtype=torch.long).contiguous()
+        nq = rows.numel()
+    pos = positions.to(device=dev, dtype=torch.long).contiguous()
+    out = full = None
+    idx = None
+    n_out = 0
+    if out_index is not None:
+        idx = out_index.to(device=dev, dtype=torch.long).contiguous()
+        n_out = idx.numel()
+        out = torch.empty(n_out, dtype=torch.float32, device=dev)
+    if want_full:
+        full = torch.empty(nk, dtype=torch.float32, device=dev)
+    lib = _native.load()
+    ws = _native.workspace(dev, lib.cbk_sparse_q_workspace_bytes(nq, nk, hq, hkv))
+    rc = lib.cbk_sparse_q_scores(
+        query.data_ptr(), query.stride(0), _native.ptr(rows), nq, pos.data_ptr(),
+        key.data_ptr(), key.stride(0), nk, hq, hkv, d, float(scale),
+        _native.DTYPE_CODES[query.dtype], _ROUND_MODES[query.dtype],
+        _native.ptr(idx), n_out, _native.ptr(out), _native.ptr(full),
+        ws.data_ptr(), ws.numel(), _native.stream_handle(dev),
+    )
+    _native.check(rc, "sparse_q_scores")
+    return out, full
+
+
+def sparse_q_masks(gap_mask: torch.Tensor, tail_query_tokens: int, radius: int):
+    """``(query_mask, forced_mask, has_gap)`` (reference ascend.py:652-671).
+
+    Without gaps the last ``min(tail, N)`` tokens are queries and forced;
+    with gaps and ``radius`` > 0 the forced set is dilated (``cbk_dilate``).
+    """
+    query_mask = gap_mask.clone()
+    forced = gap_mask.clone()
+    has_gap = bool(gap_mask.any().item())
+    if not has_gap:
+        tail = min(tail_query_tokens, gap_mask.shape[0])
+        query_mask[-tail:] = True
+        forced[-tail:] = True
+    if radius and has_gap:
+        forced |= dilate(gap_mask, radius)
+    return query_mask, forced, has_gap
+
+
 class BlendSelector:
     """The selection methods of the reference ``Qwen3BlendExecutor``.
 
@@ -220,6 +304,52 @@ class BlendSelector:
             raise ValueError("forced selection mask must match the active token shape")
         scores = self._reduce(scores)
         return select(scores, gap_mask, self.config.ratio_for(layer_id), forced_mask)
+
+    def _sparse_q_scores(
+        self,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        absolute_indices: torch.Tensor,
+        gap_mask: torch.Tensor,
+        scale: float,
+    ) -> tuple[torch.Tensor, torch.Tensor, dict]:
+        """Reference ascend.py:638-711: ``(scores[N], forced[N], stats)``.
+
+        ``query`` ``[N, Hq, D]`` (active tokens), ``key`` ``[K, Hkv, D]`` (the
+        whole context), ``absolute_indices[N]`` their positions. The score
+        loop is one MFMA kernel pair instead of ``N / query_score_chunk_size``
+        matmul + softmax launches; ``query_score_chunk_size`` bounds nothing
+        here (the kernel streams K through registers and LDS).
+        """
+        radius = self.config.overflow_blocks * self.block_size
+        query_mask, forced, has_gap = sparse_q_masks(gap_mask, self.config.tail_query_tokens, radius)
+        sparse = torch.nonzero(query_mask).flatten()
+        gap_count = int(gap_mask.sum().item())
+        scores, _ = sparse_q_full_scores(query, key, sparse, absolute_indices, scale,
+                                         out_index=absolute_indices)
+        stats = {
+            "active_tokens": int(query.shape[0]),
+            "gap_tokens": gap_count,
+            "cached_tokens": int(query.shape[0]) - gap_count,
+            "sparse_query_tokens": int(sparse.numel()),
+            "tail_fallback": not has_gap,
+            "overflow_blocks": self.config.overflow_blocks,
+        }
+        return scores, forced, stats
+
+    def sparse_q_select(
+        self,
+        query: torch.Tensor,
+        score_keys: torch.Tensor,
+        absolute_indices: torch.Tensor,
+        gap_mask: torch.Tensor,
+        scale: float,
+        layer_id: int | None = None,
+    ) -> tuple[torch.Tensor, dict]:
+        """The check-layer Sparse-Q block (ascend.py:545-566): scores, then
+        ``_select`` with the forced (gap + overflow / tail) mask."""
+        scores, forced, stats = self._sparse_q_scores(query, score_keys, absolute_indices, gap_mask, scale)
+        return self._select(scores, gap_mask, layer_id, forced_mask=forced), stats
 
     def kv_deviation_select(
         self,

@@ -1,0 +1,149 @@
+"""GPU parity: Sparse-Q attention-mass scores and selection.
+
+Scores must match the oracle within 1e-2 relative (
+the observed error is printed and is far smaller). Index sets are compared
+outside an epsilon band around the k-th score: keys whose scores differ from
+the boundary by more than the largest observed score difference must agree.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from cacheblend_vllm import selection as S
+from cacheblend_vllm import synthetic
+from cacheblend_vllm.config import CacheBlendConfig
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+RTOL = 1e-2
+
+
+def test_reference_closed_form_known_answer(golden):
+    case = golden["sparse_q_closed_form"]
+    q1 = torch.tensor(case["query_one_head"])
+    query = torch.cat((q1, q1.flip(-1)), dim=1).to(DEV)
+    key = torch.tensor(case["key"]).to(DEV)
+    sel = S.BlendSelector(CacheBlendConfig.from_extra_config({
+        "selection_strategy": "sparse_q", "check_layers": [1],
+        "query_score_chunk_size": case["query_score_chunk_size"],
+        "overflow_blocks": case["overflow_blocks"], "tail_query_tokens": case["tail_query_tokens"],
+        "strict_version_check": False}), case["block_size"])
+    scores, forced, stats = sel._sparse_q_scores(
+        query, key, torch.tensor(case["absolute"], device=DEV),
+        torch.tensor(case["gap"], device=DEV), case["scale"])
+    np.testing.assert_allclose(scores.cpu().numpy(), case["expected_scores"], rtol=1e-5)
+    assert forced.tolist() == case["expected_forced"]
+    assert stats["sparse_query_tokens"] == case["expected_sparse_query_tokens"]
+    assert stats["tail_fallback"] == case["expected_tail_fallback"]
+
+
+def test_reference_overflow_and_tail_known_answers(golden):
+    case = golden["sparse_q_overflow_and_tail"]
+    sel = S.BlendSelector(CacheBlendConfig.from_extra_config({
+        "chunk_size": 2, "selection_strategy": "sparse_q", "check_layers": [1],
+        "query_score_chunk_size": case["query_score_chunk_size"],
+        "overflow_blocks": case["overflow_blocks"], "tail_query_tokens": case["tail_query_tokens"],
+        "strict_version_check": False}), case["block_size"])
+    ones = torch.ones(6, 1, 2, device=DEV)
+    for sub in case["cases"]:
+        _, forced, stats = sel._sparse_q_scores(ones, ones, torch.tensor(case["absolute"], device=DEV),
+                                                torch.tensor(sub["gap"], device=DEV), case["scale"])
+        assert forced.tolist() == sub["expected_forced"]
+        assert stats["tail_fallback"] == sub["expected_tail_fallback"]
+        if "expected_sparse_query_tokens" in sub:
+            assert stats["sparse_query_tokens"] == sub["expected_sparse_query_tokens"]
+    with pytest.raises(ValueError, match="divisible by KV heads"):
+        sel._sparse_q_scores(torch.ones(6, 3, 2, device=DEV), torch.ones(6, 2, 2, device=DEV),
+                             torch.arange(6, device=DEV), torch.zeros(6, dtype=torch.bool, device=DEV), 1.0)
+
+
+def _inputs(n_active, prefix, hq, hkv, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    nk = prefix + n_active
+    q = (torch.randn(n_active, hq, d, generator=g) / d ** 0.5).to(dtype)
+    k = (torch.randn(nk, hkv, d, generator=g) / d ** 0.5).to(dtype)
+    gap = torch.from_numpy(synthetic.gap_layout(n_active, seed, hit_chunk=64, max_hit_chunks=5, max_gap=63))
+    absolute = torch.arange(prefix, nk)
+    return q, k, gap, absolute
+
+
+@pytest.mark.parametrize("dtype,d,hq,hkv", [
+    (torch.bfloat16, 128, 32, 4),
+    (torch.bfloat16, 64, 8, 8),
+    (torch.float16, 128, 16, 2),
+    (torch.float32, 32, 4, 2),
+])
+def test_sparse_q_scores_vs_oracle(dtype, d, hq, hkv):
+    n_active, prefix = 1200 if dtype != torch.float32 else 300, 500
+    q, k, gap, absolute = _inputs(n_active, prefix, hq, hkv, d, dtype, seed=d + hq)
+    rows = torch.nonzero(gap).flatten()
+    print(f"dtype={dtype} d={d} hq={hq} hkv={hkv} queries={rows.numel()} keys={k.shape[0]}", flush=True)
+    scale = d ** -0.5
+    got, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, scale,
+                                       out_index=absolute, want_full=True)
+    qf, kf = q.float().numpy(), k.float().numpy()
+    if dtype == torch.float16:
+        # oracle rounds logits to bf16 only: emulate f16 logit rounding by
+        # comparing against unrounded float32 logits within the tolerance
+        want_full = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], scale, False)
+    else:
+        want_full = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], scale,
+                                           dtype == torch.bfloat16)
+    full = full.cpu().numpy()
+    err = np.max(np.abs(full - want_full) / np.maximum(np.abs(want_full), 1e-30))
+    print(f"max relative score error {err:.3e}", flush=True)
+    np.testing.assert_allclose(full, want_full, rtol=RTOL, atol=1e-6)
+    np.testing.assert_allclose(got.cpu().numpy(), want_full[absolute.numpy()], rtol=RTOL, atol=1e-6)
+    # softmax mass: every (query, head) row sums to one
+    assert abs(full.sum() - rows.numel() * hq) < 1e-3 * rows.numel() * hq
+    # deterministic
+    _, again = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, scale, want_full=True)
+    assert np.array_equal(again.cpu().numpy(), full)
+
+
+def test_sparse_q_select_matches_oracle_outside_epsilon_band():
+    hq, hkv, d = 32, 4, 128
+    q, k, gap, absolute = _inputs(2000, 1000, hq, hkv, d, torch.bfloat16, seed=3)
+    cfg = CacheBlendConfig.from_extra_config({"selection_strategy": "sparse_q", "check_layers": [1]})
+    sel = S.BlendSelector(cfg, 16)
+    selected, stats = sel.sparse_q_select(q.to(DEV), k.to(DEV), absolute.to(DEV), gap.to(DEV), d ** -0.5, 1)
+    scores, forced, stats2 = sel._sparse_q_scores(q.to(DEV), k.to(DEV), absolute.to(DEV), gap.to(DEV), d ** -0.5)
+    want_scores, want_forced, want_stats = O.sparse_q_scores(
+        q.float().numpy(), k.float().numpy(), absolute.numpy(), gap.numpy(), d ** -0.5,
+        block_size=16, overflow_blocks=1, tail_query_tokens=64, round_logits_bf16=True)
+    assert forced.cpu().numpy().tolist() == want_forced.tolist()
+    for key in ("active_tokens", "gap_tokens", "cached_tokens", "sparse_query_tokens", "tail_fallback"):
+        assert stats[key] == want_stats[key]
+    got_scores = scores.cpu().numpy()
+    eps = float(np.max(np.abs(got_scores - want_scores)))
+    # the GPU selection on the GPU's own scores is exact
+    np.testing.assert_array_equal(selected.cpu().numpy(), O.select(got_scores, gap.numpy(), 0.15, want_forced))
+    # against the oracle's scores: equal outside the epsilon band at the k-th score
+    want_sel = O.select(want_scores, gap.numpy(), 0.15, want_forced)
+    base = gap.numpy() | want_forced
+    k_budget = O.select_budget(len(gap), int(gap.sum()), int(base.sum()), 0.15)
+    cand = np.sort(want_scores[~base])[::-1]
+    kth = cand[k_budget - 1]
+    band = np.abs(want_scores - kth) <= 2 * eps
+    a, b = set(selected.cpu().tolist()), set(want_sel.tolist())
+    disagree = np.array(sorted(a ^ b), dtype=np.int64)
+    print(f"eps={eps:.3e} band={int(band.sum())} disagreements={disagree.size}", flush=True)
+    assert np.all(band[disagree])
+
+
+def test_sparse_q_tail_fallback_no_gaps():
+    hq, hkv, d = 8, 2, 64
+    q, k, _, absolute = _inputs(700, 300, hq, hkv, d, torch.bfloat16, seed=9)
+    gap = torch.zeros(700, dtype=torch.bool)
+    cfg = CacheBlendConfig.from_extra_config({"selection_strategy": "sparse_q", "check_layers": [1],
+                                              "tail_query_tokens": 64})
+    sel = S.BlendSelector(cfg, 16)
+    scores, forced, stats = sel._sparse_q_scores(q.to(DEV), k.to(DEV), absolute.to(DEV), gap.to(DEV), d ** -0.5)
+    want, want_forced, want_stats = O.sparse_q_scores(
+        q.float().numpy(), k.float().numpy(), absolute.numpy(), gap.numpy(), d ** -0.5,
+        block_size=16, overflow_blocks=1, tail_query_tokens=64, round_logits_bf16=True)
+    assert stats["tail_fallback"] and stats["sparse_query_tokens"] == 64
+    assert forced.cpu().numpy().tolist() == want_forced.tolist()
+    np.testing.assert_allclose(scores.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
