@@ -32,6 +32,8 @@ import statistics
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "pic-kvcache_amd"))
 
@@ -248,11 +250,55 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     log(f"kdev select: {out['kdev_select']}")
     del fresh, cached, gap
 
+    out["sparse_q"] = sparse_q(torch, S, synthetic, dev)
+    log(f"sparse_q: {out['sparse_q']}")
     out["store_pipeline"] = store_pipeline(torch, layers, cache, src_slots, args)
     log(f"store pipeline: {out['store_pipeline']}")
     out["blend_load"] = blend_load(torch, synthetic, dev, args)
     log(f"blend load: {out['blend_load']}")
     return out
+
+
+def sparse_q(torch, S, synthetic, dev):
+    """Sparse-Q scoring at Qwen3-30B-A3B layer 6: 32 query heads over 4 KV
+    heads x 128 bf16, Q/K ~ N(0,1)/sqrt(128); 4096 non-reused query tokens in
+    gap runs over a 98,304-token causal key context (the last run ends at the
+    last token); per-key attention mass summed over heads, then the top 15% of
+    cached keys plus gaps and overflow blocks."""
+    from cacheblend_vllm.config import CacheBlendConfig
+
+    nk, hq, hkv, d, nq = 98304, 32, 4, 128, 4096
+    g = torch.Generator(device=dev).manual_seed(0)
+    query = (torch.randn((nk, hq, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+    key = (torch.randn((nk, hkv, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+    gap_np = synthetic.sparse_q_layout(nk, nq, seed=0)
+    gap = torch.from_numpy(gap_np).to(dev)
+    absolute = torch.arange(nk, device=dev)
+    rows = torch.nonzero(gap).flatten()
+    pos = np.flatnonzero(gap_np)
+    flops_pass = 2.0 * d * hq * float((pos + 1).sum())
+    scale = d ** -0.5
+    fn = lambda: S.sparse_q_full_scores(query, key, rows, absolute, scale, out_index=absolute)  # noqa: E731
+    fn()
+    ms = event_time_ms(torch, fn, 3)
+    sel = S.BlendSelector(CacheBlendConfig.from_extra_config(
+        {"selection_strategy": "sparse_q", "check_layers": [1]}), 16)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    selected, stats = sel.sparse_q_select(query, key, absolute, gap, scale, 1)
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t0) * 1e3
+    achieved = 2 * flops_pass / (ms / 1e3) / 1e12
+    return {
+        "queries": nq, "keys": nk, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+        "score_ms": round(ms, 3),
+        "flops_per_pass": flops_pass,
+        "two_pass_TFLOPs": round(achieved, 1),
+        "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4),
+        "exp_per_s": round(2 * hq * float((pos + 1).sum()) / (ms / 1e3), 1),
+        "select_total_ms_with_masks_and_sync": round(total_ms, 3),
+        "selected": int(selected.numel()),
+    }
 
 
 def store_pipeline(torch, layers, cache, src_slots, args):
@@ -416,8 +462,17 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
         copy_dst.copy_(staging)
     for _ in range(args.steps):
         _kdev_async(torch, S, fresh, cached, gap)
+    del copy_dst, fresh, cached
+    nk, hq, hkv, d = 98304, 32, 4, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    query = (torch.randn((nk, hq, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+    key = (torch.randn((nk, hkv, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+    rows = torch.from_numpy(np.flatnonzero(synthetic.sparse_q_layout(nk, 4096, seed=0))).to(dev)
+    absolute = torch.arange(nk, device=dev)
+    for _ in range(max(1, args.steps // 2)):
+        S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, out_index=absolute)
     torch.cuda.synchronize()
-    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select)")
+    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select), sparse_q")
     return 0
 
 

@@ -63,3 +63,28 @@ def block_slots(block_ids: torch.Tensor, block_size: int, tokens: int) -> torch.
     (the connector's slot mapping, reference connector.py:42-45)."""
     offsets = torch.arange(block_size, dtype=torch.long)
     return (block_ids.long()[:, None] * block_size + offsets[None, :]).reshape(-1)[:tokens]
+
+
+def sparse_q_layout(context: int, queries: int, seed: int, max_gap: int = 511,
+                    hit_chunk: int = 256) -> np.ndarray:
+    """Boolean query (gap) mask over ``context`` tokens holding exactly
+    ``queries`` gap tokens in runs of 1..max_gap, separated by hit runs of
+    ``hit_chunk`` multiples, the last run ending at the last token."""
+    rng = np.random.default_rng(seed)
+    runs = []
+    left = queries
+    while left > 0:
+        g = min(left, int(rng.integers(1, max_gap + 1)))
+        runs.append(g)
+        left -= g
+    hit_chunks = (context - queries) // hit_chunk
+    extra = context - queries - hit_chunks * hit_chunk
+    split = rng.multinomial(hit_chunks, np.full(len(runs), 1.0 / len(runs)))
+    mask = np.zeros(context, dtype=bool)
+    pos = extra
+    for g, h in zip(runs, split):
+        pos += int(h) * hit_chunk
+        mask[pos: pos + g] = True
+        pos += g
+    assert pos == context and int(mask.sum()) == queries
+    return mask

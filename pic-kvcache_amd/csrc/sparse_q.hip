@@ -97,18 +97,113 @@ __device__ __forceinline__ f32x4 mfma16<h16x8>(const h16x8& a, const h16x8& b, c
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Rounds the logits of one MFMA row group to the input dtype, two at a time
+// for bf16 (v_cvt_pk_bf16_f32), as a bf16/f16 matmul output would be.
+template <int RMODE>
+__device__ __forceinline__ void round_pair(float& x, float& y) {
+  if constexpr (RMODE == 1) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 r = __builtin_convertvector((f2){x, y}, b2);
+    const uint32_t u = __builtin_bit_cast(uint32_t, r);
+    x = __uint_as_float(u << 16);
+    y = __uint_as_float(u & 0xffff0000u);
+  } else if constexpr (RMODE == 2) {
+    x = __half2float(__float2half(x));
+    y = __half2float(__float2half(y));
+  }
+}
+
 // ------------------------------------------------------------ rowstats
 
-template <typename V, int KSTEPS>
+template <int PIECES, int D>
+__device__ __forceinline__ void load_key_block(const SqArgs& a, uint32_t g, int32_t k0, u32x4 (&pre)[PIECES]) {
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    const uint32_t kr = idx / (D / 8), piece = idx % (D / 8);
+    const int32_t key = k0 + int32_t(kr);
+    pre[p] = u32x4(0);
+    if (key < int32_t(a.nk))
+      pre[p] = *reinterpret_cast<const u32x4*>(
+          a.k + ((int64_t(key) * a.k_stride) + int64_t(g) * a.d + piece * 8) * 2);
+  }
+}
+
+template <int PIECES, int D, int LROW>
+__device__ __forceinline__ void store_block(uint16_t* lds, const u32x4 (&pre)[PIECES]) {
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    const uint32_t kr = idx / (D / 8), piece = idx % (D / 8);
+    *reinterpret_cast<u32x4*>(&lds[kr * LROW + piece * 8]) = pre[p];
+  }
+}
+
+// One 64-key block against MAXT row tiles: MFMA, round, (mask), online stats.
+template <typename V, int KSTEPS, int MAXT, int RMODE, bool MASK>
+__device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* blk, int32_t k0,
+                                               const V (&afrag)[MAXT][KSTEPS], int ntiles_w,
+                                               const int32_t (&rpos)[4], float (&m)[MAXT][4],
+                                               float (&l)[MAXT][4], uint32_t col, uint32_t rgrp) {
+  constexpr int LROW = 32 * KSTEPS + 8;
+  V bfrag[kColTiles][KSTEPS];
+#pragma unroll
+  for (int c = 0; c < kColTiles; ++c)
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      bfrag[c][s] = *reinterpret_cast<const V*>(&blk[(c * 16 + col) * LROW + 32 * s + 8 * rgrp]);
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    if (t >= ntiles_w) break;
+    f32x4 acc[kColTiles];
+#pragma unroll
+    for (int c = 0; c < kColTiles; ++c) {
+      acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) acc[c] = mfma16<V>(afrag[t][s], bfrag[c][s], acc[c]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float r[kColTiles];
+#pragma unroll
+      for (int c = 0; c < kColTiles; c += 2) {
+        r[c] = acc[c][i];
+        r[c + 1] = acc[c + 1][i];
+        round_pair<RMODE>(r[c], r[c + 1]);
+      }
+      if constexpr (MASK) {
+#pragma unroll
+        for (int c = 0; c < kColTiles; ++c) {
+          const int32_t key = k0 + c * 16 + int32_t(col);
+          if (key > rpos[i] || key >= int32_t(a.nk)) r[c] = kNegInf;
+        }
+      }
+      // max on raw logits (scale > 0 preserves order), one multiply per row
+      const float bm = fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3])) * a.c2;
+      const float mn = fmaxf(m[t][i], bm);
+      const float ms = mn == kNegInf ? 0.f : mn;
+      float sum = 0.f;
+#pragma unroll
+      for (int c = 0; c < kColTiles; ++c) sum += __builtin_amdgcn_exp2f(fmaf(r[c], a.c2, -ms));
+      l[t][i] = fmaf(l[t][i], __builtin_amdgcn_exp2f(m[t][i] - ms), sum);
+      m[t][i] = mn;
+    }
+  }
+}
+
+template <typename V, int KSTEPS, int MAXT, int RMODE>
 __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr int LROW = D + 8;  // padded LDS row (elements) against bank conflicts
-  constexpr int MAXT = 4;      // row tiles (heads) per wave: G <= 16
-  __shared__ __attribute__((aligned(16))) uint16_t kblk[kKeyBlock1 * LROW];
+  constexpr int PIECES = kKeyBlock1 * (D / 8) / kThreads;
+  __shared__ __attribute__((aligned(16))) uint16_t kblk[2][kKeyBlock1 * LROW];
   __shared__ int32_t s_pos[kQTile];
   __shared__ int32_t s_minmax[2];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t qt = blockIdx.x, g = blockIdx.y;
+  const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
+  const uint32_t qt = ntiles - 1 - blockIdx.x;  // latest positions (most keys) first
+  const uint32_t g = blockIdx.y;
   const uint32_t q0 = qt * kQTile;
   if (threadIdx.x < kQTile) s_pos[threadIdx.x] = query_pos(a, q0 + threadIdx.x);
   __syncthreads();
@@ -133,81 +228,42 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
   int32_t rpos[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) rpos[i] = s_pos[4 * rgrp + i];
-  const uint32_t qi = q0 + col;  // A row of this lane
-  const uint32_t es = sizeof(uint16_t);
+  const uint32_t qi = q0 + col;
 
   V afrag[MAXT][KSTEPS];
   float m[MAXT][4], l[MAXT][4];
-  const uint32_t ntiles_w = (a.groups > wave) ? (a.groups - wave + 3) / 4 : 0;
+  const int ntiles_w = (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
-    if (t < int(ntiles_w)) {
-      const uint32_t h = g * a.groups + wave + 4 * t;
-      const char* row = qi < a.nq ? query_row(a, qi, h, es) : nullptr;
+    const char* row = (t < ntiles_w && qi < a.nq)
+                          ? query_row(a, qi, g * a.groups + wave + 4 * t, 2) : nullptr;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        if (row) {
-          afrag[t][s] = *reinterpret_cast<const V*>(row + (32 * s + 8 * rgrp) * es);
-        } else {
-          afrag[t][s] = V(0);
-        }
-      }
-    }
+    for (int s = 0; s < KSTEPS; ++s)
+      afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (32 * s + 8 * rgrp) * 2) : V(0);
   }
   const int32_t nkb = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
+  u32x4 pre[PIECES];
+  if (nkb > 0) {
+    load_key_block<PIECES, D>(a, g, 0, pre);
+    store_block<PIECES, D, LROW>(kblk[0], pre);
+  }
   for (int32_t kb = 0; kb < nkb; ++kb) {
     const int32_t k0 = kb * kKeyBlock1;
+    if (kb + 1 < nkb) load_key_block<PIECES, D>(a, g, k0 + kKeyBlock1, pre);  // in flight
     __syncthreads();
-    // stage 64 keys x D of kv head g: 16-byte pieces
-    for (uint32_t p = threadIdx.x; p < kKeyBlock1 * (D / 8); p += kThreads) {
-      const uint32_t kr = p / (D / 8), piece = p % (D / 8);
-      const int32_t key = k0 + int32_t(kr);
-      u32x4 v = u32x4(0);
-      if (key < int32_t(a.nk))
-        v = *reinterpret_cast<const u32x4*>(a.k + ((int64_t(key) * a.k_stride) + int64_t(g) * a.d + piece * 8) * es);
-      *reinterpret_cast<u32x4*>(&kblk[kr * LROW + piece * 8]) = v;
-    }
-    __syncthreads();
-    const bool need_mask = (k0 + kKeyBlock1 - 1 > minpos) || (k0 + kKeyBlock1 > int32_t(a.nk));
-#pragma unroll
-    for (int t = 0; t < MAXT; ++t) {
-      if (t >= int(ntiles_w)) break;
-      float x[kColTiles][4];
-#pragma unroll
-      for (int c = 0; c < kColTiles; ++c) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-          const V b = *reinterpret_cast<const V*>(&kblk[(c * 16 + col) * LROW + 32 * s + 8 * rgrp]);
-          acc = mfma16<V>(afrag[t][s], b, acc);
-        }
-        const int32_t key = k0 + c * 16 + int32_t(col);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = round_logit(acc[i], a.round_mode) * a.c2;
-          if (need_mask && (key > rpos[i] || key >= int32_t(a.nk))) v = kNegInf;
-          x[c][i] = v;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float bm = fmaxf(fmaxf(x[0][i], x[1][i]), fmaxf(x[2][i], x[3][i]));
-        const float mn = fmaxf(m[t][i], bm);
-        const float ms = mn == kNegInf ? 0.f : mn;
-        float sum = 0.f;
-#pragma unroll
-        for (int c = 0; c < kColTiles; ++c) sum += __builtin_amdgcn_exp2f(x[c][i] - ms);
-        l[t][i] = l[t][i] * __builtin_amdgcn_exp2f(m[t][i] - ms) + sum;
-        m[t][i] = mn;
-      }
-    }
+    const uint16_t* blk = kblk[kb & 1];
+    if (k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk))
+      rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+    else
+      rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+    if (kb + 1 < nkb) store_block<PIECES, D, LROW>(kblk[(kb + 1) & 1], pre);
   }
   // merge the 16 lanes that hold the same rows, then publish (m2, 1/l)
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    if (t >= int(ntiles_w)) break;
+    if (t >= ntiles_w) break;
     const uint32_t h = g * a.groups + wave + 4 * t;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -226,94 +282,158 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 
 // -------------------------------------------------------------- colsum
 
-template <typename V, int KSTEPS>
+constexpr int kHeadChunk = 4;  // query heads staged per LDS buffer
+
+template <int PIECES, int D>
+__device__ __forceinline__ void load_q_unit(const SqArgs& a, uint32_t g, uint32_t q0, uint32_t h0,
+                                            uint32_t nh, u32x4 (&pre)[PIECES]) {
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    const uint32_t hl = idx / (kQTile * (D / 8));
+    const uint32_t rem = idx % (kQTile * (D / 8));
+    const uint32_t r = rem / (D / 8), piece = rem % (D / 8);
+    pre[p] = u32x4(0);
+    if (hl < nh && q0 + r < a.nq)
+      pre[p] = *reinterpret_cast<const u32x4*>(query_row(a, q0 + r, g * a.groups + h0 + hl, 2) + piece * 16);
+  }
+}
+
+template <int PIECES, int D, int LROW>
+__device__ __forceinline__ void store_q_unit(uint16_t* lds, const u32x4 (&pre)[PIECES]) {
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    const uint32_t hl = idx / (kQTile * (D / 8));
+    const uint32_t rem = idx % (kQTile * (D / 8));
+    const uint32_t r = rem / (D / 8), piece = rem % (D / 8);
+    *reinterpret_cast<u32x4*>(&lds[(hl * kQTile + r) * LROW + piece * 8]) = pre[p];
+  }
+}
+
+template <typename V, int KSTEPS, int RMODE, bool MASK>
+__device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2 (*st)[kQTile],
+                                            uint32_t nh, int32_t kw0, const int32_t (&rpos)[4],
+                                            const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
+                                            uint32_t col, uint32_t rgrp) {
+  constexpr int LROW = 32 * KSTEPS + 8;
+  for (uint32_t hl = 0; hl < nh; ++hl) {
+    V afrag[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      afrag[s] = *reinterpret_cast<const V*>(&qlds[(hl * kQTile + col) * LROW + 32 * s + 8 * rgrp]);
+    float mrow[4], irow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float2 v = st[hl][4 * rgrp + i];
+      mrow[i] = v.x;
+      irow[i] = v.y;
+    }
+#pragma unroll
+    for (int c = 0; c < kColTiles; ++c) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) acc = mfma16<V>(afrag[s], bfrag[c][s], acc);
+      float r[4] = {acc[0], acc[1], acc[2], acc[3]};
+      round_pair<RMODE>(r[0], r[1]);
+      round_pair<RMODE>(r[2], r[3]);
+      const int32_t key = kw0 + c * 16 + int32_t(col);
+      float sum = acc_col[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i])) * irow[i];
+        if constexpr (MASK) p = key > rpos[i] ? 0.f : p;
+        sum += p;
+      }
+      acc_col[c] = sum;
+    }
+  }
+}
+
+template <typename V, int KSTEPS, int RMODE>
 __global__ __launch_bounds__(kThreads) void sq_colsum_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr int LROW = D + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t qblk[kMaxHeadsInLds * kQTile * LROW];
-  __shared__ float2 s_stats[kMaxHeadsInLds][kQTile];
-  __shared__ int32_t s_pos[kQTile];
+  constexpr int PIECES = kHeadChunk * kQTile * (D / 8) / kThreads;
+  __shared__ __attribute__((aligned(16))) uint16_t qblk[2][kHeadChunk * kQTile * LROW];
+  __shared__ float2 s_stats[2][kHeadChunk][kQTile];
+  __shared__ int32_t s_pos[2][kQTile];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t g = blockIdx.y;
   const int32_t kw0 = int32_t(blockIdx.x) * kKeyBlock2 + int32_t(wave) * 16 * kColTiles;
   const int32_t kb0 = int32_t(blockIdx.x) * kKeyBlock2;
   const uint32_t col = lane & 15, rgrp = lane >> 4;
-  const uint32_t es = sizeof(uint16_t);
 
   V bfrag[kColTiles][KSTEPS];
 #pragma unroll
   for (int c = 0; c < kColTiles; ++c) {
     const int32_t key = kw0 + c * 16 + int32_t(col);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      if (key < int32_t(a.nk)) {
-        bfrag[c][s] = *reinterpret_cast<const V*>(
-            a.k + ((int64_t(key) * a.k_stride) + int64_t(g) * a.d + 32 * s + 8 * rgrp) * es);
-      } else {
-        bfrag[c][s] = V(0);
-      }
-    }
+    for (int s = 0; s < KSTEPS; ++s)
+      bfrag[c][s] = key < int32_t(a.nk)
+                        ? *reinterpret_cast<const V*>(a.k + ((int64_t(key) * a.k_stride) + int64_t(g) * a.d +
+                                                             32 * s + 8 * rgrp) * 2)
+                        : V(0);
   }
   float acc_col[kColTiles];
 #pragma unroll
   for (int c = 0; c < kColTiles; ++c) acc_col[c] = 0.f;
 
+  // units (query tile, head chunk) whose tile sees at least one key of the block
   const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
-  for (uint32_t qt = 0; qt < ntiles; ++qt) {
-    const int32_t tmax = a.tile_pos[2 * qt + 1];
-    if (tmax < kb0) continue;  // no query of the tile sees any key of the block
-    const int32_t tmin = a.tile_pos[2 * qt];
-    const uint32_t q0 = qt * kQTile;
-    for (uint32_t h0 = 0; h0 < a.groups; h0 += kMaxHeadsInLds) {
-      const uint32_t nh = min(uint32_t(kMaxHeadsInLds), a.groups - h0);
-      __syncthreads();
-      for (uint32_t p = threadIdx.x; p < nh * kQTile * (D / 8); p += kThreads) {
-        const uint32_t hl = p / (kQTile * (D / 8));
-        const uint32_t rem = p % (kQTile * (D / 8));
-        const uint32_t r = rem / (D / 8), piece = rem % (D / 8);
-        u32x4 v = u32x4(0);
-        if (q0 + r < a.nq)
-          v = *reinterpret_cast<const u32x4*>(query_row(a, q0 + r, g * a.groups + h0 + hl, es) + piece * 8 * es);
-        *reinterpret_cast<u32x4*>(&qblk[(hl * kQTile + r) * LROW + piece * 8]) = v;
-      }
-      for (uint32_t p = threadIdx.x; p < nh * kQTile; p += kThreads) {
-        const uint32_t hl = p / kQTile, r = p % kQTile;
-        s_stats[hl][r] = (q0 + r < a.nq) ? a.stats[int64_t(g * a.groups + h0 + hl) * a.nq_pad + q0 + r]
-                                         : make_float2(0.f, 0.f);
-      }
-      if (threadIdx.x < kQTile) s_pos[threadIdx.x] = query_pos(a, q0 + threadIdx.x);
-      __syncthreads();
-      if (tmax < kw0) continue;  // this wave's keys are all after the tile's queries
+  const uint32_t nchunks = (a.groups + kHeadChunk - 1) / kHeadChunk;
+  auto next_tile = [&](uint32_t qt) {
+    while (qt < ntiles && a.tile_pos[2 * qt + 1] < kb0) ++qt;
+    return qt;
+  };
+  uint32_t qt = next_tile(0), hc = 0;
+  u32x4 pre[PIECES];
+  float2 pre_st = make_float2(0.f, 0.f);
+  int32_t pre_pos = -1;
+  auto fetch = [&](uint32_t t, uint32_t c) {
+    const uint32_t h0 = c * kHeadChunk, nh = min(uint32_t(kHeadChunk), a.groups - h0);
+    load_q_unit<PIECES, D>(a, g, t * kQTile, h0, nh, pre);
+    if (threadIdx.x < kHeadChunk * kQTile) {
+      const uint32_t hl = threadIdx.x / kQTile, r = threadIdx.x % kQTile;
+      const uint32_t q = t * kQTile + r;
+      pre_st = (hl < nh && q < a.nq) ? a.stats[int64_t(g * a.groups + h0 + hl) * a.nq_pad + q]
+                                     : make_float2(0.f, 0.f);
+    }
+    if (threadIdx.x < kQTile) pre_pos = query_pos(a, t * kQTile + threadIdx.x);
+  };
+  auto commit = [&](int buf) {
+    store_q_unit<PIECES, D, LROW>(qblk[buf], pre);
+    if (threadIdx.x < kHeadChunk * kQTile) s_stats[buf][threadIdx.x / kQTile][threadIdx.x % kQTile] = pre_st;
+    if (threadIdx.x < kQTile) s_pos[buf][threadIdx.x] = pre_pos;
+  };
+  if (qt < ntiles) {
+    fetch(qt, hc);
+    commit(0);
+  }
+  for (int it = 0; qt < ntiles; ++it) {
+    // the unit after (qt, hc)
+    uint32_t nqt = qt, nhc = hc + 1;
+    if (nhc == nchunks) {
+      nhc = 0;
+      nqt = next_tile(qt + 1);
+    }
+    if (nqt < ntiles) fetch(nqt, nhc);  // in flight during the compute below
+    __syncthreads();
+    const int buf = it & 1;
+    const int32_t tmax = a.tile_pos[2 * qt + 1], tmin = a.tile_pos[2 * qt];
+    if (tmax >= kw0) {
       int32_t rpos[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rpos[i] = s_pos[4 * rgrp + i];
-      const bool need_mask = (kw0 + 16 * kColTiles - 1 > tmin) || (q0 + kQTile > a.nq);
-      for (uint32_t hl = 0; hl < nh; ++hl) {
-        V afrag[KSTEPS];
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-          afrag[s] = *reinterpret_cast<const V*>(&qblk[(hl * kQTile + col) * LROW + 32 * s + 8 * rgrp]);
-        float2 st[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[i] = s_stats[hl][4 * rgrp + i];
-#pragma unroll
-        for (int c = 0; c < kColTiles; ++c) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int s = 0; s < KSTEPS; ++s) acc = mfma16<V>(afrag[s], bfrag[c][s], acc);
-          const int32_t key = kw0 + c * 16 + int32_t(col);
-          float sum = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x = round_logit(acc[i], a.round_mode) * a.c2;
-            float p = __builtin_amdgcn_exp2f(x - st[i].x) * st[i].y;
-            if (need_mask && key > rpos[i]) p = 0.f;
-            sum += p;
-          }
-          acc_col[c] += sum;
-        }
-      }
+      for (int i = 0; i < 4; ++i) rpos[i] = s_pos[buf][4 * rgrp + i];
+      const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
+      if (kw0 + 16 * kColTiles - 1 > tmin || qt * kQTile + kQTile > a.nq)
+        colsum_unit<V, KSTEPS, RMODE, true>(a, qblk[buf], s_stats[buf], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+      else
+        colsum_unit<V, KSTEPS, RMODE, false>(a, qblk[buf], s_stats[buf], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
     }
+    if (nqt < ntiles) commit(buf ^ 1);
+    qt = nqt;
+    hc = nhc;
   }
   // column totals: the 4 lane groups hold the same column
 #pragma unroll
@@ -415,19 +535,26 @@ __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   return L;
 }
 
-template <typename V>
-int launch_mfma(const SqArgs& a, int ksteps, hipStream_t stream) {
+template <typename V, int RMODE, int KS>
+void launch_mfma_ks(const SqArgs& a, hipStream_t stream) {
   const dim3 g1((a.nq + kQTile - 1) / kQTile, a.hkv);
   const dim3 g2((a.nk + kKeyBlock2 - 1) / kKeyBlock2, a.hkv);
-#define CBK_SQ(KS)                                                                        \
-  hipLaunchKernelGGL((sq_rowstats_kernel<V, KS>), g1, dim3(kThreads), 0, stream, a);     \
-  hipLaunchKernelGGL((sq_colsum_kernel<V, KS>), g2, dim3(kThreads), 0, stream, a)
+  if (a.groups <= 4)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups <= 8)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE>), g1, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE>), g1, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE>), g2, dim3(kThreads), 0, stream, a);
+}
+
+template <typename V, int RMODE>
+int launch_mfma(const SqArgs& a, int ksteps, hipStream_t stream) {
   switch (ksteps) {
-    case 2: CBK_SQ(2); break;
-    case 4: CBK_SQ(4); break;
+    case 2: launch_mfma_ks<V, RMODE, 2>(a, stream); break;
+    case 4: launch_mfma_ks<V, RMODE, 4>(a, stream); break;
     default: return set_error(CBK_ERR_UNSUPPORTED, "head_dim %u", a.d);
   }
-#undef CBK_SQ
   return launch_status("sparse_q mfma");
 }
 
@@ -505,8 +632,12 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
                     (reinterpret_cast<uintptr_t>(q_dev) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(k_dev) & 15) == 0,
                 "q/k rows must be 16-byte aligned");
+    CBK_REQUIRE(round_logits == (dtype == CBK_DTYPE_BF16 ? 1 : 2),
+                "the MFMA path rounds logits to the input dtype (round_logits %d)",
+                dtype == CBK_DTYPE_BF16 ? 1 : 2);
+    CBK_REQUIRE(scale > 0.f, "scale must be positive");
     const int ks = int(head_dim / 32);
-    int rc = dtype == CBK_DTYPE_BF16 ? launch_mfma<s16x8>(a, ks, s) : launch_mfma<h16x8>(a, ks, s);
+    int rc = dtype == CBK_DTYPE_BF16 ? launch_mfma<s16x8, 1>(a, ks, s) : launch_mfma<h16x8, 2>(a, ks, s);
     if (rc) return rc;
   }
   if (int rc = launch_status("sparse_q")) return rc;
