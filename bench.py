@@ -303,49 +303,77 @@ def sparse_q(torch, S, synthetic, dev):
 
 def store_pipeline(torch, layers, cache, src_slots, args):
     """Qwen3-8B layerwise store: save_kv_layer for all 36 layers of the
-    8192-token prompt (32 chunks of 256) through the Store stream -- gather
-    into reused device staging, pinned D2H, publication into the host store
-    -- timed from the first save to the end of wait_for_save."""
-    from cacheblend_vllm.host_store import PinnedChunkStore
+    8192-token prompt (32 chunks of 256) through the Store stream, timed from
+    the first save to the end of wait_for_save, in two modes:
+    fused  -- one kernel per layer gathers the pages straight into pinned
+              chunk slots of a warm slab (the GPU writes host memory);
+    staged -- gather into reused device staging, then a pinned D2H copy.
+    Both include publication of every chunk into the host store."""
+    from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
     from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
 
     L = len(layers)
     T = src_slots.numel()
     slots_cpu = src_slots.cpu()
-    row_bytes = cache.row_shape[0] * cache.row_shape[1] * 2
-    nbytes = L * 2 * T * row_bytes
-    times = []
-    for rep in range(3):
-        store = PinnedChunkStore(256, 1 << 40)
-        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2)
-        request = RequestMetadata(f"r{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None, True, T)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for l in range(L):
-            writer.save_layer(l, layers[l], [request])
-        writer.wait_for_save()
-        times.append(time.perf_counter() - t0)
-        committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
-        writer.close()
-        del store, writer
-    best = min(times)
-    return {"layers": L, "tokens": T, "chunks_committed": committed, "bytes_d2h": nbytes,
-            "ms": round(best * 1e3, 3), "d2h_GBps": round(nbytes / best / 1e9, 2),
-            "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4),
-            "includes": "gather kernels + pinned D2H + host publication, first save to wait_for_save"}
+    H, D = cache.row_shape
+    nbytes = L * 2 * T * H * D * 2
+    slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=128)
+    result = {"layers": L, "tokens": T, "bytes_d2h": nbytes}
+    for mode in ("fused", "staged"):
+        times = []
+        for rep in range(4):
+            store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if mode == "fused" else None)
+            writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2,
+                                       slab=slab if mode == "fused" else None)
+            request = RequestMetadata(f"{mode}{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None,
+                                      True, T)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for l in range(L):
+                writer.save_layer(l, layers[l], [request])
+            writer.wait_for_save()
+            times.append(time.perf_counter() - t0)
+            committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
+            writer.close()
+            store.clear()
+            del store, writer
+        best = min(times[1:])  # rep 0 also pins the slab's arenas / warms the pools
+        result[mode] = {"ms": round(best * 1e3, 3), "first_rep_ms": round(times[0] * 1e3, 3),
+                        "chunks_committed": committed, "d2h_GBps": round(nbytes / best / 1e9, 2),
+                        "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4)}
+    result["slab"] = slab.stats()
+    slab.close()
+    return result
+
+
+def _sleep_cycles_per_us(torch) -> float:
+    """Clock rate of torch.cuda._sleep's spin kernel, measured."""
+    torch.cuda._sleep(1000)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(20_000_000)
+    e1.record()
+    e1.synchronize()
+    return 20_000_000 / (e0.elapsed_time(e1) * 1e3)
 
 
 def blend_load(torch, synthetic, dev, args):
     """Qwen3-30B-A3B blend load: 48 layers, 4 KV heads x 128 bf16, 16-token
     blocks; 32768-token prompt, 2048-token APC prefix, 12 reused segments of
-    256-multiples separated by 1-511-token gaps (allocation_end 32767). Per
-    layer: H2D of the hit chunks (pinned, coalesced), fused assembly with RoPE
-    relocation, commit scatter into the pages; run alone and overlapped with
-    a synthetic per-layer compute (bf16 GEMMs) on the serving stream."""
+    256-multiples separated by 1-511-token gaps (allocation_end 32767). The
+    hit chunks of each layer live in one pinned [2, hit, 4, 128] host tensor.
+    Per layer: hits cross the host link, the fused assembly relocates RoPE,
+    the commit scatters into the pages. Timed alone and overlapped with a
+    per-layer compute on the serving stream of 1.5x the per-layer load time,
+    either a busy-wait (one spinning wave) or bf16 GEMMs (every CU busy).
+    Both transfer modes are timed -- DMA of the coalesced runs (what "auto"
+    picks here) and in-place host reads -- and, for chunks scattered over
+    pinned slab slots (what the fused store produces), the "auto" choice."""
     import numpy as np
 
     from cacheblend_vllm.config import CacheBlendConfig
-    from cacheblend_vllm.host_store import PinnedChunkStore
+    from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
     from cacheblend_vllm.loader import PagedBlendLoader
     from cacheblend_vllm.types import BlendPlan, BlendSegment
 
@@ -363,21 +391,30 @@ def blend_load(torch, synthetic, dev, args):
     hit = sum(n for _, _, n in segs)
     nb = (A + BS - 1) // BS + 8
     layers = [synthetic.paged_pool(nb, BS, H, D, torch.bfloat16, dev, seed=100 + l) for l in range(L)]
-    store = PinnedChunkStore(256, 1 << 40)
-    blend_segments = []
-    host_runs = []
-    for i, (s0, t0, n) in enumerate(segs):
-        runs = [torch.empty((2, n, H, D), dtype=torch.bfloat16, pin_memory=True) for _ in range(L)]
-        for r in runs:
-            r.copy_(torch.randn(r.shape, device=dev, dtype=torch.bfloat16))
-        host_runs.append(runs)
-        for c in range(0, n, 256):
-            sid = store.begin_put("bench", s0 + c, list(range(s0 + c + 7 * i, s0 + c + 7 * i + 256)), L)
-            for l in range(L):
-                store.put_layer_host(sid, l, runs[l][:, c : c + 256])
-            blend_segments.append(BlendSegment(sid, t0 + c))
-    store.pin("blend", blend_segments)
-    plan = BlendPlan(APC, A, hit, tuple(blend_segments))
+    hosts = [torch.empty((2, hit, H, D), dtype=torch.bfloat16, pin_memory=True) for _ in range(L)]
+    for h in hosts:
+        h.copy_(torch.randn(h.shape, device=dev, dtype=torch.bfloat16))
+    slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=256)
+
+    def make_store(fragmented):
+        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if fragmented else None)
+        blend_segments = []
+        off = 0
+        for i, (s0, t0, n) in enumerate(segs):
+            for c in range(0, n, 256):
+                sid = store.begin_put("bench", s0 + c, list(range(s0 + c + 7 * i, s0 + c + 7 * i + 256)), L)
+                for l in range(L):
+                    view = hosts[l][:, off + c : off + c + 256]
+                    if fragmented:
+                        slot = slab.alloc()
+                        slot.copy_(view)
+                        view = slot
+                    store.put_layer_host(sid, l, view)
+                blend_segments.append(BlendSegment(sid, t0 + c))
+            off += n
+        store.pin("blend", blend_segments)
+        return store, BlendPlan(APC, A, hit, tuple(blend_segments))
+
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
     slots = synthetic.block_slots(perm[: (A + BS - 1) // BS], BS, A)
 
@@ -393,8 +430,9 @@ def blend_load(torch, synthetic, dev, args):
     load_stream = torch.cuda.Stream()
     h2d_bytes = L * hit * 2 * H * D * 2
 
-    def run(compute=None):
-        loader = PagedBlendLoader(layers, store, "blend", plan, slots, BS, cfg, load_stream=load_stream)
+    def run(store, plan, zero_copy, compute=None):
+        loader = PagedBlendLoader(layers, store, "blend", plan, slots, BS, cfg, load_stream=load_stream,
+                                  zero_copy=zero_copy)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         loader.prefetch(0, rope)
@@ -405,11 +443,25 @@ def blend_load(torch, synthetic, dev, args):
                 compute()
             loader.commit(l, buf)
         torch.cuda.synchronize()
-        return time.perf_counter() - t0
+        return time.perf_counter() - t0, len(loader._zc_layers) == L
 
-    run()
-    load_only = min(run() for _ in range(2))
-    # per-layer compute of about 1.5x one layer's load time
+    def best(store, plan, zero_copy, compute=None, reps=2):
+        run(store, plan, zero_copy, compute)
+        results = [run(store, plan, zero_copy, compute) for _ in range(reps)]
+        return min(r[0] for r in results), results[0][1]
+
+    contiguous, plan_c = make_store(False)
+    dma_s, dma_host_read = best(contiguous, plan_c, "auto")
+    read_s, _ = best(contiguous, plan_c, True)
+    assert not dma_host_read
+    per_layer = dma_s / L
+
+    cycles_per_us = _sleep_cycles_per_us(torch)
+    delay_cycles = int(1.5 * per_layer * 1e6 * cycles_per_us)
+
+    def busy():
+        torch.cuda._sleep(delay_cycles)
+
     a = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
     b = torch.randn(4096, 4096, device=dev, dtype=torch.bfloat16)
     c = torch.empty(4096, 4096, device=dev, dtype=torch.bfloat16)
@@ -419,33 +471,57 @@ def blend_load(torch, synthetic, dev, args):
     for _ in range(20):
         torch.mm(a, b, out=c)
     torch.cuda.synchronize()
-    gemm_s = (time.perf_counter() - t0) / 20
-    reps = max(1, int(round(1.5 * load_only / L / gemm_s)))
+    reps = max(1, int(round(1.5 * per_layer / ((time.perf_counter() - t0) / 20))))
 
-    def compute():
+    def gemms():
         for _ in range(reps):
             torch.mm(a, b, out=c)
 
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(L):
-        compute()
-    torch.cuda.synchronize()
-    compute_only = time.perf_counter() - t0
-    overlapped = min(run(compute) for _ in range(2))
-    hidden = 1.0 - max(0.0, overlapped - compute_only) / load_only
-    store.release("blend")
-    return {
-        "layers": L, "allocation_end": A, "apc_prefix": APC, "hit_tokens": hit,
-        "segments": len(segs), "h2d_bytes": h2d_bytes,
-        "load_only_ms": round(load_only * 1e3, 3),
-        "h2d_GBps_load_only": round(h2d_bytes / load_only / 1e9, 2),
-        "host_link_frac": round(h2d_bytes / load_only / 1e9 / HOST_LINK_PEAK_GBPS, 4),
-        "compute_only_ms": round(compute_only * 1e3, 3),
-        "overlapped_ms": round(overlapped * 1e3, 3),
-        "load_hidden_frac": round(hidden, 4),
-        "compute_per_layer": f"{reps} x bf16 GEMM 4096^3",
+    def alone(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(L):
+            fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    def overlap(load_s, total_s, compute_s):
+        return {"overlapped_ms": round(total_s * 1e3, 3), "compute_only_ms": round(compute_s * 1e3, 3),
+                "load_hidden_frac": round(1.0 - max(0.0, total_s - compute_s) / load_s, 4),
+                "h2d_GBps_while_hidden": round(h2d_bytes / max(total_s, 1e-9) / 1e9, 2)}
+
+    busy_s, gemm_s = alone(busy), alone(gemms)
+    out = {
+        "layers": L, "allocation_end": A, "apc_prefix": APC, "hit_tokens": hit, "segments": len(segs),
+        "h2d_bytes": h2d_bytes,
+        "dma": {"load_only_ms": round(dma_s * 1e3, 3), "h2d_GBps": round(h2d_bytes / dma_s / 1e9, 2),
+                "host_link_frac": round(h2d_bytes / dma_s / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+                "busy_wait": overlap(dma_s, best(contiguous, plan_c, "auto", busy)[0], busy_s),
+                "gemm": overlap(dma_s, best(contiguous, plan_c, "auto", gemms)[0], gemm_s)},
+        "host_read": {"load_only_ms": round(read_s * 1e3, 3), "h2d_GBps": round(h2d_bytes / read_s / 1e9, 2),
+                      "host_link_frac": round(h2d_bytes / read_s / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+                      "busy_wait": overlap(read_s, best(contiguous, plan_c, True, busy)[0], busy_s),
+                      "gemm": overlap(read_s, best(contiguous, plan_c, True, gemms)[0], gemm_s)},
+        "compute_per_layer": {"busy_wait_us": round(1.5 * per_layer * 1e6, 1),
+                              "gemm": f"{reps} x bf16 GEMM 4096^3"},
     }
+    contiguous.release("blend")
+    del contiguous
+    fragmented, plan_f = make_store(True)
+    frag_s, frag_host_read = best(fragmented, plan_f, "auto")
+    frag_dma_s, _ = best(fragmented, plan_f, False)
+    out["slab_chunks"] = {
+        "auto_mode": "host_read" if frag_host_read else "dma",
+        "load_only_ms": round(frag_s * 1e3, 3), "h2d_GBps": round(h2d_bytes / frag_s / 1e9, 2),
+        "host_link_frac": round(h2d_bytes / frag_s / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+        "dma_per_chunk_GBps": round(h2d_bytes / frag_dma_s / 1e9, 2),
+        "busy_wait": overlap(frag_s, best(fragmented, plan_f, "auto", busy)[0], busy_s),
+    }
+    fragmented.release("blend")
+    fragmented.clear()
+    slab.close()
+    return out
 
 
 def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev):

@@ -102,6 +102,56 @@ int cbk_paged_scatter_layers(const void* in_dev, int64_t in_layer_stride, int64_
                              cbk_stream_t stream);
 
 /*
+ * Gather straight into host chunks (the fused store path): token t of the
+ * batch is written to chunk c = t / chunk_tokens, row r = t % chunk_tokens,
+ * i.e. to chunk_k[c] + r * chunk_token_stride (K plane) and chunk_v[c] + ...
+ * (V plane). chunk_k / chunk_v are HOST arrays of ceil(num_tokens /
+ * chunk_tokens) device-addressable destinations (pinned host memory from
+ * cbk_slab_alloc or hipHostMalloc, 16-byte aligned). A grid of at most
+ * max_workgroups workgroups (<= 0: 64) strides over the batch: the copy is
+ * host-link bound and leaves the other CUs free.
+ * Replaces _enqueue_store_batch's gather + pinned D2H pair and the
+ * per-layer pinned batch (cacheblend_vllm/connector.py:401-429).
+ */
+int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                            int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
+                            int64_t chunk_token_stride, int32_t max_workgroups,
+                            int32_t* bad_slots_dev, cbk_stream_t stream);
+
+/*
+ * Pinned host chunk slab: fixed-size, 256-byte aligned slots carved from
+ * pinned, coherent host arenas (hipHostMalloc) of chunks_per_arena slots,
+ * recycled through a free list; max_bytes 0 = unbounded. Thread-safe.
+ * Replaces the per-layer torch pinned allocation of the reference store path
+ * (cacheblend_vllm/connector.py:421-426); slots hold the store's
+ * [2, chunk, H, D] chunk format (connector.py:449-466).
+ */
+int cbk_slab_create(size_t chunk_bytes, size_t chunks_per_arena, size_t max_bytes, void** out_handle);
+int cbk_slab_alloc(void* handle, void** out_chunk);
+int cbk_slab_free(void* handle, void* chunk);
+int cbk_slab_stats(void* handle, size_t* arenas, size_t* free_chunks, size_t* live_chunks);
+int cbk_slab_destroy(void* handle);
+
+/*
+ * *accessible = 1 when [ptr, ptr + bytes) lies in page-locked host memory
+ * that kernels can read and write at the host address (slab slots, torch
+ * pinned tensors), else 0. Pageable memory is not an error. Gates the
+ * host-chunk entry points (cbk_paged_gather_chunks, cbk_blend_assemble_chunks).
+ */
+int cbk_host_accessible(const void* ptr, size_t bytes, int* accessible);
+
+/*
+ * n asynchronous copies dst[i] <- src[i] of bytes[i] bytes on `stream`
+ * (hipMemcpyAsync, direction from the addresses), issued in order; the
+ * tables are host arrays. The DMA path of the layerwise loads and stores:
+ * one call per layer for the coalesced pinned runs that the reference
+ * copies with one non_blocking torch copy each (cacheblend_vllm/ascend.py:
+ * 358-370, connector.py:425-429).
+ */
+int cbk_memcpy_runs(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n,
+                    cbk_stream_t stream);
+
+/*
  * K-deviation scores: scores[i] = sum_j (f32(fresh[i, j]) - f32(cached[r_i, j]))^2
  * over `width` elements, r_i = cached_rows_dev ? cached_rows_dev[i] : cached_row0 + i.
  * A row index outside [0, cached_num_rows) yields a NaN score (never read).
@@ -170,6 +220,26 @@ int cbk_blend_assemble(const cbk_kv_desc* kv, const int64_t* slots_dev, const in
                        int64_t head_dim, int32_t relocate, int32_t neox, int32_t dtype,
                        void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
                        int32_t* bad_dev, cbk_stream_t stream);
+
+/*
+ * cbk_blend_assemble with the hit rows read directly from host chunks (the
+ * fused H2D path): hit row h = src_map[p] lives in chunk c = h /
+ * chunk_tokens at row h % chunk_tokens; hit_chunks_dev is a DEVICE array
+ * [chunks][2] of device-addressable K / V plane addresses (pinned host
+ * memory, 16-byte aligned). At most max_workgroups workgroups (<= 0:
+ * enough for every row) stride over the rows. Replaces the per-segment
+ * H2D copies of _load_segments_fused (cacheblend_vllm/ascend.py:333-342)
+ * together with everything cbk_blend_assemble replaces.
+ */
+int cbk_blend_assemble_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev,
+                              const int32_t* src_map_dev, int64_t num_tokens,
+                              const uint64_t* hit_chunks_dev, int64_t chunk_tokens,
+                              int64_t chunk_token_stride, int64_t hit_rows,
+                              const int32_t* old_pos_dev, const void* cos_sin_dev,
+                              int64_t cos_sin_row_stride_elems, int64_t cos_sin_rows, int64_t heads,
+                              int64_t head_dim, int32_t relocate, int32_t neox, int32_t dtype,
+                              void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
+                              int32_t* bad_dev, int32_t max_workgroups, cbk_stream_t stream);
 
 /* Workspace bytes cbk_sparse_q_scores needs. */
 size_t cbk_sparse_q_workspace_bytes(int64_t nq, int64_t nk, int64_t hq, int64_t hkv);

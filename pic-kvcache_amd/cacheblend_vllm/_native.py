@@ -89,6 +89,27 @@ _SIGNATURES = {
             c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_vp,
         ],
     ),
+    "cbk_paged_gather_chunks": (
+        ctypes.c_int,
+        [ctypes.POINTER(KVDesc), c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i32, c_vp, c_vp],
+    ),
+    "cbk_slab_create": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(c_vp)]),
+    "cbk_slab_alloc": (ctypes.c_int, [c_vp, ctypes.POINTER(c_vp)]),
+    "cbk_slab_free": (ctypes.c_int, [c_vp, c_vp]),
+    "cbk_slab_stats": (
+        ctypes.c_int,
+        [c_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    ),
+    "cbk_slab_destroy": (ctypes.c_int, [c_vp]),
+    "cbk_host_accessible": (ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(c_i32)]),
+    "cbk_memcpy_runs": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "cbk_blend_assemble_chunks": (
+        ctypes.c_int,
+        [
+            ctypes.POINTER(KVDesc), c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64,
+            c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i32, c_vp,
+        ],
+    ),
     "cbk_sparse_q_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i64, c_i64, c_i64]),
     "cbk_sparse_q_scores": (
         ctypes.c_int,
@@ -161,6 +182,18 @@ def ptr(tensor: torch.Tensor | None) -> int | None:
 
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def host_accessible(tensor: torch.Tensor) -> bool:
+    """Whether the kernels can address ``tensor``'s bytes in host memory
+    directly (page-locked, mapped at the host address)."""
+    if tensor.device.type != "cpu" or tensor.numel() == 0:
+        return False
+    span = sum((n - 1) * abs(st) for n, st in zip(tensor.shape, tensor.stride()))
+    nbytes = (span + 1) * tensor.element_size()
+    out = ctypes.c_int32()
+    check(load().cbk_host_accessible(tensor.data_ptr(), nbytes, ctypes.byref(out)), "host_accessible")
+    return bool(out.value)
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:

@@ -16,12 +16,15 @@ scheduler's control plane and are not part of this package.
 
 from __future__ import annotations
 
+import ctypes
+import math
 import threading
-from collections.abc import Iterable, Sequence
+from collections.abc import Callable, Iterable, Sequence
 from dataclasses import dataclass, field
 
 import torch
 
+from . import _native
 from .types import BlendSegment, SegmentId
 
 MASK64 = (1 << 64) - 1
@@ -45,16 +48,118 @@ class _Entry:
     pins: int = 0
     committed: bool = False
     failed: bool = False
+    # layer -> in-place address of the stored chunk (see chunk_address)
+    addresses: dict[int, tuple | None] = field(default_factory=dict)
+
+
+def chunk_address(t: torch.Tensor) -> tuple | None:
+    """``(k_ptr, v_ptr, (chunk_tokens, row_shape, dtype))`` when kernels can
+    read/write the ``[2, chunk, *row]`` host tensor ``t`` in place: each plane
+    contiguous and 16-byte aligned, all of it in page-locked host memory
+    mapped at its host address; else None."""
+    if t.device.type != "cpu" or t.dim() < 3 or t.shape[0] != 2 or t.numel() == 0:
+        return None
+    shape, stride = t.shape, t.stride()
+    expect = 1
+    for d in range(t.dim() - 1, 0, -1):
+        if shape[d] != 1 and stride[d] != expect:
+            return None
+        expect *= shape[d]
+    es = t.element_size()
+    plane = expect * es
+    k = t.data_ptr()
+    v = k + stride[0] * es
+    if k % 16 or v % 16:
+        return None
+    lo, hi = min(k, v), max(k, v) + plane  # one storage, hence one allocation
+    ok = ctypes.c_int32()
+    _native.check(_native.load().cbk_host_accessible(lo, hi - lo, ctypes.byref(ok)), "host_accessible")
+    if not ok.value:
+        return None
+    return k, v, (int(shape[1]), tuple(int(x) for x in shape[2:]), t.dtype)
+
+
+class PinnedChunkSlab:
+    """Chunk-sized pinned host slots from the native slab (``cbk_slab_*``).
+
+    Each slot is a CPU tensor ``[2, chunk, *row]`` over pinned, coherent
+    host memory that GPU kernels read and write directly. ``free`` with an
+    event defers reuse until the event (the last GPU access) completes.
+    The slab must outlive every tensor it handed out.
+    """
+
+    def __init__(self, chunk_shape: Sequence[int], dtype: torch.dtype, chunks_per_arena: int = 128,
+                 max_bytes: int = 0):
+        self.chunk_shape = tuple(int(d) for d in chunk_shape)
+        self.dtype = dtype
+        elem = torch.empty((), dtype=dtype).element_size()
+        self.nbytes = math.prod(self.chunk_shape) * elem
+        self.chunk_bytes = (self.nbytes + 255) // 256 * 256
+        handle = ctypes.c_void_p()
+        _native.check(_native.load().cbk_slab_create(self.chunk_bytes, chunks_per_arena, max_bytes,
+                                                     ctypes.byref(handle)), "slab create")
+        self._handle = handle
+        self._lock = threading.Lock()
+        self._pending: list[tuple[int, object]] = []
+        self._tensors: dict[int, torch.Tensor] = {}  # slot address -> its tensor
+
+    def _reclaim(self) -> None:
+        keep = []
+        lib = _native.load()
+        for ptr, event in self._pending:
+            if event is None or event.query():
+                _native.check(lib.cbk_slab_free(self._handle, ptr), "slab free")
+            else:
+                keep.append((ptr, event))
+        self._pending = keep
+
+    def alloc(self) -> torch.Tensor:
+        """One free slot as a ``chunk_shape`` tensor. A slot keeps one tensor
+        object for the slab's life, so recycling a slot costs no tensor
+        construction."""
+        with self._lock:
+            if self._pending:
+                self._reclaim()
+            ptr = ctypes.c_void_p()
+            _native.check(_native.load().cbk_slab_alloc(self._handle, ctypes.byref(ptr)), "slab alloc")
+            tensor = self._tensors.get(ptr.value)
+            if tensor is None:
+                raw = (ctypes.c_uint8 * self.nbytes).from_address(ptr.value)
+                tensor = torch.frombuffer(raw, dtype=torch.uint8).view(self.dtype).view(self.chunk_shape)
+                self._tensors[ptr.value] = tensor
+            return tensor
+
+    def free(self, tensor: torch.Tensor, event=None) -> None:
+        with self._lock:
+            self._pending.append((tensor.data_ptr(), event))
+            self._reclaim()
+
+    def stats(self) -> dict[str, int]:
+        arenas, free, live = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _native.check(_native.load().cbk_slab_stats(self._handle, ctypes.byref(arenas), ctypes.byref(free),
+                                                    ctypes.byref(live)), "slab stats")
+        return {"arenas": arenas.value, "free": free.value, "live": live.value,
+                "pending": len(self._pending)}
+
+    def close(self) -> None:
+        self._tensors.clear()
+        if self._handle is not None:
+            _native.check(_native.load().cbk_slab_destroy(self._handle), "slab destroy")
+            self._handle = None
 
 
 class PinnedChunkStore:
-    def __init__(self, chunk_size: int, max_bytes: int):
+    def __init__(self, chunk_size: int, max_bytes: int,
+                 on_release: Callable[[torch.Tensor], None] | None = None):
         if max_bytes <= 0:
             raise ValueError("max_bytes must be positive")
         self.chunk_size = int(chunk_size)
         self.max_bytes = int(max_bytes)
+        # called with every layer tensor the store drops (e.g. slab slots)
+        self._on_release = on_release
         self._entries: dict[SegmentId, _Entry] = {}
         self._pins: dict[str, tuple[SegmentId, ...]] = {}
+        self._pin_sets: dict[str, frozenset[SegmentId]] = {}
         self._bytes = 0
         self._lock = threading.RLock()
 
@@ -133,6 +238,12 @@ class PinnedChunkStore:
             entry.failed = True
             self._drop_if_idle(segment_id, entry)
 
+    def holds(self, segment_id: SegmentId, layer_id: int, tensor: torch.Tensor) -> bool:
+        """Whether the store kept ``tensor`` as that segment layer."""
+        with self._lock:
+            entry = self._entries.get(segment_id)
+            return entry is not None and entry.layers.get(layer_id) is tensor
+
     def is_committed(self, segment_id: SegmentId) -> bool:
         entry = self._entries.get(segment_id)
         return entry is not None and entry.committed
@@ -149,10 +260,12 @@ class PinnedChunkStore:
                 valid.append(seg)
             if valid:
                 self._pins[request_id] = tuple(s.segment_id for s in valid)
+                self._pin_sets[request_id] = frozenset(self._pins[request_id])
             return tuple(valid)
 
     def release(self, request_id: str) -> None:
         with self._lock:
+            self._pin_sets.pop(request_id, None)
             for sid in self._pins.pop(request_id, ()):
                 entry = self._entries.get(sid)
                 if entry is not None:
@@ -160,7 +273,7 @@ class PinnedChunkStore:
 
     def get_layer(self, request_id: str, segment: BlendSegment, layer_id: int) -> torch.Tensor:
         with self._lock:
-            if segment.segment_id not in self._pins.get(request_id, ()):
+            if segment.segment_id not in self._pin_sets.get(request_id, ()):
                 raise RuntimeError(f"segment {segment.segment_id} is not pinned by {request_id}")
             entry = self._entries.get(segment.segment_id)
             if entry is None or not entry.committed:
@@ -170,13 +283,55 @@ class PinnedChunkStore:
             except KeyError as error:
                 raise KeyError(f"layer {layer_id} is not stored for {segment.segment_id}") from error
 
+    def layer_chunk_addresses(self, request_id: str, segments: Sequence[BlendSegment],
+                              layer_id: int) -> tuple[tuple, list[int]] | None:
+        """``(geometry, [k0, v0, k1, v1, ...])``: in-place host addresses of
+        one layer of pinned segments, for kernels that read the chunks over
+        the host link, with their common ``(chunk_tokens, row_shape, dtype)``;
+        None when any chunk is not kernel-addressable (``chunk_address``) or
+        the geometries differ. Each stored chunk is validated once."""
+        with self._lock:
+            pinned = self._pin_sets.get(request_id, ())
+            flat: list[int] = []
+            geometry = None
+            for seg in segments:
+                if seg.segment_id not in pinned:
+                    raise RuntimeError(f"segment {seg.segment_id} is not pinned by {request_id}")
+                entry = self._entries.get(seg.segment_id)
+                if entry is None or not entry.committed:
+                    raise KeyError(seg.segment_id)
+                if layer_id in entry.addresses:
+                    info = entry.addresses[layer_id]
+                else:
+                    tensor = entry.layers.get(layer_id)
+                    if tensor is None:
+                        raise KeyError(f"layer {layer_id} is not stored for {seg.segment_id}")
+                    info = entry.addresses[layer_id] = chunk_address(tensor)
+                if info is None or (geometry is not None and info[2] != geometry):
+                    return None
+                geometry = info[2]
+                flat.append(info[0])
+                flat.append(info[1])
+            return (geometry, flat) if geometry is not None else None
+
     def clear(self) -> None:
         with self._lock:
+            for entry in self._entries.values():
+                self._release_layers(entry)
             self._entries.clear()
             self._pins.clear()
+            self._pin_sets.clear()
             self._bytes = 0
+
+    def _release_layers(self, entry: _Entry) -> None:
+        if self._on_release is not None:
+            for tensor in entry.layers.values():
+                self._on_release(tensor)
+        entry.layers.clear()
+        entry.addresses.clear()
 
     def _drop_if_idle(self, segment_id: SegmentId, entry: _Entry) -> None:
         if not entry.reserved and not entry.pins:
             self._entries.pop(segment_id, None)
             self._bytes -= entry.size_bytes
+            self._release_layers(entry)

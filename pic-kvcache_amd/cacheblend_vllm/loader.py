@@ -12,12 +12,14 @@
         loader.commit(l, buf)          # scatter [apc:] into the vLLM pages
 
 Per layer, on the Load stream (a default-priority side stream):
-  1. hipMemcpyAsync of the pinned host hit chunks into a reusable hit
-     staging ``[2, hit_tokens, H, D]``; chunks adjacent in host memory are
-     coalesced into one copy per plane;
-  2. ``cbk_blend_assemble`` writes the layer buffer in one pass: APC prefix
-     from the pages, zeros for gaps, hit rows with their K RoPE-relocated
-     from source to target positions;
+  1. the hit chunks cross the host link: either DMA (``cbk_memcpy_runs``:
+     chunks adjacent in pinned host memory coalesced into one copy per run
+     and plane, into a reusable device hit staging ``[2, hit_tokens, H, D]``)
+     or, for fragmented chunks, in place -- the assembly kernel reads them
+     from pinned host memory through a per-layer address table;
+  2. ``cbk_blend_assemble`` (``_chunks`` for in-place reads) writes the
+     layer buffer in one pass: APC prefix from the pages, zeros for gaps,
+     hit rows with their K RoPE-relocated from source to target positions;
   3. an event, waited on by ``get``.
 Two buffers alternate by layer parity; ``commit`` records a reuse event so
 buffer ``l % 2`` is not overwritten before layer ``l``'s scatter has run.
@@ -27,6 +29,7 @@ host once and uploaded once.
 
 from __future__ import annotations
 
+import ctypes
 import time
 
 import numpy as np
@@ -115,7 +118,23 @@ class PagedBlendLoader:
         config: CacheBlendConfig,
         tracer: PipelineTracer | None = None,
         load_stream: torch.cuda.Stream | None = None,
+        zero_copy: bool | str = "auto",
+        max_workgroups: int = 256,
+        dma_min_run_bytes: int = 1 << 20,
     ):
+        """How hit rows cross the host link, per layer:
+        DMA -- the chunks, coalesced into runs where adjacent in host
+               memory, are copied into a device hit staging by the DMA
+               engines (no CUs taken from the layer's compute);
+        host read -- when every hit chunk is a kernel-addressable
+               ``[2, chunk, *row]`` host tensor (page-locked, contiguous
+               16-byte aligned planes), the assembly kernel can read the hit
+               rows in place (``max_workgroups`` bounds the CUs it holds).
+        ``zero_copy``: True forces host reads where possible, False forces
+        DMA, "auto" reads in place only when the runs average fewer than
+        ``dma_min_run_bytes`` per copy, where per-copy DMA cost dominates."""
+        if zero_copy not in (True, False, "auto"):
+            raise ValueError("zero_copy must be True, False or 'auto'")
         self.kv_caches = kv_caches
         self.store = store
         self.request_id = request_id
@@ -150,6 +169,12 @@ class PagedBlendLoader:
         self._staging: list[torch.Tensor] = []
         self._hit_staging: torch.Tensor | None = None
         self._descs: dict[int, _native.KVDesc] = {}
+        self._zero_copy = zero_copy
+        self._max_workgroups = max_workgroups
+        self._dma_min_run_bytes = int(dma_min_run_bytes)
+        self._ptr_host: torch.Tensor | None = None  # [layers, chunks, 2] pinned
+        self._ptr_dev: torch.Tensor | None = None
+        self._zc_layers: set[int] = set()
         self._load_stream = None
         if config.event_pipeline:
             self._load_stream = load_stream or torch.cuda.Stream(self.device)
@@ -177,13 +202,84 @@ class PagedBlendLoader:
             self._descs[layer_id] = desc
         return desc
 
-    def _load_hits(self, layer_id: int) -> None:
-        hosts = [self.store.get_layer(self.request_id, seg, layer_id) for seg in self.plan.segments]
+    def _chunk_addresses(self, layer_id: int) -> tuple[int, list[int]] | None:
+        """(chunk_tokens, flat [k0, v0, k1, v1, ...] host addresses) of the
+        layer's hit chunks when every chunk is kernel-addressable and full
+        (row h of the hits is row h % chunk of chunk h // chunk), else None."""
+        lookup = getattr(self.store, "layer_chunk_addresses", None)
+        if lookup is None:
+            return None
+        found = lookup(self.request_id, self.plan.segments, layer_id)
+        if found is None:
+            return None
+        (chunk, row_shape, dtype), flat = found
+        if row_shape != self.row_shape or dtype != self.dtype:
+            return None
+        if any(seg.length != chunk for seg in self.plan.segments[:-1]) or self.plan.segments[-1].length > chunk:
+            return None
+        return chunk, flat
+
+    def _address_runs(self, flat: list[int], row_bytes: int) -> list[tuple[int, int, int, int]]:
+        """Maximal runs of consecutive segments whose K (and V) planes are
+        adjacent in host memory: ``(first_hit_row, tokens, k_addr, v_addr)``."""
+        runs: list[list[int]] = []
+        off = 0
+        for i, seg in enumerate(self.plan.segments):
+            k, v, n = flat[2 * i], flat[2 * i + 1], seg.length
+            if runs:
+                r = runs[-1]
+                if k == r[2] + r[1] * row_bytes and v == r[3] + r[1] * row_bytes:
+                    r[1] += n
+                    off += n
+                    continue
+            runs.append([off, n, k, v])
+            off += n
+        return [tuple(r) for r in runs]
+
+    def _ensure_hit_staging(self) -> torch.Tensor:
         if self._hit_staging is None:
             self._hit_staging = torch.empty(
                 (2, self.plan.hit_tokens, *self.row_shape), dtype=self.dtype, device=self.device
             )
-        hit = self._hit_staging
+        return self._hit_staging
+
+    def _load_hits(self, layer_id: int) -> None:
+        found = self._chunk_addresses(layer_id)
+        if found is not None:
+            chunk, flat = found
+            row_bytes = int(np.prod(self.row_shape)) * torch.empty((), dtype=self.dtype).element_size()
+            runs = self._address_runs(flat, row_bytes)
+            avg = self.plan.hit_tokens * row_bytes / max(1, len(runs))
+            host_read = self._zero_copy is True or (self._zero_copy == "auto" and avg < self._dma_min_run_bytes)
+            if host_read:
+                # publish the layer's chunk addresses; the assembly kernel
+                # reads the hit rows over the host link
+                if self._ptr_host is None:
+                    layers = len(self.kv_caches)
+                    self._ptr_host = torch.empty((layers, len(flat)), dtype=torch.int64, pin_memory=True)
+                    self._ptr_dev = torch.empty((layers, len(flat)), dtype=torch.int64, device=self.device)
+                table = self._ptr_host[layer_id]
+                table.copy_(torch.tensor(flat, dtype=torch.int64))
+                self._ptr_dev[layer_id].copy_(table, non_blocking=True)
+                self._zc_layers.add(layer_id)
+                self._zc_chunk = chunk
+                return
+            self._zc_layers.discard(layer_id)
+            hit = self._ensure_hit_staging()
+            kb, vb = hit[0].data_ptr(), hit[1].data_ptr()
+            n = 2 * len(runs)
+            dst = (ctypes.c_uint64 * n)()
+            src = (ctypes.c_uint64 * n)()
+            nbytes = (ctypes.c_uint64 * n)()
+            for i, (off, tokens, k, v) in enumerate(runs):
+                dst[2 * i], src[2 * i], nbytes[2 * i] = kb + off * row_bytes, k, tokens * row_bytes
+                dst[2 * i + 1], src[2 * i + 1], nbytes[2 * i + 1] = vb + off * row_bytes, v, tokens * row_bytes
+            _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n, _native.stream_handle(self.device)),
+                          "hit runs H2D")
+            return
+        self._zc_layers.discard(layer_id)
+        hosts = [self.store.get_layer(self.request_id, seg, layer_id) for seg in self.plan.segments]
+        hit = self._ensure_hit_staging()
         for off, n, k, v in coalesce_host_runs(hosts):
             hit[0, off : off + n].copy_(k, non_blocking=True)
             hit[1, off : off + n].copy_(v, non_blocking=True)
@@ -206,6 +302,35 @@ class PagedBlendLoader:
             if limit > table.shape[0]:
                 raise IndexError(f"positions up to {limit} exceed the RoPE cache of {table.shape[0]}")
         apc = self.plan.apc_prefix_tokens
+        if layer_id in self._zc_layers:
+            row_bytes = int(np.prod(self.row_shape)) * es
+            rc = _native.load().cbk_blend_assemble_chunks(
+                self._desc(layer_id) if apc else None,
+                self._slots.data_ptr() if apc else None,
+                self._src_map.data_ptr(),
+                self.plan.allocation_end,
+                self._ptr_dev[layer_id].data_ptr(),
+                self._zc_chunk,
+                row_bytes,
+                self.plan.hit_tokens,
+                _native.ptr(self._old_pos),
+                _native.ptr(table),
+                table.stride(0) if table is not None else 0,
+                table.shape[0] if table is not None else 0,
+                heads,
+                head_dim,
+                int(self._relocate),
+                neox,
+                _native.DTYPE_CODES[self.dtype],
+                buffer[0].data_ptr(),
+                buffer[1].data_ptr(),
+                buffer.stride(1) * es,
+                None,
+                self._max_workgroups,
+                _native.stream_handle(self.device),
+            )
+            _native.check(rc, "blend assemble (host chunks)")
+            return
         rc = _native.load().cbk_blend_assemble(
             self._desc(layer_id) if apc else None,
             self._slots.data_ptr() if apc else None,

@@ -9,11 +9,18 @@ dtype, then every product, sum and difference is rounded to the key dtype.
 
 from __future__ import annotations
 
+import threading
+import weakref
+
 import torch
 
 from . import _native
 
-_cache_lock_free: dict[tuple[int, int, torch.dtype, torch.device], torch.Tensor] = {}
+# (id(cos_sin_cache), dtype, device) -> (weakref to that cache, its _version,
+# converted table). The weakref guards against a new cache object reusing the
+# id -- or the address -- of a freed one.
+_tables: dict[tuple[int, torch.dtype, torch.device], tuple[weakref.ref, int, torch.Tensor]] = {}
+_tables_lock = threading.Lock()
 
 
 def rope_style(rotary_emb) -> tuple[int, bool]:
@@ -27,13 +34,18 @@ def cos_sin_table(rotary_emb, dtype: torch.dtype, device: torch.device) -> torch
     cache = getattr(rotary_emb, "cos_sin_cache", None)
     if not isinstance(cache, torch.Tensor) or cache.ndim != 2:
         raise ValueError("CacheBlend requires a two-dimensional RoPE cos_sin_cache")
-    key = (cache.data_ptr(), cache._version, dtype, device)
-    table = _cache_lock_free.get(key)
-    if table is None:
-        table = cache.to(device=device, dtype=dtype).contiguous()
-        if len(_cache_lock_free) > 16:
-            _cache_lock_free.clear()
-        _cache_lock_free[key] = table
+    key = (id(cache), dtype, torch.device(device))
+    with _tables_lock:
+        hit = _tables.get(key)
+        if hit is not None and hit[0]() is cache and hit[1] == cache._version:
+            return hit[2]
+    table = cache.to(device=device, dtype=dtype).contiguous()
+    if table is cache:
+        return table  # nothing converted; holding it would keep the cache alive
+    with _tables_lock:
+        for k in [k for k, v in _tables.items() if v[0]() is None]:
+            del _tables[k]
+        _tables[key] = (weakref.ref(cache), cache._version, table)
     return table
 
 

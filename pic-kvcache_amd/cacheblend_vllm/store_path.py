@@ -31,7 +31,10 @@ from typing import Any
 
 import torch
 
-from .kv_layout import gather_paged_kv, kv_planes
+import ctypes
+
+from . import _native
+from .kv_layout import gather_paged_kv, kv_desc, kv_planes
 from .trace import PipelineTracer
 from .types import BlendPlan, SegmentId
 
@@ -96,8 +99,16 @@ class StoreStreamWriter:
         tracer: PipelineTracer | None = None,
         streams=CudaStreams,
         store_stream=None,
+        slab=None,
+        max_workgroups: int = 128,
     ):
+        """``slab`` (a PinnedChunkSlab): the fused path -- each chunk is written
+        by the gather kernel straight into its own pinned slot (no device
+        staging, no DMA, no per-layer pinning); None: gather into device
+        staging + one pinned D2H per layer, as the reference does."""
         self._store = store
+        self._slab = slab
+        self._max_workgroups = max_workgroups
         self.block_size = block_size
         self.chunk_size = chunk_size
         self.num_layers = num_layers
@@ -187,18 +198,22 @@ class StoreStreamWriter:
             with self._streams.stream(self._store_stream):
                 self._store_stream.wait_stream(current)
                 slots = self._upload_slots(request_id, slots, kv_layer)
-                staging = self._store_staging_by_request.get(request_id)
-                if staging is None or staging.shape[1] != slots.numel():
-                    if staging is not None:
-                        # an earlier D2H may still read it: keep it until the
-                        # Store stream drains (wait_for_save)
-                        self._retired_store_staging.append(staging)
-                    staging = gather_paged_kv(kv_layer, slots, self.block_size).contiguous()
-                    self._store_staging_by_request[request_id] = staging
+                if self._slab is not None:
+                    host = [self._slab.alloc() for _ in pending]
+                    self._gather_to_chunks(kv_layer, slots, host)
                 else:
-                    gather_paged_kv(kv_layer, slots, self.block_size, out=staging)
-                host = torch.empty(staging.shape, dtype=staging.dtype, device="cpu", pin_memory=True)
-                host.copy_(staging, non_blocking=True)
+                    staging = self._store_staging_by_request.get(request_id)
+                    if staging is None or staging.shape[1] != slots.numel():
+                        if staging is not None:
+                            # an earlier D2H may still read it: keep it until the
+                            # Store stream drains (wait_for_save)
+                            self._retired_store_staging.append(staging)
+                        staging = gather_paged_kv(kv_layer, slots, self.block_size).contiguous()
+                        self._store_staging_by_request[request_id] = staging
+                    else:
+                        gather_paged_kv(kv_layer, slots, self.block_size, out=staging)
+                    host = torch.empty(staging.shape, dtype=staging.dtype, device="cpu", pin_memory=True)
+                    host.copy_(staging, non_blocking=True)
                 event = self._streams.Event()
                 event.record(self._store_stream)
             future = self._save_pool.submit(
@@ -206,6 +221,9 @@ class StoreStreamWriter:
             )
         except Exception:
             self._save_slots.release()
+            if self._slab is not None and isinstance(locals().get("host"), list):
+                for chunk in locals()["host"]:
+                    self._slab.free(chunk)
             raise
         with self._save_lock:
             self._save_futures.add(future)
@@ -230,14 +248,36 @@ class StoreStreamWriter:
         self._device_slots[request_id] = (host, device)
         return device
 
-    def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host: torch.Tensor) -> bool:
-        """Per-chunk views of the pinned batch into the store (connector.py:449-466)."""
+    def _gather_to_chunks(self, kv_layer: Any, slots: torch.Tensor, chunks: list[torch.Tensor]) -> None:
+        """cbk_paged_gather_chunks: the layer's pending tokens straight into
+        their pinned chunk slots, on the current (Store) stream."""
+        desc, key = kv_desc(kv_layer, self.block_size)
+        n = len(chunks)
+        plane = chunks[0].stride(0) * chunks[0].element_size()
+        k_list = [c.data_ptr() for c in chunks]
+        k_ptrs = (ctypes.c_void_p * n)(*k_list)
+        v_ptrs = (ctypes.c_void_p * n)(*[k + plane for k in k_list])
+        row_bytes = desc.row_bytes
+        rc = _native.load().cbk_paged_gather_chunks(
+            desc, slots.data_ptr(), slots.numel(), chunks[0].shape[1], k_ptrs, v_ptrs, row_bytes,
+            self._max_workgroups, None, _native.stream_handle(key.device),
+        )
+        _native.check(rc, "gather to chunks")
+
+    def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host, accepted=None) -> bool:
+        """Per-chunk host tensors into the store (connector.py:449-466): views
+        of one pinned batch, or (fused path) one slab slot per chunk.
+        ``accepted[i]`` records whether the store kept slot i."""
         offset = 0
         committed = False
-        for segment_id, layer_id, length in pending:
-            result = self._store.put_layer_host(segment_id, layer_id, host[:, offset : offset + length])
+        holds = getattr(self._store, "holds", None)
+        for index, (segment_id, layer_id, length) in enumerate(pending):
+            chunk = host[index] if isinstance(host, list) else host[:, offset : offset + length]
+            result = self._store.put_layer_host(segment_id, layer_id, chunk)
             if result is not None:
                 committed |= result
+            if accepted is not None:
+                accepted[index] = holds is not None and holds(segment_id, layer_id, chunk)
             offset += length
         return committed
 
@@ -249,10 +289,26 @@ class StoreStreamWriter:
         request_id: str | None = None,
         store_enqueued_ns: int | None = None,
     ) -> bool:
-        """Publisher thread body (reference connector.py:468-499)."""
+        """Publisher thread body (reference connector.py:468-499). Fused path:
+        slots the store did not keep go back to the slab (the ones it keeps
+        return through its release hook when it drops them)."""
+        slots = isinstance(host, list) and self._slab is not None
+        accepted = [False] * len(pending) if slots else None
+        try:
+            return self._publish_checked(event, pending, host, request_id, store_enqueued_ns, accepted)
+        finally:
+            if slots:
+                for chunk, kept in zip(host, accepted):
+                    if not kept:
+                        self._slab.free(chunk)
+
+    def _publish_checked(self, event, pending, host, request_id, store_enqueued_ns, accepted) -> bool:
         try:
             event.synchronize()
-            committed = self._publish_host_batch(pending, host)
+            if accepted is None:
+                committed = self._publish_host_batch(pending, host)
+            else:
+                committed = self._publish_host_batch(pending, host, accepted)
             if self._trace.enabled:
                 self._trace.emit(
                     "save_store_finished",

@@ -106,6 +106,75 @@ __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a)
   }
 }
 
+// Gather straight into host chunks: token t of a batch goes to chunk
+// t / chunk_tokens at row t % chunk_tokens, each chunk plane being a
+// [chunk_tokens, row] block at chunk_k[c] / chunk_v[c] (pinned host memory
+// addressed over PCIe). A bounded grid walks the batch with a stride: 16-64
+// workgroups already saturate the host link, leaving the CUs to the
+// serving stream.
+constexpr int kChunksPerLaunch = 64;
+constexpr int kChunkThreads = 256;
+constexpr int kChunkUnroll = 4;
+
+struct ChunkArgs {
+  char* chunk_k[kChunksPerLaunch];
+  char* chunk_v[kChunksPerLaunch];
+  const char* k_base;
+  const char* v_base;
+  const int64_t* slots;
+  int64_t block_stride;
+  int64_t token_stride;
+  int64_t chunk_token_stride;  // bytes between tokens inside a chunk plane
+  int32_t* bad;
+  uint32_t num_tokens;         // tokens in this launch (<= 64 chunks)
+  uint32_t row_vecs;
+  uint32_t num_slots;
+  FastDiv row_div;
+  FastDiv bs_div;
+  FastDiv chunk_div;
+};
+
+template <int VEC>
+__global__ __launch_bounds__(kChunkThreads) void gather_chunks_kernel(const ChunkArgs a) {
+  using V = typename Vec<VEC>::T;
+  const uint32_t total = a.num_tokens * 2u * a.row_vecs;
+  const uint32_t stride = gridDim.x * uint32_t(kChunkThreads * kChunkUnroll);
+  for (uint32_t base = blockIdx.x * uint32_t(kChunkThreads * kChunkUnroll) + threadIdx.x; base < total;
+       base += stride) {
+    V buf[kChunkUnroll];
+    char* dst[kChunkUnroll];
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u) {
+      const uint32_t f = base + uint32_t(u * kChunkThreads);
+      dst[u] = nullptr;
+      buf[u] = V(0);
+      if (f < total) {
+        const uint32_t row = a.row_div.div(f);
+        const uint32_t j = f - row * a.row_vecs;
+        const uint32_t c = row >= a.num_tokens ? 1u : 0u;
+        const uint32_t t = row - c * a.num_tokens;
+        const uint32_t ck = a.chunk_div.div(t);
+        const uint32_t r = t - ck * a.chunk_div.d;
+        dst[u] = (c ? a.chunk_v[ck] : a.chunk_k[ck]) + int64_t(r) * a.chunk_token_stride + int64_t(j) * VEC;
+        const int64_t slot = a.slots[t];
+        if (slot >= 0 && slot < int64_t(a.num_slots)) {
+          const uint32_t s32 = uint32_t(slot);
+          const uint32_t blk = a.bs_div.div(s32);
+          const uint32_t off = s32 - blk * a.bs_div.d;
+          buf[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(
+              (c ? a.v_base : a.k_base) + int64_t(blk) * a.block_stride + int64_t(off) * a.token_stride +
+              int64_t(j) * VEC));
+        } else if (a.bad != nullptr && c == 0 && j == 0) {
+          atomicAdd(a.bad, 1);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u)
+      if (dst[u] != nullptr) *reinterpret_cast<V*>(dst[u]) = buf[u];
+  }
+}
+
 int validate_desc(const cbk_kv_desc* kv) {
   CBK_REQUIRE(kv != nullptr, "kv descriptor is NULL");
   CBK_REQUIRE(kv->k_base != nullptr && kv->v_base != nullptr, "kv base pointer is NULL");
@@ -200,10 +269,81 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
   return CBK_OK;
 }
 
+int launch_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots, int64_t num_tokens,
+                         int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
+                         int64_t chunk_token_stride, int32_t max_workgroups, int32_t* bad,
+                         hipStream_t stream) {
+  clear_error();
+  if (int rc = validate_desc(kv)) return rc;
+  CBK_REQUIRE(num_tokens >= 0 && chunk_tokens > 0, "num_tokens/chunk_tokens invalid");
+  if (num_tokens == 0) return CBK_OK;
+  CBK_REQUIRE(slots && chunk_k && chunk_v, "NULL pointer");
+  CBK_REQUIRE(chunk_token_stride >= kv->row_bytes, "chunk token stride smaller than a row");
+  const int64_t nchunks = (num_tokens + chunk_tokens - 1) / chunk_tokens;
+  int64_t align[6] = {kv->row_bytes, kv->block_stride, kv->token_stride, chunk_token_stride,
+                      int64_t(reinterpret_cast<uintptr_t>(kv->k_base)),
+                      int64_t(reinterpret_cast<uintptr_t>(kv->v_base))};
+  int vec = common_vec_bytes(align, 6);
+  for (int64_t c = 0; c < nchunks; ++c) {
+    CBK_REQUIRE(chunk_k[c] && chunk_v[c], "chunk %lld destination is NULL", (long long)c);
+    int64_t p[2] = {int64_t(reinterpret_cast<uintptr_t>(chunk_k[c])),
+                    int64_t(reinterpret_cast<uintptr_t>(chunk_v[c]))};
+    vec = std::min(vec, common_vec_bytes(p, 2));
+  }
+  const int64_t row_vecs = kv->row_bytes / vec;
+  const int64_t per_launch = chunk_tokens * kChunksPerLaunch;
+  CBK_REQUIRE(std::min(per_launch, num_tokens) * 2 * row_vecs < (int64_t(1) << 32), "launch too large");
+  const uint32_t grid_cap = uint32_t(max_workgroups > 0 ? max_workgroups : 64);
+  ChunkArgs a{};
+  a.k_base = static_cast<const char*>(kv->k_base);
+  a.v_base = static_cast<const char*>(kv->v_base);
+  a.block_stride = kv->block_stride;
+  a.token_stride = kv->token_stride;
+  a.chunk_token_stride = chunk_token_stride;
+  a.bad = bad;
+  a.row_vecs = uint32_t(row_vecs);
+  a.num_slots = uint32_t(kv->num_blocks * kv->block_size);
+  a.row_div = FastDiv::make(uint32_t(row_vecs));
+  a.bs_div = FastDiv::make(uint32_t(kv->block_size));
+  a.chunk_div = FastDiv::make(uint32_t(chunk_tokens));
+  for (int64_t t0 = 0; t0 < num_tokens; t0 += per_launch) {
+    const int64_t n = std::min(per_launch, num_tokens - t0);
+    const int64_t c0 = t0 / chunk_tokens;
+    const int64_t nc = (n + chunk_tokens - 1) / chunk_tokens;
+    for (int64_t c = 0; c < kChunksPerLaunch; ++c) {
+      a.chunk_k[c] = static_cast<char*>(chunk_k[c0 + (c < nc ? c : 0)]);
+      a.chunk_v[c] = static_cast<char*>(chunk_v[c0 + (c < nc ? c : 0)]);
+    }
+    a.slots = slots + t0;
+    a.num_tokens = uint32_t(n);
+    const uint64_t total = uint64_t(n) * 2 * uint64_t(row_vecs);
+    const uint32_t grid = uint32_t(std::min<uint64_t>(
+        grid_cap, (total + kChunkThreads * kChunkUnroll - 1) / (kChunkThreads * kChunkUnroll)));
+    switch (vec) {
+      case 16: hipLaunchKernelGGL(gather_chunks_kernel<16>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+      case 8: hipLaunchKernelGGL(gather_chunks_kernel<8>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+      case 4: hipLaunchKernelGGL(gather_chunks_kernel<4>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+      case 2: hipLaunchKernelGGL(gather_chunks_kernel<2>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+      default: hipLaunchKernelGGL(gather_chunks_kernel<1>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+    }
+    if (int rc = launch_status("paged gather to chunks")) return rc;
+  }
+  return CBK_OK;
+}
+
 }  // namespace
 }  // namespace cbk
 
 extern "C" {
+
+int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
+                            int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
+                            int64_t chunk_token_stride, int32_t max_workgroups,
+                            int32_t* bad_slots_dev, cbk_stream_t stream) {
+  return cbk::launch_gather_chunks(kv, slots_dev, num_tokens, chunk_tokens, chunk_k, chunk_v,
+                                   chunk_token_stride, max_workgroups, bad_slots_dev,
+                                   static_cast<hipStream_t>(stream));
+}
 
 int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
                      void* out_k_dev, void* out_v_dev, int64_t out_token_stride,

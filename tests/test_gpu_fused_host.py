@@ -1,0 +1,134 @@
+"""GPU: the fused host paths -- pinned chunk slab, gather straight into host
+chunks (store) and assembly reading host chunks (load) -- bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from cacheblend_vllm import _native, synthetic
+from cacheblend_vllm.config import CacheBlendConfig
+from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
+from cacheblend_vllm.loader import PagedBlendLoader
+from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
+from cacheblend_vllm.types import BlendPlan, BlendSegment
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_slab_slots_are_pinned_recycled_and_bounded():
+    slab = PinnedChunkSlab((2, 256, 4, 128), torch.bfloat16, chunks_per_arena=4, max_bytes=8 * 512 * 1024)
+    slots = [slab.alloc() for _ in range(6)]
+    assert all(_native.host_accessible(s) for s in slots)
+    assert _native.host_accessible(torch.ones(64).pin_memory())
+    assert not _native.host_accessible(torch.ones(64))
+    assert all(s.data_ptr() % 256 == 0 for s in slots)
+    assert len({s.data_ptr() for s in slots}) == 6
+    st = slab.stats()
+    assert st["arenas"] == 2 and st["live"] == 6 and st["free"] == 2
+    ev = torch.cuda.Event()
+    ev.record()
+    freed = slots.pop()
+    slab.free(freed, ev)
+    torch.cuda.synchronize()
+    again = slab.alloc()  # the fenced slot comes back once its event completed
+    assert again.data_ptr() == freed.data_ptr()
+    slots.append(again)
+    slots += [slab.alloc(), slab.alloc()]
+    with pytest.raises(RuntimeError, match="exceed"):
+        slab.alloc()  # a third arena would pass max_bytes
+    for s in slots:
+        slab.free(s)
+    with pytest.raises(ValueError, match="not a live slot"):
+        slab.free(slots[0])
+    del slots, again, freed
+    slab.close()
+
+
+@pytest.mark.parametrize("layout", ["merged_first", "merged_block"])
+def test_fused_store_writes_chunks_bit_exact(layout):
+    L, NB, BS, H, D, CH, T = 3, 128, 16, 8, 128, 256, 1000
+    pools = [synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=40 + l) for l in range(L)]
+    layers = pools if layout == "merged_first" else [p.transpose(0, 1).contiguous() for p in pools]
+    slots = synthetic.block_slots(torch.randperm(NB)[: (T + BS - 1) // BS], BS, T)
+    slab = PinnedChunkSlab((2, CH, H, D), torch.bfloat16, chunks_per_arena=8)
+    store = PinnedChunkStore(CH, 1 << 34, on_release=slab.free)
+    writer = StoreStreamWriter(store, BS, CH, L, "m", slab=slab, max_workgroups=32)
+    request = RequestMetadata("a", list(range(T)), slots, None, True, T)  # 3 full chunks of 256
+    for l in range(L):
+        writer.save_layer(l, layers[l], [request])
+    writer.wait_for_save()
+    segs = writer._save_segments["a"]
+    assert [s for s, _ in segs] == [0, 256, 512]
+    for start, sid in segs:
+        assert store.is_committed(sid)
+        for l in range(L):
+            got = store._entries[sid].layers[l]
+            assert _native.host_accessible(got)
+            want = O.gather_paged_kv(_bits(pools[l]), slots[start:start + CH].numpy(), BS)
+            np.testing.assert_array_equal(_bits(got), want, err_msg=f"chunk {start} layer {l}")
+    assert slab.stats()["live"] == 3 * L
+    store.clear()  # release hook returns every slot
+    assert slab.stats()["live"] == 0
+    writer.close()
+    slab.close()
+
+
+def test_fused_store_then_host_read_load_round_trip():
+    """Store with the fused gather, blend-load with host reads and RoPE
+    relocation, commit: every stage bit-exact against the oracle."""
+    L, NB, BS, H, D, CH = 2, 192, 16, 4, 128, 256
+    layers = [synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=60 + l) for l in range(L)]
+    perm = torch.randperm(NB)
+    slots = synthetic.block_slots(perm[:64], BS, 1024)
+    slab = PinnedChunkSlab((2, CH, H, D), torch.bfloat16)
+    store = PinnedChunkStore(CH, 1 << 34, on_release=slab.free)
+    writer = StoreStreamWriter(store, BS, CH, L, "m", slab=slab)
+    writer.save_layer(0, layers[0], [RequestMetadata("a", list(range(1024)), slots, None, True, 1024)])
+    writer.save_layer(1, layers[1], [RequestMetadata("a", list(range(1024)), slots, None, True, 1024)])
+    writer.wait_for_save()
+    segs = writer._save_segments["a"]
+    blend = [BlendSegment(segs[3][1], 260), BlendSegment(segs[1][1], 700)]
+    store.pin("b", blend)
+    plan = BlendPlan(40, 1100, 512, tuple(blend))
+    new_slots = synthetic.block_slots(perm[64:64 + 70], BS, 1100)
+
+    class Rope:
+        head_size = rotary_dim = D
+        is_neox_style = True
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        ang = torch.arange(4096, dtype=torch.float32)[:, None] * inv[None, :]
+        cos_sin_cache = torch.cat([ang.cos(), ang.sin()], dim=-1).to(DEV)
+
+    rope = Rope()
+    cache = rope.cos_sin_cache.cpu().numpy()
+
+    def reloc(old, new, k_bits):
+        k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
+        return O.f32_to_bf16(O.relocate_key(cache, old, new, k, D, True, bf16=True)).reshape(k_bits.shape)
+
+    before = [_bits(l) for l in layers]
+    loader = PagedBlendLoader(layers, store, "b", plan, new_slots, BS, CacheBlendConfig.from_extra_config({}))
+    loader.prefetch(0, rope)
+    for l in range(L):
+        buf = loader.get(l)
+        loader.prefetch(l + 1, rope)
+        hosts = [(768, 260, O.gather_paged_kv(before[l], slots[768:1024].numpy(), BS)),
+                 (256, 700, O.gather_paged_kv(before[l], slots[256:512].numpy(), BS))]
+        want = O.loader_assemble(before[l], new_slots.numpy(), BS, 40, 1100, hosts, relocate=reloc)
+        np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
+        loader.commit(l, buf)
+        torch.cuda.synchronize()
+        expect = before[l].copy()
+        O.loader_commit(want, expect, new_slots.numpy(), BS, 40, 1100)
+        np.testing.assert_array_equal(_bits(layers[l]), expect)
+    assert loader._zc_layers == {0, 1}
+    store.release("b")
+    store.clear()
+    writer.close()
+    slab.close()

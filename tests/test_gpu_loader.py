@@ -74,18 +74,22 @@ def test_reference_known_answer(golden):
         assert paged[1].reshape(2, -1).tolist() == case["expected_pages_after_commit_v"]
 
 
+# head_dim 128 / 64: one 16-byte vector per lane with lane exchange for NeoX
+# pairs, rows of 0.75-4 KiB (1, 2 and 4 passes of 1 KiB); 80: heads straddle
+# 1 KiB passes, so the per-pair path runs
+@pytest.mark.parametrize("head_dim,heads", [(128, 4), (64, 6), (80, 3), (128, 6), (128, 8)])
 @pytest.mark.parametrize("neox", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
-def test_relocate_key_bit_exact_vs_oracle(neox, dtype):
-    rope = Rope(128, 4096, neox)
+def test_relocate_key_bit_exact_vs_oracle(neox, dtype, head_dim, heads):
+    rope = Rope(head_dim, 4096, neox)
     torch.manual_seed(0)
-    key = torch.randn(300, 4 * 128, device=DEV).to(dtype)
+    key = torch.randn(300, heads * head_dim, device=DEV).to(dtype)
     old = torch.randint(0, 4096, (300,))
     new = torch.randint(0, 4096, (300,))
     got = relocate_key(rope, old, new, key)
     cache = rope.cos_sin_cache.cpu().numpy()
     want = O.relocate_key(cache if dtype != torch.float16 else cache.astype(np.float16).astype(np.float32),
-                          old.numpy(), new.numpy(), key.float().cpu().numpy(), 128, neox,
+                          old.numpy(), new.numpy(), key.float().cpu().numpy(), head_dim, neox,
                           bf16=dtype == torch.bfloat16)
     if dtype == torch.float16:
         # the oracle's rounding helper is bf16-only: compare within one f16 ulp
@@ -162,14 +166,16 @@ def _blend_setup(num_layers, nb, bs, heads, dim, apc, segments, alloc_end, dtype
     return layers, store, plan, slots, hosts
 
 
+@pytest.mark.parametrize("zero_copy", [True, False])
 @pytest.mark.parametrize("neox", [True, False])
-def test_loader_bf16_relocation_bit_exact_vs_oracle(neox):
+def test_loader_bf16_relocation_bit_exact_vs_oracle(neox, zero_copy):
     heads, dim, bs, chunk = 4, 128, 16, 64
     segs = [(0, 100, 128), (512, 300, 64), (64, 400, 192)]  # source != target: relocate
     layers, store, plan, slots, hosts = _blend_setup(3, 200, bs, heads, dim, 37, segs, 700,
                                                      torch.bfloat16, chunk)
     rope = Rope(dim, 2048, neox)
-    loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk))
+    loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk),
+                              zero_copy=zero_copy)
     cache = rope.cos_sin_cache.cpu().numpy()
 
     def reloc(old, new, k_bits):
@@ -195,6 +201,8 @@ def test_loader_bf16_relocation_bit_exact_vs_oracle(neox):
         loader.commit(l, buf)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(_bits(layers[l]), expect_pages, err_msg=f"commit layer {l}")
+    # the pinned chunks took the host-read path exactly when asked to
+    assert (len(loader._zc_layers) > 0) == zero_copy
 
 
 def test_loader_without_relocation_is_a_bit_copy():
@@ -237,6 +245,7 @@ def test_loader_blend_load_workload_sample():
 
     loader = PagedBlendLoader(layers, store, "req", plan, slots, 16, _cfg())
     loader.prefetch(0, rope)
+    assert 0 in loader._zc_layers  # pinned chunks: hit rows read over PCIe
     for l in range(2):
         buf = loader.get(l)
         loader.prefetch(l + 1, rope)

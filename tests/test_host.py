@@ -115,3 +115,39 @@ def test_plan_invariants_and_gap_runs():
     with pytest.raises(ValueError, match="hit_tokens"):
         BlendPlan(0, 20, 5, (BlendSegment(sid(0, 4), 2),))
     assert BlendPlan.from_dict(plan.to_dict()) == plan
+
+
+def test_cos_sin_table_cache_tracks_object_and_version():
+    from types import SimpleNamespace
+
+    from cacheblend_vllm.rope import cos_sin_table
+
+    a = SimpleNamespace(cos_sin_cache=torch.ones(8, 4))
+    t1 = cos_sin_table(a, torch.bfloat16, torch.device("cpu"))
+    assert t1.dtype == torch.bfloat16 and cos_sin_table(a, torch.bfloat16, torch.device("cpu")) is t1
+    a.cos_sin_cache.mul_(2)  # in-place update: version bump, table rebuilt
+    assert float(cos_sin_table(a, torch.bfloat16, torch.device("cpu"))[0, 0]) == 2.0
+    for _ in range(8):  # freed caches whose id or address is reused never hit a stale table
+        b = SimpleNamespace(cos_sin_cache=torch.full((8, 4), 3.0))
+        assert float(cos_sin_table(b, torch.bfloat16, torch.device("cpu"))[0, 0]) == 3.0
+        del b
+    same = torch.ones(8, 4, dtype=torch.bfloat16)
+    assert cos_sin_table(SimpleNamespace(cos_sin_cache=same), torch.bfloat16, torch.device("cpu")) is same
+
+
+def test_layer_chunk_addresses_requires_pins_and_addressable_chunks():
+    from cacheblend_vllm.host_store import PinnedChunkStore
+    from cacheblend_vllm.types import BlendSegment
+
+    store = PinnedChunkStore(4, 1 << 20)
+    sid = store.begin_put("m", 0, [1, 2, 3, 4], num_layers=1)
+    store.put_layer_host(sid, 0, torch.zeros(2, 4, 2, 8))  # pageable: not kernel-addressable
+    seg = BlendSegment(sid, 0)
+    with pytest.raises(RuntimeError, match="not pinned"):
+        store.layer_chunk_addresses("r", [seg], 0)
+    store.pin("r", [seg])
+    assert store.layer_chunk_addresses("r", [seg], 0) is None
+    assert store.get_layer("r", seg, 0).shape == (2, 4, 2, 8)
+    store.release("r")
+    with pytest.raises(RuntimeError, match="not pinned"):
+        store.get_layer("r", seg, 0)
