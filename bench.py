@@ -304,11 +304,17 @@ def sparse_q(torch, S, synthetic, dev):
 def store_pipeline(torch, layers, cache, src_slots, args):
     """Qwen3-8B layerwise store: save_kv_layer for all 36 layers of the
     8192-token prompt (32 chunks of 256) through the Store stream, timed from
-    the first save to the end of wait_for_save, in two modes:
-    fused  -- one kernel per layer gathers the pages straight into pinned
-              chunk slots of a warm slab (the GPU writes host memory);
-    staged -- gather into reused device staging, then a pinned D2H copy.
-    Both include publication of every chunk into the host store."""
+    the first save to the end of wait_for_save (publication of every chunk
+    into the host store included), in three modes:
+    host_write -- (default) pinned slab slots allocated as consecutive runs,
+                  written by the gather kernel directly over the host link;
+    dma        -- the same slots; gather into a chunk-major device staging,
+                  then one hipMemcpyAsync per run of slots;
+    reference  -- gather into device staging + one D2H into a freshly pinned
+                  per-layer batch (the reference's scheme).
+    Also timed with the saves interleaved with bf16 GEMMs on the serving
+    stream (about 1.5x the per-layer transfer time per layer), as a prefill
+    would interleave them."""
     from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
     from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
 
@@ -318,29 +324,66 @@ def store_pipeline(torch, layers, cache, src_slots, args):
     H, D = cache.row_shape
     nbytes = L * 2 * T * H * D * 2
     slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=128)
+    a = torch.randn(4096, 4096, device=layers[0].device, dtype=torch.bfloat16)
+    b = torch.randn_like(a)
+    c = torch.empty_like(a)
+    rep_id = [0]
+
+    def once(mode, gemms=0):
+        use_slab = mode != "reference"
+        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if use_slab else None)
+        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2,
+                                   slab=slab if use_slab else None,
+                                   slab_transfer=mode if use_slab else "dma")
+        r = rep_id[0]
+        rep_id[0] += 1
+        request = RequestMetadata(f"{mode}{r}", list(range(r * T, r * T + T)), slots_cpu, None, True, T)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for l in range(L):
+            for _ in range(gemms):
+                torch.mm(a, b, out=c)
+            writer.save_layer(l, layers[l], [request])
+        writer.wait_for_save()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
+        writer.close()
+        store.clear()
+        return elapsed, committed
+
     result = {"layers": L, "tokens": T, "bytes_d2h": nbytes}
-    for mode in ("fused", "staged"):
-        times = []
-        for rep in range(4):
-            store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if mode == "fused" else None)
-            writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2,
-                                       slab=slab if mode == "fused" else None)
-            request = RequestMetadata(f"{mode}{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None,
-                                      True, T)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for l in range(L):
-                writer.save_layer(l, layers[l], [request])
-            writer.wait_for_save()
-            times.append(time.perf_counter() - t0)
-            committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
-            writer.close()
-            store.clear()
-            del store, writer
-        best = min(times[1:])  # rep 0 also pins the slab's arenas / warms the pools
-        result[mode] = {"ms": round(best * 1e3, 3), "first_rep_ms": round(times[0] * 1e3, 3),
-                        "chunks_committed": committed, "d2h_GBps": round(nbytes / best / 1e9, 2),
+    for mode in ("host_write", "dma", "reference"):
+        times = [once(mode) for _ in range(4)]
+        best = min(t for t, _ in times[1:])  # rep 0 also pins the slab's arenas / warms the pools
+        result[mode] = {"ms": round(best * 1e3, 3), "first_rep_ms": round(times[0][0] * 1e3, 3),
+                        "chunks_committed": times[-1][1], "d2h_GBps": round(nbytes / best / 1e9, 2),
                         "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4)}
+    # overlap with compute
+    torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    gemm_s = (time.perf_counter() - t0) / 20
+    per_layer = result["host_write"]["ms"] / 1e3 / L
+    reps = max(1, int(round(1.5 * per_layer / gemm_s)))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(L * reps):
+        torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    compute_s = time.perf_counter() - t0
+    result["with_gemm_compute"] = {"compute_only_ms": round(compute_s * 1e3, 3),
+                                   "compute_per_layer": f"{reps} x bf16 GEMM 4096^3"}
+    for mode in ("host_write", "dma"):
+        once(mode, reps)
+        total = min(once(mode, reps)[0] for _ in range(2))
+        alone = result[mode]["ms"] / 1e3
+        result["with_gemm_compute"][mode] = {
+            "total_ms": round(total * 1e3, 3),
+            "store_hidden_frac": round(1.0 - max(0.0, total - compute_s) / alone, 4)}
     result["slab"] = slab.stats()
     slab.close()
     return result
@@ -427,12 +470,10 @@ def blend_load(torch, synthetic, dev, args):
 
     rope = Rope()
     cfg = CacheBlendConfig.from_extra_config({})
-    load_stream = torch.cuda.Stream()
     h2d_bytes = L * hit * 2 * H * D * 2
 
     def run(store, plan, zero_copy, compute=None):
-        loader = PagedBlendLoader(layers, store, "blend", plan, slots, BS, cfg, load_stream=load_stream,
-                                  zero_copy=zero_copy)
+        loader = PagedBlendLoader(layers, store, "blend", plan, slots, BS, cfg, zero_copy=zero_copy)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         loader.prefetch(0, rope)

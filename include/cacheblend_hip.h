@@ -128,6 +128,10 @@ int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int
  */
 int cbk_slab_create(size_t chunk_bytes, size_t chunks_per_arena, size_t max_bytes, void** out_handle);
 int cbk_slab_alloc(void* handle, void** out_chunk);
+/* n slots into out_chunks[0..n): consecutive in one arena when a run of n
+ * free slots exists or a new arena can hold it (n <= chunks_per_arena), so
+ * one DMA copy can fill them; otherwise the lowest free slots. All or none. */
+int cbk_slab_alloc_run(void* handle, int64_t n, void** out_chunks);
 int cbk_slab_free(void* handle, void* chunk);
 int cbk_slab_stats(void* handle, size_t* arenas, size_t* free_chunks, size_t* live_chunks);
 int cbk_slab_destroy(void* handle);
@@ -139,6 +143,21 @@ int cbk_slab_destroy(void* handle);
  * host-chunk entry points (cbk_paged_gather_chunks, cbk_blend_assemble_chunks).
  */
 int cbk_host_accessible(const void* ptr, size_t bytes, int* accessible);
+
+/*
+ * Up to n non-blocking side streams (*found of them) that run concurrently
+ * with `serving` and with each other, measured: HIP maps streams onto a few
+ * hardware queues (GPU_MAX_HW_QUEUES) round-robin in creation order, and
+ * streams sharing a queue execute in order. Each of up to max_candidates new
+ * streams is kept when a spin of spin_ms on it overlaps spins on `serving`
+ * and on every stream kept so far. Synchronizes `serving` first. The Load,
+ * copy and Store side streams of the layerwise pipelines (the reference
+ * creates them with torch.npu.Stream(), cacheblend_vllm/connector.py:198-199,
+ * ascend.py:212). Release with cbk_stream_destroy.
+ */
+int cbk_side_streams(cbk_stream_t serving, int32_t n, int32_t max_candidates, float spin_ms,
+                     cbk_stream_t* out_streams, int32_t* found);
+int cbk_stream_destroy(cbk_stream_t stream);
 
 /*
  * n asynchronous copies dst[i] <- src[i] of bytes[i] bytes on `stream`

@@ -95,6 +95,7 @@ _SIGNATURES = {
     ),
     "cbk_slab_create": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(c_vp)]),
     "cbk_slab_alloc": (ctypes.c_int, [c_vp, ctypes.POINTER(c_vp)]),
+    "cbk_slab_alloc_run": (ctypes.c_int, [c_vp, c_i64, ctypes.POINTER(c_vp)]),
     "cbk_slab_free": (ctypes.c_int, [c_vp, c_vp]),
     "cbk_slab_stats": (
         ctypes.c_int,
@@ -103,6 +104,9 @@ _SIGNATURES = {
     "cbk_slab_destroy": (ctypes.c_int, [c_vp]),
     "cbk_host_accessible": (ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(c_i32)]),
     "cbk_memcpy_runs": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "cbk_side_streams": (ctypes.c_int, [c_vp, c_i32, c_i32, ctypes.c_float, ctypes.POINTER(c_vp),
+                                        ctypes.POINTER(c_i32)]),
+    "cbk_stream_destroy": (ctypes.c_int, [c_vp]),
     "cbk_blend_assemble_chunks": (
         ctypes.c_int,
         [
@@ -123,11 +127,17 @@ _SIGNATURES = {
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
 _lock = threading.Lock()
-_lib: ctypes.CDLL | None = None
+_lib: ctypes.PyDLL | None = None
 
 
-def load() -> ctypes.CDLL:
-    """Load the HIP library once; raise if it is missing or mismatched."""
+def load() -> ctypes.PyDLL:
+    """Load the HIP library once; raise if it is missing or mismatched.
+
+    Loaded as a PyDLL: calls keep the GIL. Every entry point is a short
+    enqueue (or a rare set-up call), and a ctypes call that released the
+    GIL would, on return, wait out another Python thread's switch interval
+    (5 ms by default) -- with the store publisher threads busy in Python,
+    that stalled each save_kv_layer by milliseconds."""
     global _lib
     if _lib is not None:
         return _lib
@@ -139,7 +149,7 @@ def load() -> ctypes.CDLL:
                 f"{LIB_NAME} is not built at {LIB_PATH}; run `make -C pic-kvcache_amd/csrc` "
                 "(hipcc --offload-arch=gfx950). cacheblend_vllm has no CPU fallback."
             )
-        lib = ctypes.CDLL(LIB_PATH)
+        lib = ctypes.PyDLL(LIB_PATH)
         for name, (restype, argtypes) in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = restype

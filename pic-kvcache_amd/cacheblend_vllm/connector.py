@@ -24,7 +24,8 @@ from typing import Any
 import torch
 
 from .config import CacheBlendConfig
-from .host_store import PinnedChunkStore
+from .host_store import PinnedChunkSlab, PinnedChunkStore
+from .kv_layout import kv_planes
 from .loader import PagedBlendLoader
 from .store_path import (  # noqa: F401 - re-exported reference names
     CacheBlendConnectorMetadata,
@@ -32,6 +33,7 @@ from .store_path import (  # noqa: F401 - re-exported reference names
     StoreStreamWriter,
     _slot_mapping,
 )
+from .streams import LOAD, side_stream
 from .trace import PipelineTracer
 
 try:  # vLLM's connector base when vLLM is installed
@@ -90,6 +92,7 @@ class CacheBlendConnectorV1(_Base):
         self._trace = PipelineTracer("scheduler" if role is KVConnectorRole.SCHEDULER else "worker")
         self._store: PinnedChunkStore | None = None
         self._writer: StoreStreamWriter | None = None
+        self._slab: PinnedChunkSlab | None = None
         self._kv_caches: list = []
         self._layer_ids: dict[str, int] = {}
         self._executor = None
@@ -109,12 +112,19 @@ class CacheBlendConnectorV1(_Base):
         self._kv_caches = [value for _, value in ordered]
         if not self._kv_caches:
             raise RuntimeError("CacheBlendConnectorV1 received no KV caches")
-        self._store = PinnedChunkStore(self.config.chunk_size, self.config.max_local_cpu_bytes)
-        self._load_stream = torch.cuda.Stream()
+        key, _ = kv_planes(self._kv_caches[0])
+        # chunks live in pinned slab slots (one pinned arena per 128 chunks,
+        # bounded by the store's byte cap) instead of a fresh pinned batch per
+        # layer; slots go back to the slab when the store drops a segment
+        self._slab = PinnedChunkSlab((2, self.config.chunk_size, *key.shape[2:]), key.dtype,
+                                     chunks_per_arena=128, max_bytes=0)
+        self._store = PinnedChunkStore(self.config.chunk_size, self.config.max_local_cpu_bytes,
+                                       on_release=self._slab.free)
+        self._load_stream = side_stream(LOAD, key.device)
         self._writer = StoreStreamWriter(
             self._store, self.block_size, self.config.chunk_size, len(self._kv_caches),
             self.model_scope, self.config.store_workers, self.config.max_inflight_store_batches,
-            tracer=self._trace,
+            tracer=self._trace, slab=self._slab,
         )
         self._executor = executor
         self._trace.emit("worker_registered", rank=0, layers=len(self._kv_caches),
@@ -196,6 +206,9 @@ class CacheBlendConnectorV1(_Base):
             self._writer = None
         if self._store is not None:
             self._store.clear()
+        if self._slab is not None:
+            self._slab.close()
+            self._slab = None
         self._trace.close()
 
     # ------------------------------------------------------- scheduler

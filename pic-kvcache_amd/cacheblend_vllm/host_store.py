@@ -129,6 +129,24 @@ class PinnedChunkSlab:
                 self._tensors[ptr.value] = tensor
             return tensor
 
+    def alloc_run(self, n: int) -> list[torch.Tensor]:
+        """``n`` slots, consecutive in host memory whenever the slab can
+        (``cbk_slab_alloc_run``), so one DMA copy can fill them in order."""
+        with self._lock:
+            if self._pending:
+                self._reclaim()
+            ptrs = (ctypes.c_void_p * n)()
+            _native.check(_native.load().cbk_slab_alloc_run(self._handle, n, ptrs), "slab alloc_run")
+            out = []
+            for p in ptrs:
+                tensor = self._tensors.get(p)
+                if tensor is None:
+                    raw = (ctypes.c_uint8 * self.nbytes).from_address(p)
+                    tensor = torch.frombuffer(raw, dtype=torch.uint8).view(self.dtype).view(self.chunk_shape)
+                    self._tensors[p] = tensor
+                out.append(tensor)
+            return out
+
     def free(self, tensor: torch.Tensor, event=None) -> None:
         with self._lock:
             self._pending.append((tensor.data_ptr(), event))

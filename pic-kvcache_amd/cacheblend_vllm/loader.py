@@ -39,6 +39,7 @@ from . import _native
 from .config import CacheBlendConfig
 from .kv_layout import kv_desc, kv_planes
 from .rope import cos_sin_table, rope_style
+from .streams import COPY, LOAD, side_stream
 from .trace import PipelineTracer
 from .types import BlendPlan
 
@@ -118,6 +119,7 @@ class PagedBlendLoader:
         config: CacheBlendConfig,
         tracer: PipelineTracer | None = None,
         load_stream: torch.cuda.Stream | None = None,
+        copy_stream: torch.cuda.Stream | None = None,
         zero_copy: bool | str = "auto",
         max_workgroups: int = 256,
         dma_min_run_bytes: int = 1 << 20,
@@ -167,7 +169,11 @@ class PagedBlendLoader:
         self._events: dict[int, torch.cuda.Event] = {}
         self._reuse_events: dict[int, torch.cuda.Event] = {}
         self._staging: list[torch.Tensor] = []
-        self._hit_staging: torch.Tensor | None = None
+        # hit staging by layer parity, so layer l + 1's DMA (on the copy
+        # stream) overlaps layer l's assembly; _hit_free[i] fences reuse
+        self._hit_stagings: list[torch.Tensor | None] = [None, None]
+        self._hit_free: dict[int, torch.cuda.Event] = {}
+        self._copy_stream: torch.cuda.Stream | None = None
         self._descs: dict[int, _native.KVDesc] = {}
         self._zero_copy = zero_copy
         self._max_workgroups = max_workgroups
@@ -177,7 +183,8 @@ class PagedBlendLoader:
         self._zc_layers: set[int] = set()
         self._load_stream = None
         if config.event_pipeline:
-            self._load_stream = load_stream or torch.cuda.Stream(self.device)
+            self._load_stream = load_stream or side_stream(LOAD, self.device)
+            self._copy_stream = copy_stream or side_stream(COPY, self.device)
             # tables made on the current stream are read on the Load stream
             for table in (self._src_map, self._old_pos, self._slots):
                 if table is not None:
@@ -236,12 +243,14 @@ class PagedBlendLoader:
             off += n
         return [tuple(r) for r in runs]
 
-    def _ensure_hit_staging(self) -> torch.Tensor:
-        if self._hit_staging is None:
-            self._hit_staging = torch.empty(
-                (2, self.plan.hit_tokens, *self.row_shape), dtype=self.dtype, device=self.device
-            )
-        return self._hit_staging
+    def _ensure_hit_staging(self, layer_id: int) -> torch.Tensor:
+        index = layer_id % 2
+        if self._hit_stagings[index] is None:
+            staging = torch.empty((2, self.plan.hit_tokens, *self.row_shape), dtype=self.dtype, device=self.device)
+            if self._copy_stream is not None:
+                staging.record_stream(self._copy_stream)
+            self._hit_stagings[index] = staging
+        return self._hit_stagings[index]
 
     def _load_hits(self, layer_id: int) -> None:
         found = self._chunk_addresses(layer_id)
@@ -265,7 +274,7 @@ class PagedBlendLoader:
                 self._zc_chunk = chunk
                 return
             self._zc_layers.discard(layer_id)
-            hit = self._ensure_hit_staging()
+            hit = self._ensure_hit_staging(layer_id)
             kb, vb = hit[0].data_ptr(), hit[1].data_ptr()
             n = 2 * len(runs)
             dst = (ctypes.c_uint64 * n)()
@@ -274,19 +283,34 @@ class PagedBlendLoader:
             for i, (off, tokens, k, v) in enumerate(runs):
                 dst[2 * i], src[2 * i], nbytes[2 * i] = kb + off * row_bytes, k, tokens * row_bytes
                 dst[2 * i + 1], src[2 * i + 1], nbytes[2 * i + 1] = vb + off * row_bytes, v, tokens * row_bytes
-            _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n, _native.stream_handle(self.device)),
+            if self._load_stream is None:
+                _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n,
+                                                             _native.stream_handle(self.device)), "hit runs H2D")
+                return
+            # DMA on the copy stream: waits only for the assembly that last
+            # read this staging, so it runs behind the previous layer's copy
+            # instead of behind its assembly
+            free = self._hit_free.pop(layer_id % 2, None)
+            if free is not None:
+                self._copy_stream.wait_event(free)
+            else:
+                self._copy_stream.wait_stream(self._load_stream)  # staging allocated there
+            _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n, self._copy_stream.cuda_stream),
                           "hit runs H2D")
+            copied = torch.cuda.Event()
+            copied.record(self._copy_stream)
+            self._load_stream.wait_event(copied)
             return
         self._zc_layers.discard(layer_id)
         hosts = [self.store.get_layer(self.request_id, seg, layer_id) for seg in self.plan.segments]
-        hit = self._ensure_hit_staging()
+        hit = self._ensure_hit_staging(layer_id)
         for off, n, k, v in coalesce_host_runs(hosts):
             hit[0, off : off + n].copy_(k, non_blocking=True)
             hit[1, off : off + n].copy_(v, non_blocking=True)
 
     def _assemble(self, layer_id: int, buffer: torch.Tensor, rotary_emb) -> None:
         es = buffer.element_size()
-        hit = self._hit_staging
+        hit = self._hit_stagings[layer_id % 2]
         heads = int(np.prod(self.row_shape[:-1])) if len(self.row_shape) > 1 else 1
         head_dim = self.row_shape[-1]
         table = None
@@ -381,6 +405,10 @@ class PagedBlendLoader:
             if self.plan.segments:
                 self._load_hits(layer_id)
             self._assemble(layer_id, buffer, rotary_emb)
+            if self._copy_stream is not None and self._hit_stagings[index] is not None:
+                done = torch.cuda.Event()
+                done.record(self._load_stream)
+                self._hit_free[index] = done
             self._buffers[layer_id] = buffer
 
         if self._load_stream is None:

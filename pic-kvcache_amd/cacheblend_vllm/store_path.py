@@ -7,13 +7,21 @@ gfx950 paged-gather kernel and the copies on a HIP side stream:
   save_kv_layer(layer)      per request: complete chunk_size chunks up to
                             save_end, one reservation per (chunk, layer),
                             one fused slot list over every pending chunk
-  _enqueue_store_batch      Store stream: wait for the serving stream,
-                            gather into the request's reused device staging,
-                            pinned D2H, record an event, hand the batch to a
-                            publisher thread (backpressure semaphore)
+  _enqueue_store_batch      Store stream: wait for the serving stream, then
+                            with a pinned chunk slab: slots allocated as
+                            consecutive runs, filled either by gather into a
+                            chunk-major device staging + one D2H per run
+                            ("dma") or by the gather kernel writing the
+                            slots over the host link ("host_write");
+                            without one: gather into the request's reused
+                            staging + D2H into a freshly pinned batch, as
+                            the reference does. Then an event, and the batch
+                            goes to a publisher thread (backpressure
+                            semaphore)
   _publish_after_event      publisher thread: event.synchronize(), then put
-                            per-chunk views of the pinned batch into the store;
-                            any failure aborts every chunk of the batch
+                            the per-chunk slots (or views of the batch) into
+                            the store; any failure aborts every chunk of the
+                            batch
   wait_for_save             Store-stream sync + join publishers; staging freed
 
 Everything enqueued goes to one default-priority Store stream, so the D2H of
@@ -23,6 +31,7 @@ stream keeps computing.
 
 from __future__ import annotations
 
+import ctypes
 import threading
 import time
 from concurrent.futures import Future, ThreadPoolExecutor
@@ -31,10 +40,9 @@ from typing import Any
 
 import torch
 
-import ctypes
-
 from . import _native
 from .kv_layout import gather_paged_kv, kv_desc, kv_planes
+from .streams import STORE, side_stream
 from .trace import PipelineTracer
 from .types import BlendPlan, SegmentId
 
@@ -81,7 +89,7 @@ class CudaStreams:
 
     @staticmethod
     def Stream():  # noqa: N802
-        return torch.cuda.Stream()
+        return side_stream(STORE)
 
 
 class StoreStreamWriter:
@@ -101,13 +109,25 @@ class StoreStreamWriter:
         store_stream=None,
         slab=None,
         max_workgroups: int = 128,
+        slab_transfer: str = "host_write",
     ):
-        """``slab`` (a PinnedChunkSlab): the fused path -- each chunk is written
-        by the gather kernel straight into its own pinned slot (no device
-        staging, no DMA, no per-layer pinning); None: gather into device
-        staging + one pinned D2H per layer, as the reference does."""
+        """``slab`` (a PinnedChunkSlab): every chunk gets its own pinned slot,
+        allocated as consecutive runs, so no pinned memory is allocated per
+        layer. ``slab_transfer`` picks how the bytes get there:
+        "host_write" -- (default) the gather kernel writes the slots
+                        directly over the host link: no staging, one launch
+                        per layer, holding up to ``max_workgroups``
+                        workgroups for the transfer;
+        "dma"        -- gather into a chunk-major device staging, then one
+                        hipMemcpyAsync per run of consecutive slots (HIP
+                        runs it as its own copy kernel).
+        None: gather into device staging + one pinned D2H per layer into a
+        freshly pinned batch, as the reference does."""
+        if slab_transfer not in ("dma", "host_write"):
+            raise ValueError("slab_transfer must be 'dma' or 'host_write'")
         self._store = store
         self._slab = slab
+        self._slab_transfer = slab_transfer
         self._max_workgroups = max_workgroups
         self.block_size = block_size
         self.chunk_size = chunk_size
@@ -199,8 +219,11 @@ class StoreStreamWriter:
                 self._store_stream.wait_stream(current)
                 slots = self._upload_slots(request_id, slots, kv_layer)
                 if self._slab is not None:
-                    host = [self._slab.alloc() for _ in pending]
-                    self._gather_to_chunks(kv_layer, slots, host)
+                    host = self._slab.alloc_run(len(pending))
+                    if self._slab_transfer == "host_write":
+                        self._gather_to_chunks(kv_layer, slots, [h.data_ptr() for h in host])
+                    else:
+                        self._gather_then_dma(request_id, kv_layer, slots, host)
                 else:
                     staging = self._store_staging_by_request.get(request_id)
                     if staging is None or staging.shape[1] != slots.numel():
@@ -248,21 +271,50 @@ class StoreStreamWriter:
         self._device_slots[request_id] = (host, device)
         return device
 
-    def _gather_to_chunks(self, kv_layer: Any, slots: torch.Tensor, chunks: list[torch.Tensor]) -> None:
-        """cbk_paged_gather_chunks: the layer's pending tokens straight into
-        their pinned chunk slots, on the current (Store) stream."""
+    def _gather_to_chunks(self, kv_layer: Any, slots: torch.Tensor, chunk_ptrs: list[int]) -> None:
+        """cbk_paged_gather_chunks: the layer's pending tokens into chunks
+        ``[2, chunk, *row]`` at ``chunk_ptrs`` (pinned host slots or device
+        staging), on the current (Store) stream."""
         desc, key = kv_desc(kv_layer, self.block_size)
-        n = len(chunks)
-        plane = chunks[0].stride(0) * chunks[0].element_size()
-        k_list = [c.data_ptr() for c in chunks]
-        k_ptrs = (ctypes.c_void_p * n)(*k_list)
-        v_ptrs = (ctypes.c_void_p * n)(*[k + plane for k in k_list])
-        row_bytes = desc.row_bytes
+        n = len(chunk_ptrs)
+        plane = self.chunk_size * desc.row_bytes
+        k_ptrs = (ctypes.c_void_p * n)(*chunk_ptrs)
+        v_ptrs = (ctypes.c_void_p * n)(*[k + plane for k in chunk_ptrs])
         rc = _native.load().cbk_paged_gather_chunks(
-            desc, slots.data_ptr(), slots.numel(), chunks[0].shape[1], k_ptrs, v_ptrs, row_bytes,
+            desc, slots.data_ptr(), slots.numel(), self.chunk_size, k_ptrs, v_ptrs, desc.row_bytes,
             self._max_workgroups, None, _native.stream_handle(key.device),
         )
         _native.check(rc, "gather to chunks")
+
+    def _gather_then_dma(self, request_id: str, kv_layer: Any, slots: torch.Tensor,
+                         host: list[torch.Tensor]) -> None:
+        """Gather into a chunk-major device staging laid out like the slots
+        (``chunk_bytes`` apart), then one D2H copy per run of consecutive
+        slots, all on the current (Store) stream."""
+        stride = self._slab.chunk_bytes
+        n = len(host)
+        staging = self._store_staging_by_request.get(request_id)
+        if staging is None or staging.numel() != n * stride:
+            if staging is not None:
+                self._retired_store_staging.append(staging)  # an earlier copy may still read it
+            key, _ = kv_planes(kv_layer)
+            staging = torch.empty(n * stride, dtype=torch.uint8, device=key.device)
+            self._store_staging_by_request[request_id] = staging
+        base = staging.data_ptr()
+        self._gather_to_chunks(kv_layer, slots, [base + i * stride for i in range(n)])
+        runs: list[list[int]] = []
+        for i, h in enumerate(host):
+            p = h.data_ptr()
+            if runs and p == runs[-1][0] + runs[-1][2]:
+                runs[-1][2] += stride
+            else:
+                runs.append([p, base + i * stride, stride])
+        m = len(runs)
+        dst = (ctypes.c_uint64 * m)(*[r[0] for r in runs])
+        src = (ctypes.c_uint64 * m)(*[r[1] for r in runs])
+        nbytes = (ctypes.c_uint64 * m)(*[r[2] for r in runs])
+        _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, m, _native.stream_handle(staging.device)),
+                      "chunk runs D2H")
 
     def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host, accepted=None) -> bool:
         """Per-chunk host tensors into the store (connector.py:449-466): views

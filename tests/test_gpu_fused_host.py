@@ -50,15 +50,41 @@ def test_slab_slots_are_pinned_recycled_and_bounded():
     slab.close()
 
 
+def test_slab_runs_are_consecutive_and_fall_back_when_fragmented():
+    slab = PinnedChunkSlab((2, 16, 2, 64), torch.bfloat16, chunks_per_arena=8)
+    stride = slab.chunk_bytes
+    run = slab.alloc_run(5)
+    assert [t.data_ptr() - run[0].data_ptr() for t in run] == [i * stride for i in range(5)]
+    other = slab.alloc_run(3)  # fills the arena
+    assert other[0].data_ptr() == run[-1].data_ptr() + stride
+    for t in run[1::2]:
+        slab.free(t)  # arena 0 now has free slots 1 and 3 only
+    run2 = slab.alloc_run(4)  # no run of 4 there: a fresh arena holds it
+    assert slab.stats()["arenas"] == 2
+    assert [t.data_ptr() - run2[0].data_ptr() for t in run2] == [i * stride for i in range(4)]
+    single = slab.alloc_run(2)  # the two free slots of arena 0 are not adjacent: first run in arena 1
+    assert single[1].data_ptr() == single[0].data_ptr() + stride
+    live = run[0::2] + other + run2 + single
+    assert slab.stats()["live"] == len(live)
+    big = slab.alloc_run(10)  # longer than an arena: scattered lowest slots, new arenas as needed
+    assert len({t.data_ptr() for t in big}) == 10
+    for t in live + big:
+        slab.free(t)
+    st = slab.stats()
+    assert st["live"] == 0 and st["free"] == 8 * st["arenas"]
+    slab.close()
+
+
+@pytest.mark.parametrize("transfer", ["dma", "host_write"])
 @pytest.mark.parametrize("layout", ["merged_first", "merged_block"])
-def test_fused_store_writes_chunks_bit_exact(layout):
+def test_fused_store_writes_chunks_bit_exact(layout, transfer):
     L, NB, BS, H, D, CH, T = 3, 128, 16, 8, 128, 256, 1000
     pools = [synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=40 + l) for l in range(L)]
     layers = pools if layout == "merged_first" else [p.transpose(0, 1).contiguous() for p in pools]
     slots = synthetic.block_slots(torch.randperm(NB)[: (T + BS - 1) // BS], BS, T)
     slab = PinnedChunkSlab((2, CH, H, D), torch.bfloat16, chunks_per_arena=8)
     store = PinnedChunkStore(CH, 1 << 34, on_release=slab.free)
-    writer = StoreStreamWriter(store, BS, CH, L, "m", slab=slab, max_workgroups=32)
+    writer = StoreStreamWriter(store, BS, CH, L, "m", slab=slab, max_workgroups=32, slab_transfer=transfer)
     request = RequestMetadata("a", list(range(T)), slots, None, True, T)  # 3 full chunks of 256
     for l in range(L):
         writer.save_layer(l, layers[l], [request])
