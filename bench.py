@@ -588,9 +588,90 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     absolute = torch.arange(nk, device=dev)
     for _ in range(max(1, args.steps // 2)):
         S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, out_index=absolute)
+    del query, key
+    _profile_host_link(torch, synthetic, cache, src_slots, args, dev)
     torch.cuda.synchronize()
-    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select), sparse_q")
+    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select, "
+        "store gather into host chunks, blend assembly from host chunks), sparse_q")
     return 0
+
+
+def _profile_host_link(torch, synthetic, cache, src_slots, args, dev):
+    """Host-link kernels, --steps launches each:
+    gather_chunks_kernel -- one Qwen3-8B layer of the 8192-token prompt
+        (32 chunks, 33,554,432 B) written into pinned slab slots;
+    assemble_rows_kernel -- one Qwen3-30B-A3B-shaped blend layer: 27,904 hit
+        rows (57,147,392 B) read in place from 109 pinned chunks, RoPE
+        relocation, APC prefix gather, gap zeroing (allocation_end 32767)."""
+    import ctypes
+
+    from cacheblend_vllm import _native
+    from cacheblend_vllm.config import CacheBlendConfig
+    from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
+    from cacheblend_vllm.kv_layout import kv_desc
+    from cacheblend_vllm.loader import PagedBlendLoader
+    from cacheblend_vllm.types import BlendPlan, BlendSegment
+
+    H, D = cache.row_shape
+    slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=32)
+    slots_dev = src_slots.to(dev)
+    desc, _ = kv_desc(cache.kv_layers[0], cache.block_size)
+    chunks = slab.alloc_run(32)
+    plane = 256 * desc.row_bytes
+    k_ptrs = (ctypes.c_void_p * 32)(*[c.data_ptr() for c in chunks])
+    v_ptrs = (ctypes.c_void_p * 32)(*[c.data_ptr() + plane for c in chunks])
+    lib = _native.load()
+    for _ in range(args.steps):
+        _native.check(lib.cbk_paged_gather_chunks(desc, slots_dev.data_ptr(), src_slots.numel(), 256, k_ptrs,
+                                                  v_ptrs, desc.row_bytes, 128, None,
+                                                  _native.stream_handle(dev)), "profile gather_chunks")
+    torch.cuda.synchronize()
+    for c in chunks:
+        slab.free(c)
+    slab.close()
+
+    L, BS, H3, A, APC = 1, 16, 4, 32767, 2048
+    rng = np.random.default_rng(0)
+    gaps = rng.integers(1, 512, 12)
+    total = (A - APC - int(gaps.sum())) // 256
+    lens = 1 + rng.multinomial(total - 12, np.full(12, 1 / 12))
+    nb = (A + BS - 1) // BS + 8
+    pages = synthetic.paged_pool(nb, BS, H3, D, torch.bfloat16, dev, seed=5)
+    slab3 = PinnedChunkSlab((2, 256, H3, D), torch.bfloat16, chunks_per_arena=128)
+    store = PinnedChunkStore(256, 1 << 40, on_release=slab3.free)
+    segments, pos, src = [], APC, 0
+    for i, (g, m) in enumerate(zip(gaps, lens)):
+        pos += int(g)
+        for c in range(int(m)):
+            sid = store.begin_put("p", src + 256 * c, list(range(src + 256 * c + 7 * i, src + 256 * c + 7 * i + 256)), L)
+            slot = slab3.alloc()
+            slot.copy_(torch.randn(slot.shape, dtype=torch.float32).to(torch.bfloat16))
+            store.put_layer_host(sid, 0, slot)
+            segments.append(BlendSegment(sid, pos + 256 * c))
+        src += 256 * int(m) + 512
+        pos += 256 * int(m)
+    store.pin("p", segments)
+    plan = BlendPlan(APC, A, sum(s.length for s in segments), tuple(segments))
+    slots = synthetic.block_slots(torch.randperm(nb, generator=torch.Generator().manual_seed(1))[: (A + BS - 1) // BS],
+                                  BS, A)
+
+    class Rope:
+        head_size = rotary_dim = D
+        is_neox_style = True
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+        ang = torch.arange(65536, dtype=torch.float32)[:, None] * inv
+        cos_sin_cache = torch.cat([ang.cos(), ang.sin()], -1).to(dev)
+
+    rope = Rope()
+    cfg = CacheBlendConfig.from_extra_config({})
+    for _ in range(args.steps):
+        loader = PagedBlendLoader([pages], store, "p", plan, slots, BS, cfg, zero_copy=True)
+        loader.prefetch(0, rope)
+        loader.get(0)
+    torch.cuda.synchronize()
+    store.release("p")
+    store.clear()
+    slab3.close()
 
 
 def _kdev_async(torch, S, fresh, cached, gap):
