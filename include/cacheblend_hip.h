@@ -74,6 +74,10 @@ int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t nu
 
 /*
  * Paged scatter: {K,V}[slot_t / bs][slot_t % bs] = in_{k,v}[t].
+ * With kv->v_base and in_v_dev both NULL only the K plane moves (also for
+ * cbk_paged_gather with out_v_dev NULL); a block_size of 1 turns the
+ * descriptor into a plain row table, e.g. the row write-back
+ * flat_old_k[absolute_indices] = k (cacheblend_vllm/ascend.py:552, 592-593).
  * Replaces scatter_paged_kv(contiguous, kv_layer, slot_mapping, block_size)
  * (cacheblend_vllm/kv_layout.py:125-161) and reshape_and_cache
  * (kv_layout.py:137-146). Out-of-range slots are skipped and counted.

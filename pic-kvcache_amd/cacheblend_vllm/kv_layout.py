@@ -23,6 +23,7 @@ Differences from the reference torch path, on purpose:
 
 from __future__ import annotations
 
+import ctypes
 from collections.abc import Sequence
 
 import torch
@@ -292,6 +293,72 @@ def scatter_paged_kv_layers(
         _native.stream_handle(key.device),
     )
     _native.check(rc, "scatter_paged_kv_layers")
+
+
+def _row_table(t: torch.Tensor, what: str) -> tuple[int, int]:
+    """(row stride, row bytes) of a tensor whose dim 0 indexes rows and whose
+    remaining dims are contiguous."""
+    if t.dim() < 1 or not _rows_contiguous(t, 1):
+        raise ValueError(f"{what} rows must be contiguous after dim 0")
+    es = t.element_size()
+    return t.stride(0) * es, (t.numel() // max(1, t.shape[0])) * es
+
+
+def write_rows(dst: torch.Tensor, indices: torch.Tensor, src: torch.Tensor) -> None:
+    """``dst[indices] = src`` for a row table ``dst [R, ...]`` and ``src [T, ...]``
+    (same row shape and dtype, unique indices): the reference's
+    ``score_keys[absolute_indices] = k`` (cacheblend_vllm/ascend.py:552), one
+    ``cbk_paged_scatter`` launch over a block-size-1, K-only descriptor."""
+    _native.require_device(dst, "dst")
+    _native.require_device(src, "src")
+    if src.dtype != dst.dtype:
+        raise ValueError(f"src dtype {src.dtype} does not match dst dtype {dst.dtype}")
+    if indices.numel() != src.shape[0]:
+        raise ValueError(f"{indices.numel()} indices for {src.shape[0]} rows")
+    d_stride, row_bytes = _row_table(dst, "dst")
+    s_stride, s_row = _row_table(src, "src")
+    if s_row != row_bytes:
+        raise ValueError("src and dst rows differ in size")
+    if src.shape[0] == 0:
+        return
+    desc = _native.KVDesc(dst.data_ptr(), None, dst.shape[0], 1, d_stride, d_stride, row_bytes)
+    slots = _device_slots(indices, dst.device, dst.shape[0])
+    rc = _native.load().cbk_paged_scatter(src.data_ptr(), None, s_stride, ctypes.byref(desc),
+                                          slots.data_ptr(), src.shape[0], None,
+                                          _native.stream_handle(dst.device))
+    _native.check(rc, "write_rows")
+
+
+def write_back_kv(old_kv: torch.Tensor, indices: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """``old_kv[0][indices] = k`` and ``old_kv[1][indices] = v`` for the layer
+    buffer ``[2, A, H, D]`` and recomputed ``k``/``v`` ``[T, H*D]`` -- the
+    check layer's write-back (reference ascend.py:592-595) -- in one launch."""
+    _native.require_device(old_kv, "old_kv")
+    if old_kv.dim() < 3 or old_kv.shape[0] != 2:
+        raise ValueError("old_kv must be [2, tokens, ...]")
+    if k.shape != v.shape or k.dtype != old_kv.dtype or v.dtype != old_kv.dtype:
+        raise ValueError("k and v must have the same shape and the buffer's dtype")
+    if indices.numel() != k.shape[0]:
+        raise ValueError(f"{indices.numel()} indices for {k.shape[0]} rows")
+    planes_ok = _rows_contiguous(old_kv[0], 1) and _rows_contiguous(old_kv[1], 1)
+    if not planes_ok or old_kv[0].stride(0) != old_kv[1].stride(0):
+        raise ValueError("old_kv planes must hold contiguous rows with one row stride")
+    es = old_kv.element_size()
+    row_bytes = (old_kv[0].numel() // old_kv.shape[1]) * es
+    if k.numel() // max(1, k.shape[0]) * es != row_bytes:
+        raise ValueError("k/v rows do not match the buffer's rows")
+    if k.shape[0] == 0:
+        return
+    if not (_rows_contiguous(k, 1) and _rows_contiguous(v, 1)) or k.stride(0) != v.stride(0):
+        k, v = k.contiguous(), v.contiguous()
+    stride = old_kv.stride(1) * es
+    desc = _native.KVDesc(old_kv[0].data_ptr(), old_kv[1].data_ptr(), old_kv.shape[1], 1, stride, stride,
+                          row_bytes)
+    slots = _device_slots(indices, old_kv.device, old_kv.shape[1])
+    rc = _native.load().cbk_paged_scatter(k.data_ptr(), v.data_ptr(), k.stride(0) * es, ctypes.byref(desc),
+                                          slots.data_ptr(), k.shape[0], None,
+                                          _native.stream_handle(old_kv.device))
+    _native.check(rc, "write_back_kv")
 
 
 class PagedKVCache:

@@ -19,10 +19,13 @@ size the returned tensor, as the reference's ``torch.where`` does;
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from . import _native
 from .config import CacheBlendConfig
+from .kv_layout import write_rows
 
 
 def _mask_u8(mask: torch.Tensor, n: int, what: str) -> torch.Tensor:
@@ -269,6 +272,15 @@ def sparse_q_masks(gap_mask: torch.Tensor, tail_query_tokens: int, radius: int):
     return query_mask, forced, has_gap
 
 
+@dataclass
+class CheckLayerSelection:
+    """What the check layer's selection block produces (ascend.py:529-531)."""
+
+    deviation_selected: torch.Tensor | None
+    sparse_q_selected: torch.Tensor | None
+    sparse_q_stats: dict
+
+
 class BlendSelector:
     """The selection methods of the reference ``Qwen3BlendExecutor``.
 
@@ -350,6 +362,63 @@ class BlendSelector:
         ``_select`` with the forced (gap + overflow / tail) mask."""
         scores, forced, stats = self._sparse_q_scores(query, score_keys, absolute_indices, gap_mask, scale)
         return self._select(scores, gap_mask, layer_id, forced_mask=forced), stats
+
+    def check_layer(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        flat_old_k: torch.Tensor,
+        absolute_indices: torch.Tensor,
+        active_gap_mask: torch.Tensor,
+        layer_id: int,
+        scale: float,
+        num_heads: int,
+        num_kv_heads: int,
+        head_size: int,
+        strategy: str | None = None,
+        tracer=None,
+        request_id: str | None = None,
+    ) -> CheckLayerSelection:
+        """The selection part of the reference's check layer
+        (``Qwen3BlendExecutor._compute_layer``, ascend.py:533-580), for the
+        configured (or given) ``selection_strategy``:
+
+        kv_deviation -- K-deviation scores of the fresh ``k`` against
+                        ``flat_old_k[absolute_indices]``, then ``_select``;
+        sparse_q     -- ``flat_old_k[absolute_indices] = k`` in place (the
+                        reference aliases ``score_keys`` to ``flat_old_k``),
+                        Sparse-Q scores against it, then ``_select`` with the
+                        forced mask;
+        compare      -- both, Sparse-Q on a copy of ``flat_old_k``, and a
+                        ``selection_compared`` trace event.
+        The caller applies the result as the reference does: K-deviation
+        (and compare) prune before the check-layer attention, Sparse-Q after.
+        """
+        strategy = strategy or self.config.selection_strategy
+        if strategy not in ("kv_deviation", "sparse_q", "compare"):
+            raise ValueError(f"unknown selection strategy {strategy!r}")
+        result = CheckLayerSelection(None, None, {})
+        if strategy in ("kv_deviation", "compare"):
+            result.deviation_selected = self.kv_deviation_select(
+                k, flat_old_k, absolute_indices, active_gap_mask, layer_id)
+        if strategy in ("sparse_q", "compare"):
+            score_keys = flat_old_k if strategy == "sparse_q" else flat_old_k.clone()
+            write_rows(score_keys, absolute_indices, k.reshape(k.shape[0], -1))
+            result.sparse_q_selected, result.sparse_q_stats = self.sparse_q_select(
+                q.reshape(-1, num_heads, head_size), score_keys.view(-1, num_kv_heads, head_size),
+                absolute_indices, active_gap_mask, scale, layer_id)
+        if strategy == "compare" and tracer is not None and tracer.enabled:
+            dev, sq = result.deviation_selected, result.sparse_q_selected
+            size = max(int(dev.max()) if dev.numel() else -1, int(sq.max()) if sq.numel() else -1) + 1
+            a = torch.zeros(size, dtype=torch.bool, device=dev.device)
+            b = torch.zeros_like(a)
+            a[dev] = True
+            b[sq] = True
+            overlap, union = int((a & b).sum()), int((a | b).sum())
+            tracer.emit("selection_compared", request_id=request_id, layer_id=layer_id,
+                        deviation_tokens=dev.numel(), sparse_q_tokens=sq.numel(), overlap_tokens=overlap,
+                        jaccard=overlap / max(union, 1), **result.sparse_q_stats)
+        return result
 
     def kv_deviation_select(
         self,

@@ -42,6 +42,7 @@ struct PagedArgs {
   int64_t token_stride;     // page side, bytes
   int32_t* bad;             // optional out-of-range slot counter
   uint32_t num_tokens;
+  uint32_t planes;          // 2: K and V; 1: K only
   uint32_t row_vecs;
   uint32_t num_slots;
   FastDiv row_div;          // by row_vecs
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a)
   const char* kb = a.k_base[layer];
   const char* vb = a.v_base[layer];
   char* cb = a.c_base + int64_t(layer) * a.c_layer_stride;
-  const uint32_t total = a.num_tokens * 2u * a.row_vecs;
+  const uint32_t total = a.num_tokens * a.planes * a.row_vecs;
   const uint32_t f0 = blockIdx.x * uint32_t(kThreads * kUnroll) + threadIdx.x;
 
   const char* page[kUnroll];
@@ -177,9 +178,9 @@ __global__ __launch_bounds__(kChunkThreads) void gather_chunks_kernel(const Chun
   }
 }
 
-int validate_desc(const cbk_kv_desc* kv) {
+int validate_desc(const cbk_kv_desc* kv, int planes = 2) {
   CBK_REQUIRE(kv != nullptr, "kv descriptor is NULL");
-  CBK_REQUIRE(kv->k_base != nullptr && kv->v_base != nullptr, "kv base pointer is NULL");
+  CBK_REQUIRE(kv->k_base != nullptr && (kv->v_base != nullptr || planes == 1), "kv base pointer is NULL");
   CBK_REQUIRE(kv->num_blocks > 0 && kv->block_size > 0, "num_blocks and block_size must be positive");
   CBK_REQUIRE(kv->row_bytes > 0, "row_bytes must be positive");
   CBK_REQUIRE(kv->num_blocks * kv->block_size < (int64_t(1) << 32),
@@ -192,9 +193,9 @@ int validate_desc(const cbk_kv_desc* kv) {
 
 int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const int64_t* slots,
                  int64_t num_tokens, char* c_base, int64_t c_layer_stride, int64_t c_plane_stride,
-                 int64_t c_token_stride, int32_t* bad, hipStream_t stream) {
+                 int64_t c_token_stride, int32_t* bad, hipStream_t stream, int planes = 2) {
   clear_error();
-  if (int rc = validate_desc(kv)) return rc;
+  if (int rc = validate_desc(kv, planes)) return rc;
   CBK_REQUIRE(num_layers >= 1, "num_layers must be >= 1");
   CBK_REQUIRE(num_tokens >= 0, "num_tokens must be >= 0");
   if (num_tokens == 0) return CBK_OK;
@@ -219,7 +220,7 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
     vec = std::min(vec, common_vec_bytes(p, 2));
   }
   const int64_t row_vecs = kv->row_bytes / vec;
-  CBK_REQUIRE(num_tokens * 2 * row_vecs < (int64_t(1) << 32),
+  CBK_REQUIRE(num_tokens * planes * row_vecs < (int64_t(1) << 32),
               "too many vectors in one launch (%lld tokens)", (long long)num_tokens);
 
   PagedArgs a;
@@ -232,12 +233,13 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
   a.token_stride = kv->token_stride;
   a.bad = bad;
   a.num_tokens = uint32_t(num_tokens);
+  a.planes = uint32_t(planes);
   a.row_vecs = uint32_t(row_vecs);
   a.num_slots = uint32_t(kv->num_blocks * kv->block_size);
   a.row_div = FastDiv::make(uint32_t(row_vecs));
   a.bs_div = FastDiv::make(uint32_t(kv->block_size));
 
-  const uint64_t total = uint64_t(num_tokens) * 2 * uint64_t(row_vecs);
+  const uint64_t total = uint64_t(num_tokens) * uint64_t(planes) * uint64_t(row_vecs);
   const int threads = gather ? kGatherThreads : kScatterThreads;
   const uint32_t grid_x = uint32_t((total + threads * kUnroll - 1) / (threads * kUnroll));
 
@@ -333,6 +335,15 @@ int launch_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots, int64_t nu
   return CBK_OK;
 }
 
+// K plane only when the V pointers on both sides are NULL
+int planes_of(const cbk_kv_desc* kv, const void* contiguous_v, int64_t num_tokens, int* planes) {
+  *planes = 2;
+  if (kv != nullptr && kv->v_base == nullptr && contiguous_v == nullptr) *planes = 1;
+  else if (num_tokens > 0 && contiguous_v == nullptr)
+    return set_error(CBK_ERR_INVALID, "V pointer is NULL while the descriptor has a V plane");
+  return CBK_OK;
+}
+
 }  // namespace
 }  // namespace cbk
 
@@ -350,23 +361,25 @@ int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int
 int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
                      void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
                      int32_t* bad_slots_dev, cbk_stream_t stream) {
-  if (num_tokens > 0 && (out_k_dev == nullptr || out_v_dev == nullptr))
-    return cbk::set_error(CBK_ERR_INVALID, "output pointer is NULL");
+  if (num_tokens > 0 && out_k_dev == nullptr) return cbk::set_error(CBK_ERR_INVALID, "output pointer is NULL");
+  int planes = 2;
+  if (int rc = cbk::planes_of(kv, out_v_dev, num_tokens, &planes)) return rc;
   char* k = static_cast<char*>(out_k_dev);
-  const int64_t plane = static_cast<char*>(out_v_dev) - k;
+  const int64_t plane = planes == 2 ? static_cast<char*>(out_v_dev) - k : 0;
   return cbk::launch_paged(true, kv, 1, slots_dev, num_tokens, k, 0, plane, out_token_stride,
-                           bad_slots_dev, static_cast<hipStream_t>(stream));
+                           bad_slots_dev, static_cast<hipStream_t>(stream), planes);
 }
 
 int cbk_paged_scatter(const void* in_k_dev, const void* in_v_dev, int64_t in_token_stride,
                       const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,
                       int32_t* bad_slots_dev, cbk_stream_t stream) {
-  if (num_tokens > 0 && (in_k_dev == nullptr || in_v_dev == nullptr))
-    return cbk::set_error(CBK_ERR_INVALID, "input pointer is NULL");
+  if (num_tokens > 0 && in_k_dev == nullptr) return cbk::set_error(CBK_ERR_INVALID, "input pointer is NULL");
+  int planes = 2;
+  if (int rc = cbk::planes_of(kv, in_v_dev, num_tokens, &planes)) return rc;
   char* k = const_cast<char*>(static_cast<const char*>(in_k_dev));
-  const int64_t plane = static_cast<const char*>(in_v_dev) - k;
+  const int64_t plane = planes == 2 ? static_cast<const char*>(in_v_dev) - k : 0;
   return cbk::launch_paged(false, kv, 1, slots_dev, num_tokens, k, 0, plane, in_token_stride,
-                           bad_slots_dev, static_cast<hipStream_t>(stream));
+                           bad_slots_dev, static_cast<hipStream_t>(stream), planes);
 }
 
 int cbk_paged_gather_layers(const cbk_kv_desc* kv, int32_t num_layers, const int64_t* slots_dev,
