@@ -276,13 +276,19 @@ class PagedBlendLoader:
             self._zc_layers.discard(layer_id)
             hit = self._ensure_hit_staging(layer_id)
             kb, vb = hit[0].data_ptr(), hit[1].data_ptr()
-            n = 2 * len(runs)
-            dst = (ctypes.c_uint64 * n)()
-            src = (ctypes.c_uint64 * n)()
-            nbytes = (ctypes.c_uint64 * n)()
-            for i, (off, tokens, k, v) in enumerate(runs):
-                dst[2 * i], src[2 * i], nbytes[2 * i] = kb + off * row_bytes, k, tokens * row_bytes
-                dst[2 * i + 1], src[2 * i + 1], nbytes[2 * i + 1] = vb + off * row_bytes, v, tokens * row_bytes
+            copies: list[list[int]] = []  # [dst, src, bytes]; K runs, then V runs
+            for plane_base, which in ((kb, 2), (vb, 3)):
+                for run in runs:
+                    dst, src, nb = plane_base + run[0] * row_bytes, run[which], run[1] * row_bytes
+                    last = copies[-1] if copies else None
+                    if last is not None and last[0] + last[2] == dst and last[1] + last[2] == src:
+                        last[2] += nb  # adjacent on both sides (e.g. K plane end = V plane start)
+                    else:
+                        copies.append([dst, src, nb])
+            n = len(copies)
+            dst = (ctypes.c_uint64 * n)(*[c[0] for c in copies])
+            src = (ctypes.c_uint64 * n)(*[c[1] for c in copies])
+            nbytes = (ctypes.c_uint64 * n)(*[c[2] for c in copies])
             if self._load_stream is None:
                 _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n,
                                                              _native.stream_handle(self.device)), "hit runs H2D")
