@@ -2,15 +2,17 @@
 
 The store/load kernels exchange KV with host memory in the reference's
 chunk format: per segment (one ``chunk_size``-token chunk) and layer, a host
-tensor ``[2, chunk, *row]`` whose K and V planes are each contiguous -- in
-practice a view ``host[:, off:off + chunk]`` of one pinned per-layer batch
-(reference connector.py:449-466). This class keeps that contract and the
-method names/semantics the save and load paths call on
-``LocalPinnedCPUStore`` (reference storage.py:56-263): ``begin_put``,
-``reserve_layer``, ``put_layer_host``, ``abort_put``, ``pin``, ``release``,
-``get_layer``. Commit happens when every layer is present; a failed or
-aborted segment is dropped as a unit; the byte cap is fail-closed.
-The content-addressed matcher, LRU eviction and lookup RPC are the
+tensor ``[2, chunk, *row]`` whose K and V planes are each contiguous -- a
+slot of the pinned chunk slab, or a view ``host[:, off:off + chunk]`` of one
+pinned per-layer batch (reference connector.py:449-466). This class keeps
+that contract and the method names/semantics of ``LocalPinnedCPUStore``
+(reference storage.py:33-294) that the save and load paths call:
+``begin_put`` (with the content-hash collision check), ``reserve_layer``,
+``cancel_layer``, ``put_layer``, ``put_layer_host``, ``abort_put``,
+``validate``, ``pin``, ``release``, ``get_layer``, ``clear``. A segment
+commits when every layer is present; a failed or aborted segment is dropped
+as a unit; the byte cap is fail-closed after evicting least recently used,
+committed, unpinned segments. The token-range matcher and lookup RPC are the
 scheduler's control plane and are not part of this package.
 """
 
@@ -19,6 +21,7 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
+from collections import OrderedDict
 from collections.abc import Callable, Iterable, Sequence
 from dataclasses import dataclass, field
 
@@ -42,6 +45,7 @@ def content_hash(tokens: Sequence[int]) -> int:
 @dataclass
 class _Entry:
     num_layers: int
+    tokens: tuple[int, ...] = ()
     layers: dict[int, torch.Tensor] = field(default_factory=dict)
     reserved: set[int] = field(default_factory=set)
     size_bytes: int = 0
@@ -175,7 +179,8 @@ class PinnedChunkStore:
         self.max_bytes = int(max_bytes)
         # called with every layer tensor the store drops (e.g. slab slots)
         self._on_release = on_release
-        self._entries: dict[SegmentId, _Entry] = {}
+        # least recently used first (reference storage.py:42, 273-275)
+        self._entries: OrderedDict[SegmentId, _Entry] = OrderedDict()
         self._pins: dict[str, tuple[SegmentId, ...]] = {}
         self._pin_sets: dict[str, frozenset[SegmentId]] = {}
         self._bytes = 0
@@ -183,7 +188,13 @@ class PinnedChunkStore:
 
     @property
     def current_bytes(self) -> int:
-        return self._bytes
+        with self._lock:
+            return self._bytes
+
+    @property
+    def committed_entries(self) -> int:
+        with self._lock:
+            return sum(1 for e in self._entries.values() if e.committed)
 
     def begin_put(self, model_scope: str, source_start: int, tokens: Sequence[int],
                   num_layers: int) -> SegmentId:
@@ -191,14 +202,45 @@ class PinnedChunkStore:
             raise ValueError("num_layers must be positive")
         if len(tokens) != self.chunk_size:
             raise ValueError(f"fingerprint requires exactly {self.chunk_size} tokens, got {len(tokens)}")
-        sid = SegmentId(model_scope, content_hash(tokens), source_start, len(tokens))
+        key = tuple(int(t) for t in tokens)
+        sid = SegmentId(model_scope, content_hash(key), source_start, len(key))
         with self._lock:
             entry = self._entries.get(sid)
             if entry is None:
-                self._entries[sid] = _Entry(num_layers)
-            elif entry.num_layers != num_layers:
-                raise ValueError("num_layers changed for an existing segment")
+                self._entries[sid] = _Entry(num_layers, key)
+            else:
+                if entry.tokens != key:
+                    raise RuntimeError("content-hash collision for an existing segment id")
+                if entry.num_layers != num_layers:
+                    raise ValueError("num_layers changed for an existing segment")
+                self._entries.move_to_end(sid)
         return sid
+
+    def cancel_layer(self, segment_id: SegmentId, layer_id: int) -> None:
+        """Give up a reserved layer: an uncommitted segment fails as a unit
+        (reference storage.py:120-129)."""
+        with self._lock:
+            entry = self._entries.get(segment_id)
+            if entry is None:
+                return
+            entry.reserved.discard(layer_id)
+            if not entry.committed:
+                entry.failed = True
+            if entry.failed:
+                self._drop_if_idle(segment_id, entry)
+
+    def put_layer(self, segment_id: SegmentId, layer_id: int, kv: torch.Tensor) -> bool | None:
+        """Copy one layer ``[2, chunk, *row]`` (any device) into fresh pinned
+        host memory and publish it (reference storage.py:78-102)."""
+        with self._lock:
+            entry = self._entries.get(segment_id)
+            if entry is None:
+                raise KeyError(segment_id)
+            if not 0 <= layer_id < entry.num_layers:
+                raise ValueError(f"layer {layer_id} is outside [0, {entry.num_layers})")
+        host = torch.empty(kv.shape, dtype=kv.dtype, pin_memory=torch.cuda.is_available())
+        host.copy_(kv.detach())
+        return self.put_layer_host(segment_id, layer_id, host)
 
     def reserve_layer(self, segment_id: SegmentId, layer_id: int) -> bool:
         with self._lock:
@@ -234,15 +276,21 @@ class PinnedChunkStore:
             added = cpu_tensor.numel() * cpu_tensor.element_size()
             previous = entry.layers.get(layer_id)
             growth = added - (previous.numel() * previous.element_size() if previous is not None else 0)
+            if growth > 0:
+                self._evict(growth, exclude=segment_id)
             if self._bytes + growth > self.max_bytes:
                 entry.reserved.discard(layer_id)
                 entry.failed = True
                 self._drop_if_idle(segment_id, entry)
                 return None
             entry.reserved.discard(layer_id)
+            if previous is not None and self._on_release is not None:
+                self._on_release(previous)
             entry.layers[layer_id] = cpu_tensor
+            entry.addresses.pop(layer_id, None)
             entry.size_bytes += growth
             self._bytes += growth
+            self._entries.move_to_end(segment_id)
             if len(entry.layers) == entry.num_layers:
                 entry.committed = True
                 return True
@@ -263,18 +311,33 @@ class PinnedChunkStore:
             return entry is not None and entry.layers.get(layer_id) is tensor
 
     def is_committed(self, segment_id: SegmentId) -> bool:
-        entry = self._entries.get(segment_id)
-        return entry is not None and entry.committed
-
-    def pin(self, request_id: str, segments: Iterable[BlendSegment]) -> tuple[BlendSegment, ...]:
         with self._lock:
-            self.release(request_id)
-            valid = []
+            entry = self._entries.get(segment_id)
+            return entry is not None and entry.committed
+
+    def validate(self, segments: Iterable[BlendSegment]) -> tuple[BlendSegment, ...]:
+        """The committed subset of ``segments`` (reference storage.py:210-219)."""
+        valid = []
+        with self._lock:
             for seg in segments:
                 entry = self._entries.get(seg.segment_id)
                 if entry is None or not entry.committed:
                     continue
+                self._entries.move_to_end(seg.segment_id)
+                valid.append(seg)
+        return tuple(valid)
+
+    def pin(self, request_id: str, segments: Iterable[BlendSegment]) -> tuple[BlendSegment, ...]:
+        requested = tuple(segments)
+        with self._lock:
+            self.release(request_id)
+            valid = []
+            for seg in requested:
+                entry = self._entries.get(seg.segment_id)
+                if entry is None or not entry.committed:
+                    continue
                 entry.pins += 1
+                self._entries.move_to_end(seg.segment_id)
                 valid.append(seg)
             if valid:
                 self._pins[request_id] = tuple(s.segment_id for s in valid)
@@ -288,6 +351,7 @@ class PinnedChunkStore:
                 entry = self._entries.get(sid)
                 if entry is not None:
                     entry.pins = max(0, entry.pins - 1)
+            self._evict(0)
 
     def get_layer(self, request_id: str, segment: BlendSegment, layer_id: int) -> torch.Tensor:
         with self._lock:
@@ -297,9 +361,11 @@ class PinnedChunkStore:
             if entry is None or not entry.committed:
                 raise KeyError(segment.segment_id)
             try:
-                return entry.layers[layer_id]
+                tensor = entry.layers[layer_id]
             except KeyError as error:
                 raise KeyError(f"layer {layer_id} is not stored for {segment.segment_id}") from error
+            self._entries.move_to_end(segment.segment_id)
+            return tensor
 
     def layer_chunk_addresses(self, request_id: str, segments: Sequence[BlendSegment],
                               layer_id: int) -> tuple[tuple, list[int]] | None:
@@ -327,6 +393,7 @@ class PinnedChunkStore:
                     info = entry.addresses[layer_id] = chunk_address(tensor)
                 if info is None or (geometry is not None and info[2] != geometry):
                     return None
+                self._entries.move_to_end(seg.segment_id)
                 geometry = info[2]
                 flat.append(info[0])
                 flat.append(info[1])
@@ -347,6 +414,20 @@ class PinnedChunkStore:
                 self._on_release(tensor)
         entry.layers.clear()
         entry.addresses.clear()
+
+    def _evict(self, required_bytes: int, exclude: SegmentId | None = None) -> None:
+        """Drop least recently used committed, unpinned segments until
+        ``required_bytes`` more fit (reference storage.py:282-294)."""
+        if self._bytes + required_bytes <= self.max_bytes:
+            return
+        for sid, entry in list(self._entries.items()):
+            if self._bytes + required_bytes <= self.max_bytes:
+                break
+            if sid == exclude or entry.pins or not entry.committed:
+                continue
+            self._entries.pop(sid, None)
+            self._bytes -= entry.size_bytes
+            self._release_layers(entry)
 
     def _drop_if_idle(self, segment_id: SegmentId, entry: _Entry) -> None:
         if not entry.reserved and not entry.pins:

@@ -1,0 +1,84 @@
+"""CPU: the pinned chunk store's segment lifecycle, LRU eviction and byte cap
+(reference storage.py:33-294 semantics; the token matcher is not part of it)."""
+
+import pytest
+import torch
+
+from cacheblend_vllm.host_store import PinnedChunkStore, content_hash
+from cacheblend_vllm.types import BlendSegment, SegmentId
+
+CH = 4
+CHUNK_BYTES = 2 * CH * 8 * 4  # [2, 4, 8] float32
+
+
+def _chunk(v):
+    return torch.full((2, CH, 8), float(v))
+
+
+def _put(store, start, layers=1, value=0.0):
+    sid = store.begin_put("m", start, list(range(start, start + CH)), layers)
+    results = [store.put_layer_host(sid, l, _chunk(value)) for l in range(layers)]
+    return sid, results
+
+
+def test_commit_after_all_layers_and_known_hash():
+    store = PinnedChunkStore(CH, 1 << 20)
+    sid, results = _put(store, 0, layers=3)
+    assert results == [False, False, True] and store.is_committed(sid)
+    assert sid.content_hash == content_hash(range(CH)) and store.committed_entries == 1
+    assert store.put_layer_host(sid, 1, _chunk(9)) is False  # committed entries are immutable
+    with pytest.raises(RuntimeError, match="collision"):
+        store._entries[sid].tokens = (7,) * CH
+        store.begin_put("m", 0, list(range(CH)), 3)
+
+
+def test_lru_eviction_skips_pinned_and_uncommitted_then_fails_closed():
+    released = []
+    store = PinnedChunkStore(CH, 3 * CHUNK_BYTES, on_release=released.append)
+    a, _ = _put(store, 0)
+    b, _ = _put(store, 100)
+    c, _ = _put(store, 200)
+    store.pin("r", [BlendSegment(a, 0)])          # a pinned and most recent
+    store.validate([BlendSegment(c, 0)])          # c touched: LRU order b, a, c
+    d, res = _put(store, 300)                     # evicts b (oldest unpinned committed)
+    assert res == [True] and not store.is_committed(b) and store.is_committed(a)
+    assert len(released) == 1 and store.current_bytes == 3 * CHUNK_BYTES
+    e, res = _put(store, 400)                     # evicts c next, a stays pinned
+    assert res == [True] and not store.is_committed(c) and store.is_committed(a)
+    store.pin("s", [BlendSegment(d, 0), BlendSegment(e, 0)])
+    f, res = _put(store, 500)                     # everything pinned: fail closed
+    assert res == [None] and f not in store._entries
+    store.release("s")                            # unpinned now, still within the cap
+    assert store.current_bytes == 3 * CHUNK_BYTES
+    g, res = _put(store, 600)
+    assert res == [True] and not store.is_committed(d)
+
+
+def test_cancel_abort_and_failed_segments_drop_as_a_unit():
+    released = []
+    store = PinnedChunkStore(CH, 1 << 20, on_release=released.append)
+    sid = store.begin_put("m", 0, list(range(CH)), 2)
+    assert store.reserve_layer(sid, 0) and store.reserve_layer(sid, 1)
+    assert not store.reserve_layer(sid, 1)         # already in flight
+    assert store.put_layer_host(sid, 0, _chunk(1)) is False
+    store.cancel_layer(sid, 1)                     # uncommitted: the segment fails
+    assert sid not in store._entries and len(released) == 1 and store.current_bytes == 0
+    sid2 = store.begin_put("m", 8, list(range(8, 8 + CH)), 2)
+    store.put_layer_host(sid2, 0, _chunk(2))
+    store.abort_put(sid2)
+    assert sid2 not in store._entries and store.current_bytes == 0
+
+
+def test_put_layer_copies_and_get_layer_requires_pin():
+    store = PinnedChunkStore(CH, 1 << 20)
+    sid = store.begin_put("m", 0, list(range(CH)), 1)
+    src = _chunk(3)
+    assert store.put_layer(sid, 0, src) is True
+    seg = BlendSegment(sid, 0)
+    with pytest.raises(RuntimeError, match="not pinned"):
+        store.get_layer("r", seg, 0)
+    assert store.pin("r", [seg]) == (seg,)
+    got = store.get_layer("r", seg, 0)
+    assert torch.equal(got, src) and got.data_ptr() != src.data_ptr()
+    with pytest.raises(KeyError):
+        store.put_layer(SegmentId("m", 1, 0, CH), 0, src)  # never begun
