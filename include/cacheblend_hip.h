@@ -264,6 +264,23 @@ int cbk_blend_assemble_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev,
                               void* out_k_dev, void* out_v_dev, int64_t out_token_stride,
                               int32_t* bad_dev, int32_t max_workgroups, cbk_stream_t stream);
 
+/*
+ * Side-forward attention of the selected queries:
+ *   out[i, h] = sum_{k <= pos_i} softmax_k( r(r(q[i, h] . key[k, h/G]) * scale) ) value[k, h/G]
+ * q [nq, hq, head_dim], key/value [nk, hkv, head_dim], out [nq, hq, head_dim]
+ * (row strides in elements), pos [nq] int64 in [0, nk), G = hq / hkv, r
+ * rounding to the input dtype (none for float32). Replaces
+ * Qwen3BlendExecutor._attention (cacheblend_vllm/ascend.py:798-846:
+ * npu_fused_infer_attention_score or the einsum path) with the causal mask
+ * q_pos < k_pos evaluated in the kernel. bf16/f16: head_dim 64 or 128,
+ * 16-byte aligned pointers and row strides; float32: head_dim <= 128.
+ */
+int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems, const int64_t* q_pos_dev, int64_t nq,
+                        const void* k_dev, int64_t k_row_stride_elems, const void* v_dev,
+                        int64_t v_row_stride_elems, int64_t nk, int64_t hq, int64_t hkv, int64_t head_dim,
+                        float scale, int32_t dtype, void* out_dev, int64_t out_row_stride_elems,
+                        cbk_stream_t stream);
+
 /* Workspace bytes cbk_sparse_q_scores needs. */
 size_t cbk_sparse_q_workspace_bytes(int64_t nq, int64_t nk, int64_t hq, int64_t hkv);
 

@@ -37,6 +37,9 @@ Pinning (what checks each function, all in tests/test_oracle.py):
   (tests/test_ascend.py:91-100), group property R(a)R(b)^-1.
 * loader_assemble / loader_commit: reference known answer
   (tests/test_ascend.py:136-181).
+* blend_attention: float64 closed forms -- identical keys give the mean of
+  the visible values, a one-key context returns that value, uniform logits
+  average the visible rows, and a brute-force per-query softmax loop.
 """
 
 from __future__ import annotations
@@ -64,6 +67,8 @@ __all__ = [
     "relocate_key",
     "loader_assemble",
     "loader_commit",
+    "round_f16",
+    "blend_attention",
 ]
 
 
@@ -501,3 +506,68 @@ def loader_commit(
         np.asarray(slots)[start:allocation_end],
         block_size,
     )
+
+
+# ---------------------------------------------------------------------------
+# Side-forward attention of the selected queries
+# ---------------------------------------------------------------------------
+
+
+def round_f16(x: np.ndarray) -> np.ndarray:
+    """float32 -> float16 (round to nearest even) -> float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def blend_attention(
+    query: np.ndarray,
+    key: np.ndarray,
+    value: np.ndarray,
+    q_positions: np.ndarray,
+    scale: float,
+    rounding: str | None = "bf16",
+    chunk: int = 64,
+    return_mass: bool = False,
+):
+    """``out[q, h] = sum_k softmax_k(w[h, q, :])[k] * value[k, h // G]`` with
+    ``w = r(r(query[q, h] . key[k, h // G]) * scale)`` and keys ``k >
+    q_positions[q]`` masked out, G = Hq / Hkv.
+
+    Follows cacheblend_vllm/ascend.py:798-846 (the einsum path of
+    ``Qwen3BlendExecutor._attention``): the score einsum and the ``* scale``
+    are rounded to the input dtype (``r``: bf16 or f16, none for float32),
+    the softmax is float32 over all keys with masked entries at the dtype's
+    minimum (exactly zero weight), the probabilities are rounded to the input
+    dtype, and the value einsum accumulates them in float32 before rounding
+    the output to the input dtype. Inputs are float32 arrays holding the
+    dtype's values; returns float32 ``[Nq, Hq, D]`` -- and, with
+    ``return_mass``, also ``sum_k p[k] * |value[k]|`` per output element, the
+    L1 size of the terms each output sums (rounding errors of the
+    probabilities scale with it, not with a possibly cancelled output).
+    """
+    r = {"bf16": round_bf16, "f16": round_f16, None: lambda x: np.asarray(x, np.float32)}[rounding]
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    nq, hq, d = q.shape
+    nk, hkv, _ = k.shape
+    if hq % hkv:
+        raise ValueError("query heads must be divisible by KV heads")
+    g = hq // hkv
+    pos = np.asarray(q_positions, dtype=np.int64)
+    out = np.empty((nq, hq, d), dtype=np.float32)
+    mass = np.empty((nq, hq, d), dtype=np.float64) if return_mass else None
+    keys = np.arange(nk)
+    for c0 in range(0, nq, chunk):
+        qc = q[c0:c0 + chunk]
+        mask = pos[c0:c0 + chunk, None] < keys[None, :]                  # [c, nk]
+        for h in range(hq):
+            kh, vh = k[:, h // g, :], v[:, h // g, :]
+            w = r(r(qc[:, h, :].astype(np.float64) @ kh.T.astype(np.float64)) * np.float32(scale))
+            w = np.where(mask, -np.inf, w.astype(np.float64))
+            w = w - w.max(axis=1, keepdims=True)
+            e = np.exp(w)
+            p = r(e / e.sum(axis=1, keepdims=True))
+            out[c0:c0 + chunk, h, :] = r(p.astype(np.float64) @ vh.astype(np.float64))
+            if mass is not None:
+                mass[c0:c0 + chunk, h, :] = p.astype(np.float64) @ np.abs(vh.astype(np.float64))
+    return (out, mass) if return_mass else out

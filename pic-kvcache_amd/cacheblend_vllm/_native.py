@@ -114,6 +114,11 @@ _SIGNATURES = {
             c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_i64, c_vp, c_i32, c_vp,
         ],
     ),
+    "cbk_blend_attention": (
+        ctypes.c_int,
+        [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float,
+         c_i32, c_vp, c_i64, c_vp],
+    ),
     "cbk_sparse_q_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i64, c_i64, c_i64]),
     "cbk_sparse_q_scores": (
         ctypes.c_int,

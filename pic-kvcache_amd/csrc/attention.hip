@@ -1,0 +1,460 @@
+// Side-forward attention of the selected queries for gfx950 (the blend
+// executor's attention over the layer buffer, cacheblend_vllm/ascend.py:
+// 798-846):
+//
+//   out[i, h] = sum_{k <= pos_i} softmax_k( r(r(q[i, h] . key[k, h/G]) * scale) ) value[k, h/G]
+//
+// with r rounding to the input dtype (the reference's bf16/f16 einsum output
+// and its "* scale"), the softmax in float32, G = Hq / Hkv.
+//
+// One workgroup (4 waves) per (64 rows of (query, group head), kv head):
+// row r of the 64 is query r / G, head kv * G + r % G, so the K/V tiles
+// staged in LDS serve all G heads of several queries. Per 32-key block:
+//   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K rows, B = Q rows,
+//                   both 16-byte loads of 8 consecutive dims; the result
+//                   holds key 4*(lane/16)+i of row lane%16 in register i
+//   online softmax  per row in the log2 domain, the row's 32 keys spread
+//                   over its 4 lane groups (two xor shuffles)
+//   O += P . V      v_mfma_f32_16x16x16_{bf16,f16}: the S^T registers are
+//                   exactly the A operand (row lane%16, keys 4*(lane/16)..+3);
+//                   B needs 4 consecutive keys of one dim, so V is staged
+//                   transposed in LDS ([dim][key], key pairs per 32-bit word)
+// K/V blocks are double-buffered through LDS with a register prefetch; the
+// row tiles with the latest positions (most keys) are scheduled first.
+// MFMA layouts (checked on gfx950): 16x16x32 A[i][k] in lane i+16*(k/8)
+// element k%8, B[k][j] in lane j+16*(k/8); 16x16x16 A[i][k] in lane
+// i+16*(k/4) element k%4, B[k][j] in lane j+16*(k/4); D[i][j] in lane
+// j+16*(i/4), register i%4.
+//
+// float32 inputs take an exact float32 path (one wave per (query, head)).
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cmath>
+
+#include "cbk_common.hpp"
+
+namespace cbk {
+namespace {
+
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerWg = 64;
+constexpr int kKeyBlock = 32;
+constexpr int kVtWords = 18;  // words per transposed V row (32 keys + 4 pad), conflict-free stores
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+struct AttnArgs {
+  const uint16_t* q;      // [nq, hq, d], row stride q_stride elements
+  const int64_t* pos;     // [nq] key positions of the queries
+  const uint16_t* k;      // [nk, hkv, d], row stride k_stride
+  const uint16_t* v;      // [nk, hkv, d], row stride v_stride
+  uint16_t* out;          // [nq, hq, d], row stride out_stride
+  int64_t q_stride, k_stride, v_stride, out_stride;
+  uint32_t nq, nk, hq, hkv, group, d;
+  float scale;
+};
+
+template <bool F16> struct Ops;
+template <> struct Ops<false> {  // bf16
+  typedef s16x8 A8;
+  typedef s16x4 A4;
+  static __device__ __forceinline__ f32x4 mma32(const A8& a, const A8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(const A4& a, const A4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  // two floats -> two bf16 (round to nearest even) packed low/high
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){x, y}, b2));
+  }
+  static __device__ __forceinline__ float lo(uint32_t u) { return __uint_as_float(u << 16); }
+  static __device__ __forceinline__ float hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+};
+template <> struct Ops<true> {  // f16
+  typedef h16x8 A8;
+  typedef h16x4 A4;
+  static __device__ __forceinline__ f32x4 mma32(const A8& a, const A8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(const A4& a, const A4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float x, float y) {
+    const __half2 h = __floats2half2_rn(x, y);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  static __device__ __forceinline__ float lo(uint32_t u) {
+    return __half2float(__builtin_bit_cast(__half, uint16_t(u & 0xffffu)));
+  }
+  static __device__ __forceinline__ float hi(uint32_t u) {
+    return __half2float(__builtin_bit_cast(__half, uint16_t(u >> 16)));
+  }
+};
+
+// Rounds a pair to the dtype and back (the dtype's matmul / multiply output).
+template <bool F16>
+__device__ __forceinline__ void round2(float& x, float& y) {
+  const uint32_t u = Ops<F16>::pack(x, y);
+  x = Ops<F16>::lo(u);
+  y = Ops<F16>::hi(u);
+}
+
+template <int D>
+struct KvRegs {
+  static constexpr int KPIECES = kKeyBlock * (D / 8) / kThreads;  // 16-byte K pieces per thread
+  static constexpr int VJOBS = 16 * (D / 8);                     // (key pair, dim chunk) jobs
+  u32x4 k[KPIECES];
+  u32x4 v0, v1;
+};
+
+template <int D>
+__device__ __forceinline__ void load_kv(const AttnArgs& a, uint32_t kvh, int32_t k0, KvRegs<D>& r) {
+#pragma unroll
+  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    const int32_t key = k0 + int32_t(idx / (D / 8));
+    const uint32_t chunk = idx % (D / 8);
+    r.k[p] = u32x4(0u);
+    if (key < int32_t(a.nk))
+      r.k[p] = *reinterpret_cast<const u32x4*>(a.k + int64_t(key) * a.k_stride + int64_t(kvh) * D + chunk * 8);
+  }
+  r.v0 = u32x4(0u);
+  r.v1 = u32x4(0u);
+  if (threadIdx.x < uint32_t(KvRegs<D>::VJOBS)) {
+    const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
+    const int32_t key = k0 + int32_t(2 * kp);
+    const uint16_t* base = a.v + int64_t(kvh) * D + dc * 8;
+    if (key < int32_t(a.nk)) r.v0 = *reinterpret_cast<const u32x4*>(base + int64_t(key) * a.v_stride);
+    if (key + 1 < int32_t(a.nk)) r.v1 = *reinterpret_cast<const u32x4*>(base + int64_t(key + 1) * a.v_stride);
+  }
+}
+
+// K rows [32][D + 8] (padded); V transposed as words [D][kVtWords], word
+// (dim, kp) = {V[2kp][dim], V[2kp+1][dim]}.
+template <int D>
+__device__ __forceinline__ void store_kv(uint16_t* ks, uint32_t* vt, const KvRegs<D>& r) {
+  constexpr int LK = D + 8;
+#pragma unroll
+  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
+    const uint32_t idx = threadIdx.x + p * kThreads;
+    *reinterpret_cast<u32x4*>(&ks[(idx / (D / 8)) * LK + (idx % (D / 8)) * 8]) = r.k[p];
+  }
+  if (threadIdx.x < uint32_t(KvRegs<D>::VJOBS)) {
+    const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t a0 = r.v0[w], a1 = r.v1[w];  // dims 8dc+2w (low), 8dc+2w+1 (high)
+      vt[(dc * 8 + 2 * w) * kVtWords + kp] = (a0 & 0xffffu) | (a1 << 16);
+      vt[(dc * 8 + 2 * w + 1) * kVtWords + kp] = (a0 >> 16) | (a1 & 0xffff0000u);
+    }
+  }
+}
+
+template <bool F16, int D, bool MASK>
+__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t* vt, int32_t k0, float scale,
+                                             const typename Ops<F16>::A8 (&qf)[D / 32], int32_t rpos,
+                                             float& m, float& l, f32x4 (&o)[D / 16], uint32_t lane) {
+  using O = Ops<F16>;
+  constexpr int LK = D + 8;
+  const uint32_t row = lane & 15, grp = lane >> 4;
+  f32x4 s[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) {
+      const typename O::A8 kf =
+          *reinterpret_cast<const typename O::A8*>(&ks[(16 * h + row) * LK + 32 * st + 8 * grp]);
+      s[h] = O::mma32(kf, qf[st], s[h]);
+    }
+  }
+  // logits: r(r(dot) * scale) as the dtype's einsum and multiply produce
+  float x[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    x[h][0] = s[h][0]; x[h][1] = s[h][1]; x[h][2] = s[h][2]; x[h][3] = s[h][3];
+    round2<F16>(x[h][0], x[h][1]);
+    round2<F16>(x[h][2], x[h][3]);
+    x[h][0] *= scale; x[h][1] *= scale; x[h][2] *= scale; x[h][3] *= scale;
+    round2<F16>(x[h][0], x[h][1]);
+    round2<F16>(x[h][2], x[h][3]);
+    if constexpr (MASK) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (k0 + 16 * h + int32_t(4 * grp) + i > rpos) x[h][i] = kNegInf;
+    }
+  }
+  float bm = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                   fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  const float mn = fmaxf(m, bm * kLog2e);
+  const float ms = mn == kNegInf ? 0.f : mn;
+  const float alpha = __builtin_amdgcn_exp2f(m - ms);
+  m = mn;
+  float p[2][4];
+  float sum = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[h][i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
+      sum += p[h][i];
+    }
+  l = fmaf(l, alpha, sum);
+  // rescale O rows (row 4*grp + i lives in register i) by their alpha
+  float ao[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha, int(4 * grp + i));
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) {
+    o[t][0] *= ao[0]; o[t][1] *= ao[1]; o[t][2] *= ao[2]; o[t][3] *= ao[3];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const u32x2 pk = u32x2{O::pack(p[h][0], p[h][1]), O::pack(p[h][2], p[h][3])};
+    const typename O::A4 pa = __builtin_bit_cast(typename O::A4, pk);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(&vt[(16 * t + row) * kVtWords + 8 * h + 2 * grp]);
+      o[t] = O::mma16(pa, __builtin_bit_cast(typename O::A4, w), o[t]);
+    }
+  }
+}
+
+template <bool F16, int D>
+__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
+  constexpr int LK = D + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeyBlock * LK];
+  __shared__ __attribute__((aligned(16))) uint32_t vt[2][D * kVtWords];
+  __shared__ int32_t s_max[4];
+  using O = Ops<F16>;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t row = lane & 15, grp = lane >> 4;
+  const uint32_t kvh = blockIdx.y;
+  const uint32_t nrows = a.nq * a.group;
+  const uint32_t ntiles = (nrows + kRowsPerWg - 1) / kRowsPerWg;
+  const uint32_t tile = ntiles - 1 - blockIdx.x;  // latest positions (most keys) first
+  const uint32_t r_wave = tile * kRowsPerWg + wave * 16;
+
+  // this lane's row: (query, head) and its Q fragments
+  const uint32_t r = r_wave + row;
+  const bool valid = r < nrows;
+  const uint32_t qi = valid ? r / a.group : 0;
+  const uint32_t qh = kvh * a.group + (valid ? r % a.group : 0);
+  const int32_t rpos = valid ? int32_t(a.pos[qi]) : -1;
+  typename O::A8 qf[D / 32];
+#pragma unroll
+  for (int st = 0; st < D / 32; ++st) {
+    u32x4 w = u32x4(0u);
+    if (valid)
+      w = *reinterpret_cast<const u32x4*>(a.q + int64_t(qi) * a.q_stride + int64_t(qh) * D + 32 * st + 8 * grp);
+    qf[st] = __builtin_bit_cast(typename O::A8, w);
+  }
+  int32_t wmax = rpos, wmin = valid ? rpos : 0x7fffffff;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    wmax = max(wmax, __shfl_xor(wmax, off));
+    wmin = min(wmin, __shfl_xor(wmin, off));
+  }
+  if (lane == 0) s_max[wave] = wmax;
+  __syncthreads();
+  const int32_t gmax = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+  const int32_t nblocks = gmax < 0 ? 0 : (gmax + kKeyBlock) / kKeyBlock;
+
+  float m = kNegInf, l = 0.f;
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  KvRegs<D> pre;
+  if (nblocks > 0) {
+    load_kv<D>(a, kvh, 0, pre);
+    store_kv<D>(ks[0], vt[0], pre);
+  }
+  __syncthreads();
+  for (int32_t b = 0; b < nblocks; ++b) {
+    const int32_t k0 = b * kKeyBlock;
+    const int buf = b & 1;
+    if (b + 1 < nblocks) load_kv<D>(a, kvh, k0 + kKeyBlock, pre);
+    if (k0 <= wmax) {
+      if (k0 + kKeyBlock - 1 > wmin)
+        attend_block<F16, D, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+      else
+        attend_block<F16, D, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+    }
+    if (b + 1 < nblocks) store_kv<D>(ks[buf ^ 1], vt[buf ^ 1], pre);
+    __syncthreads();
+  }
+
+  // normalize: the row sum is spread over the row's 4 lane groups
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  const float linv = l > 0.f ? 1.f / l : 0.f;
+  float lo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo[i] = __shfl(linv, int(4 * grp + i));
+  // stage the wave's 16 x D output tile in LDS (the K buffers are free now),
+  // then write whole 16-byte pieces of each (query, head) row
+  uint16_t* os = &ks[0][0] + wave * 16 * D;
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) {
+    const uint32_t u01 = O::pack(o[t][0] * lo[0], o[t][1] * lo[1]);
+    const uint32_t u23 = O::pack(o[t][2] * lo[2], o[t][3] * lo[3]);
+    const uint32_t col = 16 * t + row;
+    os[(4 * grp + 0) * D + col] = uint16_t(u01 & 0xffffu);
+    os[(4 * grp + 1) * D + col] = uint16_t(u01 >> 16);
+    os[(4 * grp + 2) * D + col] = uint16_t(u23 & 0xffffu);
+    os[(4 * grp + 3) * D + col] = uint16_t(u23 >> 16);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 16 * (D / 8) / 64; ++c) {
+    const uint32_t idx = lane + 64 * c;
+    const uint32_t orow = idx / (D / 8), chunk = idx % (D / 8);
+    const uint32_t rr = r_wave + orow;
+    if (rr < nrows) {
+      const uint32_t oq = rr / a.group, oh = kvh * a.group + rr % a.group;
+      *reinterpret_cast<u32x4*>(a.out + int64_t(oq) * a.out_stride + int64_t(oh) * D + chunk * 8) =
+          *reinterpret_cast<const u32x4*>(&os[orow * D + chunk * 8]);
+    }
+  }
+}
+
+// float32: one wave per (query, head), exact float32 dots and accumulation,
+// two dims per lane (D <= 128).
+struct AttnArgsF32 {
+  const float* q;
+  const int64_t* pos;
+  const float* k;
+  const float* v;
+  float* out;
+  int64_t q_stride, k_stride, v_stride, out_stride;
+  uint32_t nq, nk, hq, hkv, group, d;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void attn_f32_kernel(const AttnArgsF32 a) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t job = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (job >= a.nq * a.hq) return;  // whole waves exit together
+  const uint32_t qi = job / a.hq, h = job % a.hq, kvh = h / a.group;
+  const float* q = a.q + int64_t(qi) * a.q_stride + int64_t(h) * a.d;
+  const float q0 = lane < a.d ? q[lane] : 0.f;
+  const float q1 = lane + 64 < a.d ? q[lane + 64] : 0.f;
+  int64_t last = a.pos[qi];
+  if (last >= int64_t(a.nk)) last = int64_t(a.nk) - 1;
+  float m = kNegInf, l = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int64_t j = 0; j <= last; ++j) {
+    const float* kr = a.k + j * a.k_stride + int64_t(kvh) * a.d;
+    const float* vr = a.v + j * a.v_stride + int64_t(kvh) * a.d;
+    float dot = (lane < a.d ? q0 * kr[lane] : 0.f) + (lane + 64 < a.d ? q1 * kr[lane + 64] : 0.f);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) dot += __shfl_xor(dot, off);
+    const float x = dot * a.scale;
+    const float mn = fmaxf(m, x);
+    const float alpha = expf(m - mn);
+    const float p = expf(x - mn);
+    l = l * alpha + p;
+    o0 = o0 * alpha + p * (lane < a.d ? vr[lane] : 0.f);
+    o1 = o1 * alpha + p * (lane + 64 < a.d ? vr[lane + 64] : 0.f);
+    m = mn;
+  }
+  float* out = a.out + int64_t(qi) * a.out_stride + int64_t(h) * a.d;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (lane < a.d) out[lane] = o0 * inv;
+  if (lane + 64 < a.d) out[lane + 64] = o1 * inv;
+}
+
+}  // namespace
+}  // namespace cbk
+
+extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems, const int64_t* q_pos_dev,
+                                   int64_t nq, const void* k_dev, int64_t k_row_stride_elems,
+                                   const void* v_dev, int64_t v_row_stride_elems, int64_t nk, int64_t hq,
+                                   int64_t hkv, int64_t head_dim, float scale, int32_t dtype, void* out_dev,
+                                   int64_t out_row_stride_elems, cbk_stream_t stream) {
+  using namespace cbk;
+  clear_error();
+  CBK_REQUIRE(nq >= 0 && nq < (int64_t(1) << 26), "nq out of range");
+  if (nq == 0) return CBK_OK;
+  CBK_REQUIRE(q_dev && q_pos_dev && k_dev && v_dev && out_dev, "NULL pointer");
+  CBK_REQUIRE(nk > 0 && nk < (int64_t(1) << 31), "nk out of range");
+  CBK_REQUIRE(hq > 0 && hkv > 0 && hq % hkv == 0, "query heads must be divisible by KV heads");
+  CBK_REQUIRE(nq * hq < (int64_t(1) << 31), "nq * hq too large");
+  CBK_REQUIRE(q_row_stride_elems >= hq * head_dim && out_row_stride_elems >= hq * head_dim &&
+                  k_row_stride_elems >= hkv * head_dim && v_row_stride_elems >= hkv * head_dim,
+              "row stride smaller than a row");
+  CBK_REQUIRE(std::isfinite(scale), "scale must be finite");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == CBK_DTYPE_F32) {
+    CBK_REQUIRE(head_dim > 0 && head_dim <= 128, "float32 path needs head_dim <= 128");
+    AttnArgsF32 a;
+    a.q = static_cast<const float*>(q_dev);
+    a.pos = q_pos_dev;
+    a.k = static_cast<const float*>(k_dev);
+    a.v = static_cast<const float*>(v_dev);
+    a.out = static_cast<float*>(out_dev);
+    a.q_stride = q_row_stride_elems;
+    a.k_stride = k_row_stride_elems;
+    a.v_stride = v_row_stride_elems;
+    a.out_stride = out_row_stride_elems;
+    a.nq = uint32_t(nq);
+    a.nk = uint32_t(nk);
+    a.hq = uint32_t(hq);
+    a.hkv = uint32_t(hkv);
+    a.group = uint32_t(hq / hkv);
+    a.d = uint32_t(head_dim);
+    a.scale = scale;
+    const uint64_t jobs = uint64_t(nq) * uint64_t(hq);
+    hipLaunchKernelGGL(attn_f32_kernel, dim3(uint32_t((jobs + 3) / 4)), dim3(256), 0, s, a);
+    return launch_status("blend attention f32");
+  }
+  CBK_REQUIRE(dtype == CBK_DTYPE_BF16 || dtype == CBK_DTYPE_F16, "dtype %d", int(dtype));
+  CBK_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim %lld: 64 or 128 supported", (long long)head_dim);
+  const int64_t align[8] = {q_row_stride_elems * 2, k_row_stride_elems * 2, v_row_stride_elems * 2,
+                            out_row_stride_elems * 2,
+                            int64_t(reinterpret_cast<uintptr_t>(q_dev)), int64_t(reinterpret_cast<uintptr_t>(k_dev)),
+                            int64_t(reinterpret_cast<uintptr_t>(v_dev)), int64_t(reinterpret_cast<uintptr_t>(out_dev))};
+  CBK_REQUIRE(common_vec_bytes(align, 8) == 16, "q/k/v/out pointers and row strides must be 16-byte aligned");
+  AttnArgs a;
+  a.q = static_cast<const uint16_t*>(q_dev);
+  a.pos = q_pos_dev;
+  a.k = static_cast<const uint16_t*>(k_dev);
+  a.v = static_cast<const uint16_t*>(v_dev);
+  a.out = static_cast<uint16_t*>(out_dev);
+  a.q_stride = q_row_stride_elems;
+  a.k_stride = k_row_stride_elems;
+  a.v_stride = v_row_stride_elems;
+  a.out_stride = out_row_stride_elems;
+  a.nq = uint32_t(nq);
+  a.nk = uint32_t(nk);
+  a.hq = uint32_t(hq);
+  a.hkv = uint32_t(hkv);
+  a.group = uint32_t(hq / hkv);
+  a.d = uint32_t(head_dim);
+  a.scale = scale;
+  const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
+  const dim3 grid(uint32_t((nrows + kRowsPerWg - 1) / kRowsPerWg), uint32_t(hkv));
+  const bool f16 = dtype == CBK_DTYPE_F16;
+  if (head_dim == 128) {
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 128>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 128>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 64>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 64>), grid, dim3(kThreads), 0, s, a);
+  }
+  return launch_status("blend attention");
+}

@@ -374,3 +374,48 @@ def test_select_exhaustive_permutations_tiny():
         cached = [i for i in range(5) if not gap[i]]
         top = sorted(cached, key=lambda i: -scores[i])[:2]
         assert got.tolist() == sorted({1, *top})
+
+
+# ---- blend_attention (side-forward attention of the selected queries) ----
+
+def test_blend_attention_single_visible_key_returns_its_value_per_kv_head():
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((3, 4, 16)).astype(np.float32)
+    k = rng.standard_normal((6, 2, 16)).astype(np.float32)
+    v = O.round_bf16(rng.standard_normal((6, 2, 16)))
+    out = O.blend_attention(q, k, v, np.zeros(3, dtype=np.int64), 0.25, "bf16")
+    for h in range(4):  # GQA: heads 0,1 read KV head 0, heads 2,3 read KV head 1
+        np.testing.assert_array_equal(out[:, h, :], np.broadcast_to(v[0, h // 2], (3, 16)))
+
+
+def test_blend_attention_identical_keys_average_the_visible_values():
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal((4, 2, 8)).astype(np.float32)
+    k = np.broadcast_to(rng.standard_normal((1, 1, 8)), (10, 1, 8)).astype(np.float32)
+    v = rng.standard_normal((10, 1, 8)).astype(np.float32)
+    pos = np.array([0, 3, 9, 5])
+    out = O.blend_attention(q, k, v, pos, 0.5, None)
+    for i, p in enumerate(pos):
+        np.testing.assert_allclose(out[i], np.broadcast_to(v[: p + 1, 0].mean(axis=0), (2, 8)), rtol=1e-6)
+
+
+def test_blend_attention_zero_query_is_uniform_and_rounding_is_bounded():
+    rng = np.random.default_rng(13)
+    k = rng.standard_normal((50, 2, 32)).astype(np.float32)
+    v = O.round_bf16(rng.standard_normal((50, 2, 32)))
+    pos = np.array([49, 20])
+    zero = O.blend_attention(np.zeros((2, 2, 32), np.float32), k, v, pos, 1.0, None)
+    np.testing.assert_allclose(zero[0], v[:, :, :].mean(axis=0), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(zero[1], v[:21].mean(axis=0), rtol=1e-5, atol=1e-7)
+    q = O.round_bf16(rng.standard_normal((40, 4, 32)))
+    pos2 = np.arange(40) % 50
+    exact = O.blend_attention(q, k, v, pos2, 32 ** -0.5, None)
+    rounded = O.blend_attention(q, k, v, pos2, 32 ** -0.5, "bf16")
+    diff = np.abs(rounded - exact)
+    assert diff.max() < 3e-2 * np.abs(v).max()  # bf16 rounding of logits, probabilities and output
+    assert diff.max() > 0                        # ... which does change the result
+
+
+def test_blend_attention_rejects_non_divisible_heads():
+    with pytest.raises(ValueError, match="divisible"):
+        O.blend_attention(np.zeros((1, 3, 4)), np.zeros((2, 2, 4)), np.zeros((2, 2, 4)), np.zeros(1), 1.0)
