@@ -46,11 +46,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWg = 64;
+constexpr int kRowTiles = 1;  // 16-row tiles per wave (2 needs ~290 registers: one wave per SIMD, slower)
 constexpr int kKeyBlock = 32;
 constexpr int kVtWords = 18;  // words per transposed V row (32 keys + 4 pad), conflict-free stores
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kRescale = 8.f;  // log2 headroom of the lazy softmax rescaling
 
 struct AttnArgs {
   const uint16_t* q;      // [nq, hq, d], row stride q_stride elements
@@ -119,25 +120,46 @@ struct KvRegs {
   u32x4 v0, v1;
 };
 
+// This thread's K/V sources for key block 0; advanced by one block per call.
 template <int D>
-__device__ __forceinline__ void load_kv(const AttnArgs& a, uint32_t kvh, int32_t k0, KvRegs<D>& r) {
+struct KvSrc {
+  const uint16_t* k[KvRegs<D>::KPIECES];
+  const uint16_t* v0;
+  int32_t kkey[KvRegs<D>::KPIECES];
+  int32_t vkey;
+};
+
+template <int D>
+__device__ __forceinline__ void init_kv_src(const AttnArgs& a, uint32_t kvh, KvSrc<D>& src) {
 #pragma unroll
   for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
     const uint32_t idx = threadIdx.x + p * kThreads;
-    const int32_t key = k0 + int32_t(idx / (D / 8));
-    const uint32_t chunk = idx % (D / 8);
+    src.kkey[p] = int32_t(idx / (D / 8));
+    src.k[p] = a.k + int64_t(src.kkey[p]) * a.k_stride + int64_t(kvh) * D + (idx % (D / 8)) * 8;
+  }
+  const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
+  src.vkey = int32_t(2 * kp);
+  src.v0 = a.v + int64_t(src.vkey) * a.v_stride + int64_t(kvh) * D + dc * 8;
+}
+
+// Loads key block k0 (= b * kKeyBlock) into registers; blocks entirely inside
+// the context load without per-key checks, the last one zero-fills.
+template <int D>
+__device__ __forceinline__ void load_kv(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
+  const int32_t k0 = b * kKeyBlock;
+  const int64_t koff = int64_t(k0) * a.k_stride, voff = int64_t(k0) * a.v_stride;
+  const bool inside = k0 + kKeyBlock <= int32_t(a.nk);
+#pragma unroll
+  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
     r.k[p] = u32x4(0u);
-    if (key < int32_t(a.nk))
-      r.k[p] = *reinterpret_cast<const u32x4*>(a.k + int64_t(key) * a.k_stride + int64_t(kvh) * D + chunk * 8);
+    if (inside || k0 + src.kkey[p] < int32_t(a.nk)) r.k[p] = *reinterpret_cast<const u32x4*>(src.k[p] + koff);
   }
   r.v0 = u32x4(0u);
   r.v1 = u32x4(0u);
   if (threadIdx.x < uint32_t(KvRegs<D>::VJOBS)) {
-    const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
-    const int32_t key = k0 + int32_t(2 * kp);
-    const uint16_t* base = a.v + int64_t(kvh) * D + dc * 8;
-    if (key < int32_t(a.nk)) r.v0 = *reinterpret_cast<const u32x4*>(base + int64_t(key) * a.v_stride);
-    if (key + 1 < int32_t(a.nk)) r.v1 = *reinterpret_cast<const u32x4*>(base + int64_t(key + 1) * a.v_stride);
+    const int32_t key = k0 + src.vkey;
+    if (inside || key < int32_t(a.nk)) r.v0 = *reinterpret_cast<const u32x4*>(src.v0 + voff);
+    if (inside || key + 1 < int32_t(a.nk)) r.v1 = *reinterpret_cast<const u32x4*>(src.v0 + voff + a.v_stride);
   }
 }
 
@@ -162,81 +184,102 @@ __device__ __forceinline__ void store_kv(uint16_t* ks, uint32_t* vt, const KvReg
   }
 }
 
-template <bool F16, int D, bool MASK>
+template <bool F16, int D, int RT, bool MASK>
 __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t* vt, int32_t k0, float scale,
-                                             const typename Ops<F16>::A8 (&qf)[D / 32], int32_t rpos,
-                                             float& m, float& l, f32x4 (&o)[D / 16], uint32_t lane) {
+                                             const typename Ops<F16>::A8 (&qf)[RT][D / 32],
+                                             const int32_t (&rpos)[RT], float (&m)[RT], float (&l)[RT],
+                                             f32x4 (&o)[RT][D / 16], uint32_t lane) {
   using O = Ops<F16>;
   constexpr int LK = D + 8;
   const uint32_t row = lane & 15, grp = lane >> 4;
-  f32x4 s[2];
+  // S^T = K . Q^T for every row tile; each K fragment is read from LDS once
+  f32x4 s[RT][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < RT; ++t) s[t][0] = s[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int st = 0; st < D / 32; ++st) {
       const typename O::A8 kf =
           *reinterpret_cast<const typename O::A8*>(&ks[(16 * h + row) * LK + 32 * st + 8 * grp]);
-      s[h] = O::mma32(kf, qf[st], s[h]);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) s[t][h] = O::mma32(kf, qf[t][st], s[t][h]);
+    }
+  typename O::A4 pa[RT][2];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    // logits: r(r(dot) * scale) as the dtype's einsum and multiply produce
+    float x[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      x[h][0] = s[t][h][0]; x[h][1] = s[t][h][1]; x[h][2] = s[t][h][2]; x[h][3] = s[t][h][3];
+      round2<F16>(x[h][0], x[h][1]);
+      round2<F16>(x[h][2], x[h][3]);
+      x[h][0] *= scale; x[h][1] *= scale; x[h][2] *= scale; x[h][3] *= scale;
+      round2<F16>(x[h][0], x[h][1]);
+      round2<F16>(x[h][2], x[h][3]);
+      if constexpr (MASK) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (k0 + 16 * h + int32_t(4 * grp) + i > rpos[t]) x[h][i] = kNegInf;
+      }
+    }
+    float bm = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                     fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    // Lazy rescaling: exponents stay relative to a reference max m that is
+    // raised -- and O, l rescaled -- only when some row of the wave sees a
+    // block max above m + kRescale (log2 units); otherwise p <= 2^kRescale.
+    // O lives in accumulation registers, so skipping the rescale saves a
+    // read-multiply-write of every O register per block.
+    const float bm2 = bm * kLog2e;
+    if (__any(bm2 > m[t] + kRescale)) {
+      const float mn = fmaxf(m[t], bm2);
+      const float alpha = mn == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[t] - mn);
+      m[t] = mn;
+      l[t] *= alpha;
+      float ao[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha, int(4 * grp + i));
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        o[t][c][0] *= ao[0]; o[t][c][1] *= ao[1]; o[t][c][2] *= ao[2]; o[t][c][3] *= ao[3];
+      }
+    }
+    const float ms = m[t] == kNegInf ? 0.f : m[t];
+    float p[2][4];
+    float sum = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[h][i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
+        sum += p[h][i];
+      }
+    l[t] += sum;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x2 pk = u32x2{O::pack(p[h][0], p[h][1]), O::pack(p[h][2], p[h][3])};
+      pa[t][h] = __builtin_bit_cast(typename O::A4, pk);
     }
   }
-  // logits: r(r(dot) * scale) as the dtype's einsum and multiply produce
-  float x[2][4];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    x[h][0] = s[h][0]; x[h][1] = s[h][1]; x[h][2] = s[h][2]; x[h][3] = s[h][3];
-    round2<F16>(x[h][0], x[h][1]);
-    round2<F16>(x[h][2], x[h][3]);
-    x[h][0] *= scale; x[h][1] *= scale; x[h][2] *= scale; x[h][3] *= scale;
-    round2<F16>(x[h][0], x[h][1]);
-    round2<F16>(x[h][2], x[h][3]);
-    if constexpr (MASK) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (k0 + 16 * h + int32_t(4 * grp) + i > rpos) x[h][i] = kNegInf;
-    }
-  }
-  float bm = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
-                   fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
-  const float mn = fmaxf(m, bm * kLog2e);
-  const float ms = mn == kNegInf ? 0.f : mn;
-  const float alpha = __builtin_amdgcn_exp2f(m - ms);
-  m = mn;
-  float p[2][4];
-  float sum = 0.f;
+  // O += P . V; each transposed V fragment is read from LDS once
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[h][i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
-      sum += p[h][i];
+    for (int c = 0; c < D / 16; ++c) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(&vt[(16 * c + row) * kVtWords + 8 * h + 2 * grp]);
+      const typename O::A4 vb = __builtin_bit_cast(typename O::A4, w);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) o[t][c] = O::mma16(pa[t][h], vb, o[t][c]);
     }
-  l = fmaf(l, alpha, sum);
-  // rescale O rows (row 4*grp + i lives in register i) by their alpha
-  float ao[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha, int(4 * grp + i));
-#pragma unroll
-  for (int t = 0; t < D / 16; ++t) {
-    o[t][0] *= ao[0]; o[t][1] *= ao[1]; o[t][2] *= ao[2]; o[t][3] *= ao[3];
-  }
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const u32x2 pk = u32x2{O::pack(p[h][0], p[h][1]), O::pack(p[h][2], p[h][3])};
-    const typename O::A4 pa = __builtin_bit_cast(typename O::A4, pk);
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-      const u32x2 w = *reinterpret_cast<const u32x2*>(&vt[(16 * t + row) * kVtWords + 8 * h + 2 * grp]);
-      o[t] = O::mma16(pa, __builtin_bit_cast(typename O::A4, w), o[t]);
-    }
-  }
 }
 
-template <bool F16, int D>
+template <bool F16, int D, int RT>
 __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   constexpr int LK = D + 8;
+  constexpr int kRows = 4 * 16 * RT;  // rows per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeyBlock * LK];
   __shared__ __attribute__((aligned(16))) uint32_t vt[2][D * kVtWords];
   __shared__ int32_t s_max[4];
@@ -245,25 +288,31 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   const uint32_t row = lane & 15, grp = lane >> 4;
   const uint32_t kvh = blockIdx.y;
   const uint32_t nrows = a.nq * a.group;
-  const uint32_t ntiles = (nrows + kRowsPerWg - 1) / kRowsPerWg;
+  const uint32_t ntiles = (nrows + kRows - 1) / kRows;
   const uint32_t tile = ntiles - 1 - blockIdx.x;  // latest positions (most keys) first
-  const uint32_t r_wave = tile * kRowsPerWg + wave * 16;
+  const uint32_t r_wave = tile * kRows + wave * 16 * RT;
 
-  // this lane's row: (query, head) and its Q fragments
-  const uint32_t r = r_wave + row;
-  const bool valid = r < nrows;
-  const uint32_t qi = valid ? r / a.group : 0;
-  const uint32_t qh = kvh * a.group + (valid ? r % a.group : 0);
-  const int32_t rpos = valid ? int32_t(a.pos[qi]) : -1;
-  typename O::A8 qf[D / 32];
+  // this lane's rows (one per row tile): (query, head) and their Q fragments
+  typename O::A8 qf[RT][D / 32];
+  int32_t rpos[RT];
+  int32_t wmax = -1, wmin = 0x7fffffff;
 #pragma unroll
-  for (int st = 0; st < D / 32; ++st) {
-    u32x4 w = u32x4(0u);
-    if (valid)
-      w = *reinterpret_cast<const u32x4*>(a.q + int64_t(qi) * a.q_stride + int64_t(qh) * D + 32 * st + 8 * grp);
-    qf[st] = __builtin_bit_cast(typename O::A8, w);
+  for (int t = 0; t < RT; ++t) {
+    const uint32_t r = r_wave + 16 * t + row;
+    const bool valid = r < nrows;
+    const uint32_t qi = valid ? r / a.group : 0;
+    const uint32_t qh = kvh * a.group + (valid ? r % a.group : 0);
+    rpos[t] = valid ? int32_t(a.pos[qi]) : -1;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) {
+      u32x4 w = u32x4(0u);
+      if (valid)
+        w = *reinterpret_cast<const u32x4*>(a.q + int64_t(qi) * a.q_stride + int64_t(qh) * D + 32 * st + 8 * grp);
+      qf[t][st] = __builtin_bit_cast(typename O::A8, w);
+    }
+    wmax = max(wmax, rpos[t]);
+    if (valid) wmin = min(wmin, rpos[t]);
   }
-  int32_t wmax = rpos, wmin = valid ? rpos : 0x7fffffff;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     wmax = max(wmax, __shfl_xor(wmax, off));
@@ -274,62 +323,73 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   const int32_t gmax = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
   const int32_t nblocks = gmax < 0 ? 0 : (gmax + kKeyBlock) / kKeyBlock;
 
-  float m = kNegInf, l = 0.f;
-  f32x4 o[D / 16];
+  float m[RT], l[RT];
+  f32x4 o[RT][D / 16];
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < RT; ++t) {
+    m[t] = kNegInf;
+    l[t] = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) o[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   KvRegs<D> pre;
+  KvSrc<D> src;
+  init_kv_src<D>(a, kvh, src);
   if (nblocks > 0) {
-    load_kv<D>(a, kvh, 0, pre);
+    load_kv<D>(a, src, 0, pre);
     store_kv<D>(ks[0], vt[0], pre);
   }
   __syncthreads();
   for (int32_t b = 0; b < nblocks; ++b) {
     const int32_t k0 = b * kKeyBlock;
     const int buf = b & 1;
-    if (b + 1 < nblocks) load_kv<D>(a, kvh, k0 + kKeyBlock, pre);
+    if (b + 1 < nblocks) load_kv<D>(a, src, b + 1, pre);
     if (k0 <= wmax) {
       if (k0 + kKeyBlock - 1 > wmin)
-        attend_block<F16, D, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+        attend_block<F16, D, RT, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
       else
-        attend_block<F16, D, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+        attend_block<F16, D, RT, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
     }
     if (b + 1 < nblocks) store_kv<D>(ks[buf ^ 1], vt[buf ^ 1], pre);
     __syncthreads();
   }
 
-  // normalize: the row sum is spread over the row's 4 lane groups
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  const float linv = l > 0.f ? 1.f / l : 0.f;
-  float lo[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) lo[i] = __shfl(linv, int(4 * grp + i));
-  // stage the wave's 16 x D output tile in LDS (the K buffers are free now),
-  // then write whole 16-byte pieces of each (query, head) row
+  // normalize and write, one row tile at a time through the wave's LDS
+  // staging area (the K buffers are free now): whole 16-byte pieces per row
   uint16_t* os = &ks[0][0] + wave * 16 * D;
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t) {
-    const uint32_t u01 = O::pack(o[t][0] * lo[0], o[t][1] * lo[1]);
-    const uint32_t u23 = O::pack(o[t][2] * lo[2], o[t][3] * lo[3]);
-    const uint32_t col = 16 * t + row;
-    os[(4 * grp + 0) * D + col] = uint16_t(u01 & 0xffffu);
-    os[(4 * grp + 1) * D + col] = uint16_t(u01 >> 16);
-    os[(4 * grp + 2) * D + col] = uint16_t(u23 & 0xffffu);
-    os[(4 * grp + 3) * D + col] = uint16_t(u23 >> 16);
-  }
-  __syncthreads();
+  for (int t = 0; t < RT; ++t) {
+    float lt = l[t];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const float linv = lt > 0.f ? 1.f / lt : 0.f;
+    float lo[4];
 #pragma unroll
-  for (int c = 0; c < 16 * (D / 8) / 64; ++c) {
-    const uint32_t idx = lane + 64 * c;
-    const uint32_t orow = idx / (D / 8), chunk = idx % (D / 8);
-    const uint32_t rr = r_wave + orow;
-    if (rr < nrows) {
-      const uint32_t oq = rr / a.group, oh = kvh * a.group + rr % a.group;
-      *reinterpret_cast<u32x4*>(a.out + int64_t(oq) * a.out_stride + int64_t(oh) * D + chunk * 8) =
-          *reinterpret_cast<const u32x4*>(&os[orow * D + chunk * 8]);
+    for (int i = 0; i < 4; ++i) lo[i] = __shfl(linv, int(4 * grp + i));
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const uint32_t u01 = O::pack(o[t][c][0] * lo[0], o[t][c][1] * lo[1]);
+      const uint32_t u23 = O::pack(o[t][c][2] * lo[2], o[t][c][3] * lo[3]);
+      const uint32_t col = 16 * c + row;
+      os[(4 * grp + 0) * D + col] = uint16_t(u01 & 0xffffu);
+      os[(4 * grp + 1) * D + col] = uint16_t(u01 >> 16);
+      os[(4 * grp + 2) * D + col] = uint16_t(u23 & 0xffffu);
+      os[(4 * grp + 3) * D + col] = uint16_t(u23 >> 16);
     }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 16 * (D / 8) / 64; ++c) {
+      const uint32_t idx = lane + 64 * c;
+      const uint32_t orow = idx / (D / 8), chunk = idx % (D / 8);
+      const uint32_t rr = r_wave + 16 * t + orow;
+      if (rr < nrows) {
+        const uint32_t oq = rr / a.group, oh = kvh * a.group + rr % a.group;
+        *reinterpret_cast<u32x4*>(a.out + int64_t(oq) * a.out_stride + int64_t(oh) * D + chunk * 8) =
+            *reinterpret_cast<const u32x4*>(&os[orow * D + chunk * 8]);
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -447,14 +507,15 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
   a.d = uint32_t(head_dim);
   a.scale = scale;
   const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
-  const dim3 grid(uint32_t((nrows + kRowsPerWg - 1) / kRowsPerWg), uint32_t(hkv));
+  constexpr int RT = kRowTiles;
+  const dim3 grid(uint32_t((nrows + 64 * RT - 1) / (64 * RT)), uint32_t(hkv));
   const bool f16 = dtype == CBK_DTYPE_F16;
   if (head_dim == 128) {
-    if (f16) hipLaunchKernelGGL((attn_kernel<true, 128>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<false, 128>), grid, dim3(kThreads), 0, s, a);
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 128, RT>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 128, RT>), grid, dim3(kThreads), 0, s, a);
   } else {
-    if (f16) hipLaunchKernelGGL((attn_kernel<true, 64>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<false, 64>), grid, dim3(kThreads), 0, s, a);
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 64, RT>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 64, RT>), grid, dim3(kThreads), 0, s, a);
   }
   return launch_status("blend attention");
 }
