@@ -144,11 +144,11 @@ __device__ __forceinline__ void init_kv_src(const AttnArgs& a, uint32_t kvh, KvS
 
 // Loads key block k0 (= b * kKeyBlock) into registers; blocks entirely inside
 // the context load without per-key checks, the last one zero-fills.
-template <int D>
-__device__ __forceinline__ void load_kv(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
+template <int D, bool EDGE>
+__device__ __forceinline__ void load_kv_block(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
   const int32_t k0 = b * kKeyBlock;
   const int64_t koff = int64_t(k0) * a.k_stride, voff = int64_t(k0) * a.v_stride;
-  const bool inside = k0 + kKeyBlock <= int32_t(a.nk);
+  constexpr bool inside = !EDGE;
 #pragma unroll
   for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
     r.k[p] = u32x4(0u);
@@ -161,6 +161,14 @@ __device__ __forceinline__ void load_kv(const AttnArgs& a, const KvSrc<D>& src, 
     if (inside || key < int32_t(a.nk)) r.v0 = *reinterpret_cast<const u32x4*>(src.v0 + voff);
     if (inside || key + 1 < int32_t(a.nk)) r.v1 = *reinterpret_cast<const u32x4*>(src.v0 + voff + a.v_stride);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void load_kv(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
+  if ((b + 1) * kKeyBlock <= int32_t(a.nk))  // uniform: k0 and nk are scalars
+    load_kv_block<D, false>(a, src, b, r);
+  else
+    load_kv_block<D, true>(a, src, b, r);
 }
 
 // K rows [32][D + 8] (padded); V transposed as words [D][kVtWords], word
@@ -178,17 +186,22 @@ __device__ __forceinline__ void store_kv(uint16_t* ks, uint32_t* vt, const KvReg
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const uint32_t a0 = r.v0[w], a1 = r.v1[w];  // dims 8dc+2w (low), 8dc+2w+1 (high)
-      vt[(dc * 8 + 2 * w) * kVtWords + kp] = (a0 & 0xffffu) | (a1 << 16);
-      vt[(dc * 8 + 2 * w + 1) * kVtWords + kp] = (a0 >> 16) | (a1 & 0xffff0000u);
+      // v_perm_b32: {a0.lo16, a1.lo16} and {a0.hi16, a1.hi16}
+      vt[(dc * 8 + 2 * w) * kVtWords + kp] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+      vt[(dc * 8 + 2 * w + 1) * kVtWords + kp] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
     }
   }
 }
 
+// bf16 / f16 1.0 in both halves of a word: the B operand of the "ones"
+// column whose MFMA accumulates each row's sum of (rounded) probabilities
+template <bool F16> constexpr uint32_t kOnesPair = F16 ? 0x3c003c00u : 0x3f803f80u;
+
 template <bool F16, int D, int RT, bool MASK>
 __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t* vt, int32_t k0, float scale,
                                              const typename Ops<F16>::A8 (&qf)[RT][D / 32],
-                                             const int32_t (&rpos)[RT], float (&m)[RT], float (&l)[RT],
-                                             f32x4 (&o)[RT][D / 16], uint32_t lane) {
+                                             const int32_t (&rpos)[RT], float (&m)[RT],
+                                             f32x4 (&o)[RT][D / 16], f32x4 (&ol)[RT], uint32_t lane) {
   using O = Ops<F16>;
   constexpr int LK = D + 8;
   const uint32_t row = lane & 15, grp = lane >> 4;
@@ -208,37 +221,44 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
   typename O::A4 pa[RT][2];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    // logits: r(r(dot) * scale) as the dtype's einsum and multiply produce
-    float x[2][4];
+    // y = r(dot) * scale; the logits are x = r(y), as the dtype's einsum and
+    // multiply produce them
+    float y[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      x[h][0] = s[t][h][0]; x[h][1] = s[t][h][1]; x[h][2] = s[t][h][2]; x[h][3] = s[t][h][3];
-      round2<F16>(x[h][0], x[h][1]);
-      round2<F16>(x[h][2], x[h][3]);
-      x[h][0] *= scale; x[h][1] *= scale; x[h][2] *= scale; x[h][3] *= scale;
-      round2<F16>(x[h][0], x[h][1]);
-      round2<F16>(x[h][2], x[h][3]);
+      y[h][0] = s[t][h][0]; y[h][1] = s[t][h][1]; y[h][2] = s[t][h][2]; y[h][3] = s[t][h][3];
+      round2<F16>(y[h][0], y[h][1]);
+      round2<F16>(y[h][2], y[h][3]);
+      y[h][0] *= scale; y[h][1] *= scale; y[h][2] *= scale; y[h][3] *= scale;
       if constexpr (MASK) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (k0 + 16 * h + int32_t(4 * grp) + i > rpos[t]) x[h][i] = kNegInf;
+          if (k0 + 16 * h + int32_t(4 * grp) + i > rpos[t]) y[h][i] = kNegInf;
       }
     }
-    float bm = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
-                     fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    // This lane's max over its 8 logits, taken before the second rounding
+    // (rounding is monotonic, and the reference max only needs to bound the
+    // logits within the rescale headroom).
+    const float lm = fmaxf(fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3])),
+                           fmaxf(fmaxf(y[1][0], y[1][1]), fmaxf(y[1][2], y[1][3])));
+    float x[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      x[h][0] = y[h][0]; x[h][1] = y[h][1]; x[h][2] = y[h][2]; x[h][3] = y[h][3];
+      round2<F16>(x[h][0], x[h][1]);
+      round2<F16>(x[h][2], x[h][3]);
+    }
     // Lazy rescaling: exponents stay relative to a reference max m that is
-    // raised -- and O, l rescaled -- only when some row of the wave sees a
-    // block max above m + kRescale (log2 units); otherwise p <= 2^kRescale.
-    // O lives in accumulation registers, so skipping the rescale saves a
-    // read-multiply-write of every O register per block.
-    const float bm2 = bm * kLog2e;
-    if (__any(bm2 > m[t] + kRescale)) {
-      const float mn = fmaxf(m[t], bm2);
+    // raised -- and O rescaled -- only when some lane sees a logit above
+    // m + kRescale (log2 units); otherwise p <= 2^kRescale. The row max across
+    // the row's 4 lane groups is only needed then.
+    if (__any(lm * kLog2e > m[t] + kRescale)) {
+      float bm = lm;
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float mn = fmaxf(m[t], bm * kLog2e + 1.f);  // +1: covers the second rounding
       const float alpha = mn == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[t] - mn);
       m[t] = mn;
-      l[t] *= alpha;
       float ao[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha, int(4 * grp + i));
@@ -246,27 +266,23 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
       for (int c = 0; c < D / 16; ++c) {
         o[t][c][0] *= ao[0]; o[t][c][1] *= ao[1]; o[t][c][2] *= ao[2]; o[t][c][3] *= ao[3];
       }
+      ol[t][0] *= ao[0]; ol[t][1] *= ao[1]; ol[t][2] *= ao[2]; ol[t][3] *= ao[3];
     }
     const float ms = m[t] == kNegInf ? 0.f : m[t];
-    float p[2][4];
-    float sum = 0.f;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[h][i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
-        sum += p[h][i];
-      }
-    l[t] += sum;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const u32x2 pk = u32x2{O::pack(p[h][0], p[h][1]), O::pack(p[h][2], p[h][3])};
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
+      const u32x2 pk = u32x2{O::pack(p[0], p[1]), O::pack(p[2], p[3])};
       pa[t][h] = __builtin_bit_cast(typename O::A4, pk);
     }
   }
-  // O += P . V; each transposed V fragment is read from LDS once
+  // O += P . V (each transposed V fragment read from LDS once), and the row
+  // sums l += P . 1 in the same layout as O
+  const typename O::A4 ones = __builtin_bit_cast(typename O::A4, u32x2{kOnesPair<F16>, kOnesPair<F16>});
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int h = 0; h < 2; ++h) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       const u32x2 w = *reinterpret_cast<const u32x2*>(&vt[(16 * c + row) * kVtWords + 8 * h + 2 * grp]);
@@ -274,6 +290,9 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
 #pragma unroll
       for (int t = 0; t < RT; ++t) o[t][c] = O::mma16(pa[t][h], vb, o[t][c]);
     }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) ol[t] = O::mma16(pa[t][h], ones, ol[t]);
+  }
 }
 
 template <bool F16, int D, int RT>
@@ -320,15 +339,16 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   }
   if (lane == 0) s_max[wave] = wmax;
   __syncthreads();
-  const int32_t gmax = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+  // workgroup-uniform: a scalar loop bound
+  const int32_t gmax = __builtin_amdgcn_readfirstlane(max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
   const int32_t nblocks = gmax < 0 ? 0 : (gmax + kKeyBlock) / kKeyBlock;
 
-  float m[RT], l[RT];
-  f32x4 o[RT][D / 16];
+  float m[RT];
+  f32x4 o[RT][D / 16], ol[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     m[t] = kNegInf;
-    l[t] = 0.f;
+    ol[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) o[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -347,9 +367,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
     if (b + 1 < nblocks) load_kv<D>(a, src, b + 1, pre);
     if (k0 <= wmax) {
       if (k0 + kKeyBlock - 1 > wmin)
-        attend_block<F16, D, RT, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+        attend_block<F16, D, RT, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
       else
-        attend_block<F16, D, RT, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, l, o, lane);
+        attend_block<F16, D, RT, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
     }
     if (b + 1 < nblocks) store_kv<D>(ks[buf ^ 1], vt[buf ^ 1], pre);
     __syncthreads();
@@ -360,13 +380,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   uint16_t* os = &ks[0][0] + wave * 16 * D;
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    float lt = l[t];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
-    const float linv = lt > 0.f ? 1.f / lt : 0.f;
+    // row sums of the rounded probabilities, already in O's layout
     float lo[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lo[i] = __shfl(linv, int(4 * grp + i));
+    for (int i = 0; i < 4; ++i) lo[i] = ol[t][i] > 0.f ? 1.f / ol[t][i] : 0.f;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       const uint32_t u01 = O::pack(o[t][c][0] * lo[0], o[t][c][1] * lo[1]);
