@@ -252,6 +252,8 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
 
     out["sparse_q"] = sparse_q(torch, S, synthetic, dev)
     log(f"sparse_q: {out['sparse_q']}")
+    out["blend_attention"] = blend_attention_bench(torch, dev)
+    log(f"blend attention: {out['blend_attention']}")
     out["store_pipeline"] = store_pipeline(torch, layers, cache, src_slots, args)
     log(f"store pipeline: {out['store_pipeline']}")
     out["blend_load"] = blend_load(torch, synthetic, dev, args)
@@ -299,6 +301,37 @@ def sparse_q(torch, S, synthetic, dev):
         "select_total_ms_with_masks_and_sync": round(total_ms, 3),
         "selected": int(selected.numel()),
     }
+
+
+def _attention_inputs(torch, dev, nq=7000, nk=32767):
+    """Qwen3-30B-A3B blend layer after selection: 7000 selected queries (about
+    the gaps plus 15% of the cached tokens of the blend-load prompt) at
+    sorted uniform positions in [2048, 32767), 32 query heads over the layer
+    buffer's 32767 keys of 4 KV heads x 128 bf16; Q, K ~ N(0,1)/128^(1/4)."""
+    hq, hkv, d = 32, 4, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = (torch.randn((nq, hq, d), generator=g, device=dev) / d ** 0.25).to(torch.bfloat16)
+    k = (torch.randn((nk, hkv, d), generator=g, device=dev) / d ** 0.25).to(torch.bfloat16)
+    v = torch.randn((nk, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    pos = np.sort(np.random.default_rng(0).choice(np.arange(2048, nk), nq, replace=False))
+    return q, k, v, torch.from_numpy(pos).to(dev), pos
+
+
+def blend_attention_bench(torch, dev):
+    """Side-forward attention of the selected queries (_attention_inputs):
+    QK^T and PV flops = 4 * D * Hq * sum(pos + 1) over the causal logits."""
+    from cacheblend_vllm.attention import blend_attention
+
+    q, k, v, pos, pos_np = _attention_inputs(torch, dev)
+    d, hq = q.shape[2], q.shape[1]
+    flops = 4.0 * d * hq * float((pos_np + 1).sum())
+    fn = lambda: blend_attention(q, k, v, pos, d ** -0.5)  # noqa: E731
+    fn()
+    ms = event_time_ms(torch, fn, 5)
+    achieved = flops / (ms / 1e3) / 1e12
+    return {"queries": q.shape[0], "keys": k.shape[0], "q_heads": hq, "kv_heads": k.shape[1], "head_dim": d,
+            "ms": round(ms, 3), "flops": flops, "TFLOPs": round(achieved, 1),
+            "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4)}
 
 
 def store_pipeline(torch, layers, cache, src_slots, args):
@@ -589,6 +622,12 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     for _ in range(max(1, args.steps // 2)):
         S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, out_index=absolute)
     del query, key
+    from cacheblend_vllm.attention import blend_attention
+
+    aq, ak, av, apos, _ = _attention_inputs(torch, dev)
+    for _ in range(max(1, args.steps // 2)):
+        blend_attention(aq, ak, av, apos, 128 ** -0.5)
+    del aq, ak, av
     _profile_host_link(torch, synthetic, cache, src_slots, args, dev)
     torch.cuda.synchronize()
     log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select, "
