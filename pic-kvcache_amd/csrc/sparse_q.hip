@@ -9,10 +9,10 @@
 //   rowstats  one workgroup per (16-query tile, kv head): the G query heads
 //             of the group x 16 queries against 64-key blocks staged in LDS,
 //             online max / sum per row in the log2 domain, merged across
-//             the 16 lanes that share a row -> (m, 1/l) per (head, query)
+//             the 16 lanes that share a row -> m + log2(l) per (head, query)
 //   colsum    one workgroup per (256-key block, kv head): each wave keeps its
 //             64 keys' K fragments in registers and streams the query tiles
-//             (all G heads staged in LDS), accumulating exp2(x - m) / l per
+//             (all G heads staged in LDS), accumulating exp2(x - m - log2 l) per
 //             key column in registers -> partial[kv head][key]; every key is
 //             owned by exactly one wave, so the sum order is fixed and the
 //             result is identical run to run (no float atomics)
@@ -55,7 +55,7 @@ struct SqArgs {
   uint32_t nq, nk, hq, hkv, d, groups;
   float c2;               // scale * log2(e)
   int32_t round_mode;     // 0 none, 1 bf16, 2 f16
-  float2* stats;          // [hq][nq_pad] (m2, 1/l)
+  float2* stats;          // [hq][nq_pad] (m2 + log2(l), unused)
   int32_t* tile_pos;      // [ntiles][2] (min, max) position per query tile
   float* partial;         // [hkv][nk]
   uint32_t nq_pad;
@@ -76,6 +76,12 @@ __device__ __forceinline__ int32_t query_pos(const SqArgs& a, uint32_t qi) {
 __device__ __forceinline__ const char* query_row(const SqArgs& a, uint32_t qi, uint32_t h, uint32_t es) {
   const int64_t row = a.q_index ? a.q_index[qi] : int64_t(qi);
   return a.q + (row * a.q_stride + int64_t(h) * a.d) * es;
+}
+
+// Published per (head, query) row: x = m + log2(l), so that a probability
+// is the single exp2(logit * scale * log2(e) - x) (+inf: an empty row).
+__device__ __forceinline__ float2 row_stats(float m, float l) {
+  return make_float2(l > 0.f ? m + log2f(l) : __builtin_inff(), 0.f);
 }
 
 // Online (max, sum) update in the log2 domain with -inf guards.
@@ -165,23 +171,27 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float r[kColTiles];
+      float raw[kColTiles], r[kColTiles];
 #pragma unroll
-      for (int c = 0; c < kColTiles; c += 2) {
-        r[c] = acc[c][i];
-        r[c + 1] = acc[c + 1][i];
-        round_pair<RMODE>(r[c], r[c + 1]);
-      }
-      if constexpr (MASK) {
-#pragma unroll
-        for (int c = 0; c < kColTiles; ++c) {
+      for (int c = 0; c < kColTiles; ++c) {
+        raw[c] = acc[c][i];
+        if constexpr (MASK) {
           const int32_t key = k0 + c * 16 + int32_t(col);
-          if (key > rpos[i] || key >= int32_t(a.nk)) r[c] = kNegInf;
+          if (key > rpos[i] || key >= int32_t(a.nk)) raw[c] = kNegInf;
         }
       }
-      // max on raw logits (scale > 0 preserves order), one multiply per row
-      const float bm = fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3])) * a.c2;
-      const float mn = fmaxf(m[t][i], bm);
+#pragma unroll
+      for (int c = 0; c < kColTiles; c += 2) {
+        r[c] = raw[c];
+        r[c + 1] = raw[c + 1];
+        round_pair<RMODE>(r[c], r[c + 1]);  // -inf stays -inf
+      }
+      // online max / sum in the log2 domain; the max is taken on the
+      // unrounded dots (canonical floats, no extra max(x, x); rounding is
+      // monotonic, so exponents exceed 0 by at most a rounding step), and
+      // scale > 0 preserves order
+      const float bm2 = fmaxf(fmaxf(raw[0], raw[1]), fmaxf(raw[2], raw[3])) * a.c2;
+      const float mn = fmaxf(m[t][i], bm2);
       const float ms = mn == kNegInf ? 0.f : mn;
       float sum = 0.f;
 #pragma unroll
@@ -260,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
       rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
     if (kb + 1 < nkb) store_block<PIECES, D, LROW>(kblk[(kb + 1) & 1], pre);
   }
-  // merge the 16 lanes that hold the same rows, then publish (m2, 1/l)
+  // merge the 16 lanes that hold the same rows, then publish m2 + log2(l)
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     if (t >= ntiles_w) break;
@@ -275,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
         stats_merge(mm, ll, mo, lo);
       }
       const uint32_t q = q0 + 4 * rgrp + i;
-      if (col == 0 && q < a.nq) a.stats[int64_t(h) * a.nq_pad + q] = make_float2(mm, ll > 0.f ? 1.f / ll : 0.f);
+      if (col == 0 && q < a.nq) a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
     }
   }
 }
@@ -322,13 +332,9 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
       afrag[s] = *reinterpret_cast<const V*>(&qlds[(hl * kQTile + col) * LROW + 32 * s + 8 * rgrp]);
-    float mrow[4], irow[4];
+    float mrow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float2 v = st[hl][4 * rgrp + i];
-      mrow[i] = v.x;
-      irow[i] = v.y;
-    }
+    for (int i = 0; i < 4; ++i) mrow[i] = st[hl][4 * rgrp + i].x;
 #pragma unroll
     for (int c = 0; c < kColTiles; ++c) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -341,7 +347,7 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
       float sum = acc_col[c];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i])) * irow[i];
+        float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i]));
         if constexpr (MASK) p = key > rpos[i] ? 0.f : p;
         sum += p;
       }
@@ -468,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_f32_kernel(const SqArgs 
     const float mo = __shfl_xor(m, off, 64), lo = __shfl_xor(l, off, 64);
     stats_merge(m, l, mo, lo);
   }
-  if (lane == 0) a.stats[int64_t(h) * a.nq_pad + qi] = make_float2(m, l > 0.f ? 1.f / l : 0.f);
+  if (lane == 0) a.stats[int64_t(h) * a.nq_pad + qi] = row_stats(m, l);
 }
 
 // colsum: one thread per (key, kv head), fixed query/head order.
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(kThreads) void sq_colsum_f32_kernel(const SqArgs a)
       float dot = 0.f;
       for (uint32_t e = 0; e < a.d; ++e) dot = fmaf(qrow[e], krow[e], dot);
       const float2 st = a.stats[int64_t(h) * a.nq_pad + qi];
-      acc += __builtin_amdgcn_exp2f(round_logit(dot, a.round_mode) * a.c2 - st.x) * st.y;
+      acc += __builtin_amdgcn_exp2f(round_logit(dot, a.round_mode) * a.c2 - st.x);
     }
   }
   a.partial[int64_t(g) * a.nk + key] = acc;
