@@ -258,6 +258,57 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     log(f"store pipeline: {out['store_pipeline']}")
     out["blend_load"] = blend_load(torch, synthetic, dev, args)
     log(f"blend load: {out['blend_load']}")
+    out["token_matcher"] = token_matcher_bench(args)
+    log(f"token matcher: {out['token_matcher']}")
+    return out
+
+
+def token_matcher_bench(args, n_tokens=131072, n_chunks=512, chunk=256):
+    """Scheduler lookup (host code): find 256-token stored chunks at any
+    offset of a 128K-token prompt, half of it made of registered chunks
+    placed at unaligned offsets. The oracle's leg evaluates every window
+    hash on its own (the reference's sliding-window product) and verifies
+    candidates in Python."""
+    import numpy as np
+
+    from cacheblend_vllm.matcher import TokenRangeMatcher
+
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, 152_000, size=n_tokens)
+    chunks = rng.integers(0, 152_000, size=(n_chunks, chunk))
+    matcher = TokenRangeMatcher(chunk)
+    for i in range(n_chunks):
+        matcher.register(matcher.make_record("bench", i * chunk, chunks[i].tolist()))
+    at = 17
+    for i in range(0, n_chunks, 2):  # every other chunk, 3 tokens apart
+        if at + chunk > n_tokens:
+            break
+        prompt[at:at + chunk] = chunks[i]
+        at += chunk + 3 + chunk
+    tokens = prompt.tolist()  # the scheduler holds prompt ids as a Python list
+    found = matcher.match("bench", tokens)
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        matcher.match("bench", tokens)
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        matcher.match("bench", prompt)
+    ms_array = (time.perf_counter() - t0) / reps * 1e3
+    out = {"prompt_tokens": n_tokens, "registered_chunks": n_chunks, "chunk": chunk,
+           "matches": len(found), "ms_per_lookup": round(ms, 3),
+           "ms_per_lookup_int64_array": round(ms_array, 3)}
+    if not args.skip_cpu_baseline:
+        import oracle as O
+
+        records = [("bench", O.content_hash(c), tuple(int(t) for t in c)) for c in chunks]
+        t0 = time.perf_counter()
+        ref = O.match_tokens(records, "bench", tokens, 0, chunk)
+        out["cpu_baseline_ms"] = round((time.perf_counter() - t0) * 1e3, 3)
+        out["cpu_baseline_kind"] = "port"
+        if [(s, i) for s, i in ref] != [(m.target_start, m.source_start // chunk) for m in found]:
+            raise RuntimeError("token matcher disagrees with the oracle")
     return out
 
 

@@ -318,6 +318,55 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
 int cbk_dilate(const uint8_t* gap_dev, int64_t n, int64_t radius, uint8_t* forced_dev,
                cbk_stream_t stream);
 
+/* ------------------------------------------------ token-range matcher
+ * Host code (no GPU calls): the scheduler-side lookup that finds stored
+ * chunks at any offset of a prompt. Tokens are int64; a chunk's hash is
+ * H(t_0..t_{w-1}) = sum_j (t_j + 1) * 1000003^(w-1-j) mod 2^64.
+ */
+
+/*
+ * out[i] = H(tokens[i .. i + window)) for i in [0, n - window]; writes
+ * nothing when n < window. O(n) rolling update.
+ * Replaces rolling_hash_values (cacheblend_vllm/hashing.py:42-53).
+ */
+int cbk_rolling_hashes(const int64_t* tokens, int64_t n, int64_t window, uint64_t* out);
+
+/* Creates an empty matcher of chunk_size-token records
+ * (TokenRangeMatcher.__init__, cacheblend_vllm/matcher.py:25-32). */
+int cbk_matcher_create(int64_t chunk_size, void** out_handle);
+int cbk_matcher_destroy(void* handle);
+
+/*
+ * Registers chunk_size tokens under (scope, hash) with the caller's record
+ * key; a key registered before is replaced (its old record is removed and
+ * the new one appended after the others of its (scope, hash)). The hash is
+ * taken as given, unchecked against the tokens.
+ * Replaces TokenRangeMatcher.register (cacheblend_vllm/matcher.py:53-63).
+ */
+int cbk_matcher_register(void* handle, uint64_t scope, uint64_t key, uint64_t hash,
+                         const int64_t* tokens);
+
+/* Removes a key's record; unknown keys are ignored
+ * (TokenRangeMatcher.unregister, cacheblend_vllm/matcher.py:65-78). */
+int cbk_matcher_unregister(void* handle, uint64_t key);
+
+/* Number of registered records (TokenRangeMatcher.__len__, matcher.py:131-133). */
+int64_t cbk_matcher_size(void* handle);
+
+/*
+ * Leftmost-greedy, non-overlapping exact matches of registered chunks in
+ * tokens[start .. n) for one scope: scanning window starts in increasing
+ * order, a start at or after the end of the last match whose window hash is
+ * registered and whose tokens equal a record's (the first such record in
+ * registration order) is a match. Writes out_starts[i] (absolute start) and
+ * out_keys[i] for i < *out_count; more than `capacity` matches is an error
+ * (n / chunk_size + 1 is always enough).
+ * Replaces TokenRangeMatcher.match (cacheblend_vllm/matcher.py:80-125).
+ */
+int cbk_matcher_match(void* handle, uint64_t scope, const int64_t* tokens, int64_t n,
+                      int64_t start, int64_t* out_starts, uint64_t* out_keys, int64_t capacity,
+                      int64_t* out_count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,12 @@ Pinning (what checks each function, all in tests/test_oracle.py):
 * blend_attention: float64 closed forms -- identical keys give the mean of
   the visible values, a one-key context returns that value, uniform logits
   average the visible rows, and a brute-force per-query softmax loop.
+* content_hash / window_hashes / match_tokens: reference known answers
+  (tests/test_matcher.py:6-31), closed forms of one- and two-token hashes,
+  the wrap at 2^64, window hashes equal the Horner hash at every offset, and
+  brute-force properties of matches on tiny vocabularies (sorted,
+  non-overlapping, every match verified, no unmatched registered window left
+  between matches).
 """
 
 from __future__ import annotations
@@ -69,6 +75,9 @@ __all__ = [
     "loader_commit",
     "round_f16",
     "blend_attention",
+    "content_hash",
+    "window_hashes",
+    "match_tokens",
 ]
 
 
@@ -571,3 +580,65 @@ def blend_attention(
             if mass is not None:
                 mass[c0:c0 + chunk, h, :] = p.astype(np.float64) @ np.abs(vh.astype(np.float64))
     return (out, mass) if return_mass else out
+
+
+# ---------------------------------------------------------------------------
+# token-range matching (reference cacheblend_vllm/hashing.py, matcher.py)
+# ---------------------------------------------------------------------------
+
+MASK64 = (1 << 64) - 1
+POLY_BASE = 1_000_003
+
+
+def content_hash(tokens: Sequence[int]) -> int:
+    """Horner evaluation of sum_j (t_j + 1) * B^(w-1-j) mod 2^64 with Python
+    integers (reference hashing.py:14-22)."""
+    value = 0
+    for token in tokens:
+        value = (value * POLY_BASE + ((int(token) + 1) & MASK64)) & MASK64
+    return value
+
+
+def window_hashes(tokens: Sequence[int], window: int) -> np.ndarray:
+    """Hash of every full window, each evaluated on its own as a dot product
+    with the power vector B^(w-1) .. B^0 in wrapping uint64 arithmetic
+    (reference hashing.py:25-53)."""
+    if window <= 0:
+        raise ValueError("window must be positive")
+    values = np.asarray(tokens, dtype=np.int64).astype(np.uint64) + np.uint64(1)
+    if values.shape[0] < window:
+        return np.empty(0, dtype=np.uint64)
+    powers = np.array([pow(POLY_BASE, e, 1 << 64) for e in range(window - 1, -1, -1)], dtype=np.uint64)
+    windows = np.lib.stride_tricks.sliding_window_view(values, window)
+    return windows @ powers
+
+
+def match_tokens(records: Sequence[tuple[str, int, tuple[int, ...]]], scope: str,
+                 tokens: Sequence[int], start_offset: int, chunk_size: int) -> list[tuple[int, int]]:
+    """Leftmost-greedy, non-overlapping exact matches (reference
+    matcher.py:80-125). ``records`` are ``(scope, hash, tokens)`` in
+    registration order; returns ``(target_start, record_index)`` pairs, the
+    record being the first registered one of that scope and window hash whose
+    tokens equal the window."""
+    if start_offset < 0 or start_offset > len(tokens):
+        raise ValueError("start_offset is outside the token sequence")
+    by_hash: dict[int, list[int]] = {}
+    for index, (s, h, _) in enumerate(records):
+        if s == scope:
+            by_hash.setdefault(int(h), []).append(index)
+    if not by_hash:
+        return []
+    hashes = window_hashes(list(tokens)[start_offset:], chunk_size)
+    out: list[tuple[int, int]] = []
+    next_allowed = start_offset
+    for rel, value in enumerate(hashes):
+        target = start_offset + rel
+        if target < next_allowed or int(value) not in by_hash:
+            continue
+        window = tuple(int(t) for t in tokens[target:target + chunk_size])
+        for index in by_hash[int(value)]:
+            if tuple(records[index][2]) == window:
+                out.append((target, index))
+                next_allowed = target + chunk_size
+                break
+    return out

@@ -27,6 +27,7 @@ MAX_DILATION_RADIUS = 4096
 
 c_i64 = ctypes.c_int64
 c_i32 = ctypes.c_int32
+c_u64 = ctypes.c_uint64
 c_vp = ctypes.c_void_p
 
 
@@ -119,6 +120,14 @@ _SIGNATURES = {
         [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float,
          c_i32, c_vp, c_i64, c_vp],
     ),
+    "cbk_rolling_hashes": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp]),
+    "cbk_matcher_create": (ctypes.c_int, [c_i64, ctypes.POINTER(c_vp)]),
+    "cbk_matcher_destroy": (ctypes.c_int, [c_vp]),
+    "cbk_matcher_register": (ctypes.c_int, [c_vp, c_u64, c_u64, c_u64, c_vp]),
+    "cbk_matcher_unregister": (ctypes.c_int, [c_vp, c_u64]),
+    "cbk_matcher_size": (c_i64, [c_vp]),
+    "cbk_matcher_match": (ctypes.c_int, [c_vp, c_u64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64,
+                                         ctypes.POINTER(c_i64)]),
     "cbk_sparse_q_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i64, c_i64, c_i64]),
     "cbk_sparse_q_scores": (
         ctypes.c_int,

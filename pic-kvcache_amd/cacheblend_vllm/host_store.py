@@ -9,11 +9,12 @@ that contract and the method names/semantics of ``LocalPinnedCPUStore``
 (reference storage.py:33-294) that the save and load paths call:
 ``begin_put`` (with the content-hash collision check), ``reserve_layer``,
 ``cancel_layer``, ``put_layer``, ``put_layer_host``, ``abort_put``,
-``validate``, ``pin``, ``release``, ``get_layer``, ``clear``. A segment
-commits when every layer is present; a failed or aborted segment is dropped
-as a unit; the byte cap is fail-closed after evicting least recently used,
-committed, unpinned segments. The token-range matcher and lookup RPC are the
-scheduler's control plane and are not part of this package.
+``match``, ``validate``, ``pin``, ``release``, ``get_layer``, ``clear``. A
+segment commits when every layer is present and is then registered with the
+token-range matcher; a failed or aborted segment is dropped as a unit; the
+byte cap is fail-closed after evicting least recently used, committed,
+unpinned segments. The lookup RPC around ``match`` is the scheduler's
+control plane and is not part of this package.
 """
 
 from __future__ import annotations
@@ -28,19 +29,9 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native
+from .hashing import content_hash  # noqa: F401 - the store's segment hash
+from .matcher import FingerprintRecord, TokenRangeMatcher
 from .types import BlendSegment, SegmentId
-
-MASK64 = (1 << 64) - 1
-POLY_BASE = 1_000_003
-
-
-def content_hash(tokens: Sequence[int]) -> int:
-    """Polynomial token hash mod 2^64 (reference hashing.py:10-22)."""
-    value = 0
-    for token in tokens:
-        value = (value * POLY_BASE + ((int(token) + 1) & MASK64)) & MASK64
-    return value
-
 
 @dataclass
 class _Entry:
@@ -185,6 +176,8 @@ class PinnedChunkStore:
         self._pin_sets: dict[str, frozenset[SegmentId]] = {}
         self._bytes = 0
         self._lock = threading.RLock()
+        # committed segments, found at any prompt offset by ``match``
+        self.matcher = TokenRangeMatcher(self.chunk_size)
 
     @property
     def current_bytes(self) -> int:
@@ -193,8 +186,7 @@ class PinnedChunkStore:
 
     @property
     def committed_entries(self) -> int:
-        with self._lock:
-            return sum(1 for e in self._entries.values() if e.committed)
+        return len(self.matcher)
 
     def begin_put(self, model_scope: str, source_start: int, tokens: Sequence[int],
                   num_layers: int) -> SegmentId:
@@ -293,6 +285,7 @@ class PinnedChunkStore:
             self._entries.move_to_end(segment_id)
             if len(entry.layers) == entry.num_layers:
                 entry.committed = True
+                self.matcher.register(FingerprintRecord(segment_id, entry.tokens))
                 return True
             return False
 
@@ -314,6 +307,12 @@ class PinnedChunkStore:
         with self._lock:
             entry = self._entries.get(segment_id)
             return entry is not None and entry.committed
+
+    def match(self, model_scope: str, tokens: Sequence[int],
+              start_offset: int) -> tuple[BlendSegment, ...]:
+        """Committed segments found in ``tokens[start_offset:]``, leftmost
+        first and non-overlapping (reference storage.py:201-208)."""
+        return self.validate(self.matcher.match(model_scope, tokens, start_offset))
 
     def validate(self, segments: Iterable[BlendSegment]) -> tuple[BlendSegment, ...]:
         """The committed subset of ``segments`` (reference storage.py:210-219)."""
@@ -401,7 +400,8 @@ class PinnedChunkStore:
 
     def clear(self) -> None:
         with self._lock:
-            for entry in self._entries.values():
+            for sid, entry in self._entries.items():
+                self.matcher.unregister(sid)
                 self._release_layers(entry)
             self._entries.clear()
             self._pins.clear()
@@ -426,11 +426,13 @@ class PinnedChunkStore:
             if sid == exclude or entry.pins or not entry.committed:
                 continue
             self._entries.pop(sid, None)
+            self.matcher.unregister(sid)
             self._bytes -= entry.size_bytes
             self._release_layers(entry)
 
     def _drop_if_idle(self, segment_id: SegmentId, entry: _Entry) -> None:
         if not entry.reserved and not entry.pins:
             self._entries.pop(segment_id, None)
+            self.matcher.unregister(segment_id)
             self._bytes -= entry.size_bytes
             self._release_layers(entry)

@@ -1,10 +1,11 @@
-"""CPU: the pinned chunk store's segment lifecycle, LRU eviction and byte cap
-(reference storage.py:33-294 semantics; the token matcher is not part of it)."""
+"""CPU: the pinned chunk store's segment lifecycle, LRU eviction, byte cap
+and token-range lookup (reference storage.py:33-294 semantics)."""
 
 import pytest
 import torch
 
-from cacheblend_vllm.host_store import PinnedChunkStore, content_hash
+import oracle as O
+from cacheblend_vllm.host_store import PinnedChunkStore
 from cacheblend_vllm.types import BlendSegment, SegmentId
 
 CH = 4
@@ -25,7 +26,7 @@ def test_commit_after_all_layers_and_known_hash():
     store = PinnedChunkStore(CH, 1 << 20)
     sid, results = _put(store, 0, layers=3)
     assert results == [False, False, True] and store.is_committed(sid)
-    assert sid.content_hash == content_hash(range(CH)) and store.committed_entries == 1
+    assert sid.content_hash == O.content_hash(range(CH)) and store.committed_entries == 1
     assert store.put_layer_host(sid, 1, _chunk(9)) is False  # committed entries are immutable
     with pytest.raises(RuntimeError, match="collision"):
         store._entries[sid].tokens = (7,) * CH
@@ -82,3 +83,67 @@ def test_put_layer_copies_and_get_layer_requires_pin():
     assert torch.equal(got, src) and got.data_ptr() != src.data_ptr()
     with pytest.raises(KeyError):
         store.put_layer(SegmentId("m", 1, 0, CH), 0, src)  # never begun
+
+
+def _put_ref(store, scope, source, token_base, value):
+    """Reference tests/test_storage.py:6-12: a two-layer segment is not found
+    by ``match`` until its last layer commits."""
+    tokens = list(range(token_base, token_base + 4))
+    sid = store.begin_put(scope, source, tokens, num_layers=2)
+    assert not store.put_layer(sid, 0, torch.full((2, 4, 2), value))
+    assert store.match(scope, tokens, 0) == ()
+    assert store.put_layer(sid, 1, torch.full((2, 4, 2), value + 1))
+    return sid, tokens
+
+
+def test_match_sees_only_committed_segments_and_they_pin():
+    """Reference tests/test_storage.py:15-22."""
+    store = PinnedChunkStore(4, 4096)
+    sid, tokens = _put_ref(store, "m", 0, 10, 1)
+    (segment,) = store.match("m", tokens, 0)
+    assert segment.segment_id == sid and segment.target_start == 0
+    assert store.pin("r", [segment]) == (segment,)
+    assert torch.equal(store.get_layer("r", segment, 1), torch.full((2, 4, 2), 2))
+    store.release("r")
+    # found again at any offset of a longer prompt, and not in another scope
+    (again,) = store.match("m", [0, 0, 0] + tokens + [5], 1)
+    assert again.target_start == 3 and store.match("x", tokens, 0) == ()
+
+
+def test_match_forgets_evicted_and_rejected_segments():
+    """Reference tests/test_storage.py:25-43: the pinned entry survives, the
+    rejected one is never matched, the evicted one is no longer matched."""
+    per_entry = 2 * 2 * 4 * 2 * 4
+    store = PinnedChunkStore(4, per_entry)
+    _, tokens1 = _put_ref(store, "m", 0, 10, 1.0)
+    (segment1,) = store.match("m", tokens1, 0)
+    store.pin("r", [segment1])
+    tokens2 = list(range(20, 24))
+    sid2 = store.begin_put("m", 4, tokens2, num_layers=2)
+    assert store.put_layer(sid2, 0, torch.full((2, 4, 2), 2.0)) is None
+    assert store.match("m", tokens1, 0) == (segment1,)
+    assert store.match("m", tokens2, 0) == ()
+    assert store.current_bytes == per_entry
+    store.release("r")
+    _, tokens3 = _put_ref(store, "m", 8, 30, 3.0)
+    assert store.current_bytes <= store.max_bytes
+    assert store.match("m", tokens1, 0) == ()
+    assert store.match("m", tokens3, 0)
+    assert store.committed_entries == 1
+
+
+def test_cancelled_and_cleared_segments_are_not_matched():
+    """Reference tests/test_storage.py:60-73, and ``clear``."""
+    store = PinnedChunkStore(4, 4096)
+    tokens = [1, 2, 3, 4]
+    sid = store.begin_put("m", 0, tokens, num_layers=2)
+    assert store.reserve_layer(sid, 0)
+    assert not store.put_layer_host(sid, 0, torch.ones(2, 4, 2))
+    assert store.reserve_layer(sid, 1)
+    store.cancel_layer(sid, 1)
+    assert store.current_bytes == 0 and store.match("m", tokens, 0) == ()
+    sid = store.begin_put("m", 0, tokens, num_layers=1)
+    assert store.put_layer_host(sid, 0, torch.ones(2, 4, 2))
+    assert len(store.match("m", tokens + tokens, 0)) == 2
+    store.clear()
+    assert store.match("m", tokens, 0) == () and store.committed_entries == 0

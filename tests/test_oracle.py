@@ -419,3 +419,77 @@ def test_blend_attention_zero_query_is_uniform_and_rounding_is_bounded():
 def test_blend_attention_rejects_non_divisible_heads():
     with pytest.raises(ValueError, match="divisible"):
         O.blend_attention(np.zeros((1, 3, 4)), np.zeros((2, 2, 4)), np.zeros((2, 2, 4)), np.zeros(1), 1.0)
+
+
+# ---------------------------------------------------------------- token matching
+
+
+def test_content_hash_closed_forms_and_wrap():
+    assert O.content_hash([]) == 0
+    assert O.content_hash([0]) == 1
+    assert O.content_hash([41]) == 42
+    assert O.content_hash([2, 5]) == 3 * 1_000_003 + 6
+    assert O.content_hash([-1]) == 0  # token + 1 wraps to zero
+    big = [2**40] * 9  # overflows 64 bits: the sum of powers, reduced once
+    assert O.content_hash(big) == sum((2**40 + 1) * 1_000_003 ** (8 - j) for j in range(9)) % 2**64
+
+
+def test_window_hashes_reference_known_answer(golden):
+    case = golden["rolling_hash_every_offset"]
+    tokens, w = case["tokens"], case["window"]
+    got = O.window_hashes(tokens, w)
+    assert [int(v) for v in got] == [O.content_hash(tokens[i:i + w]) for i in range(len(tokens) - w + 1)]
+    assert O.window_hashes(tokens[:2], w).shape == (0,)
+    with pytest.raises(ValueError):
+        O.window_hashes(tokens, 0)
+
+
+def test_window_hashes_long_windows_wrap_like_horner():
+    rng = np.random.default_rng(3)
+    tokens = rng.integers(0, 150_000, size=600).tolist()
+    got = O.window_hashes(tokens, 256)
+    for i in (0, 1, 17, 344):
+        assert int(got[i]) == O.content_hash(tokens[i:i + 256])
+
+
+def _records(case):
+    return [(s, O.content_hash(t), tuple(t)) for s, _, t in case["register"]]
+
+
+def test_match_tokens_reference_known_answers(golden):
+    case = golden["matcher_offsets_and_overlaps"]
+    records = _records(case)
+    got = O.match_tokens(records, "m", case["query"], case["start_offset"], case["chunk_size"])
+    sources = [r[1] for r in case["register"]]
+    assert [[t, sources[i]] for t, i in got] == case["expected_target_source"]
+    assert O.match_tokens(records, "other", case["query"], 0, 4) == []
+    col = golden["matcher_collision_verified"]
+    fake = [(col["fake_record"]["scope"], O.content_hash(col["fake_record"]["hash_of"]),
+             tuple(col["fake_record"]["tokens"]))]
+    assert O.match_tokens(fake, "m", col["query"], 0, col["chunk_size"]) == col["expected"]
+    with pytest.raises(ValueError):
+        O.match_tokens(records, "m", [1, 2], 3, 4)
+
+
+def test_match_tokens_brute_force_properties():
+    """Tiny vocabularies: matches are sorted, non-overlapping, verified, and
+    greedy -- no registered chunk occurs at a start between matches that the
+    scan could have taken."""
+    rng = np.random.default_rng(11)
+    for trial in range(300):
+        w = int(rng.integers(1, 4))
+        tokens = rng.integers(0, 3, size=int(rng.integers(0, 24))).tolist()
+        chunks = {tuple(rng.integers(0, 3, size=w).tolist()) for _ in range(int(rng.integers(1, 5)))}
+        records = [("m", O.content_hash(c), c) for c in sorted(chunks)]
+        start = int(rng.integers(0, len(tokens) + 1))
+        got = O.match_tokens(records, "m", tokens, start, w)
+        # brute force: walk positions, take every registered window greedily
+        expect, p = [], start
+        while p + w <= len(tokens):
+            window = tuple(tokens[p:p + w])
+            if window in chunks:
+                expect.append((p, sorted(chunks).index(window)))
+                p += w
+            else:
+                p += 1
+        assert got == expect, (trial, tokens, chunks, start)
