@@ -29,7 +29,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native
-from .hashing import content_hash  # noqa: F401 - the store's segment hash
+from .hashing import as_token_array, content_hash, rolling_hash_values
 from .matcher import FingerprintRecord, TokenRangeMatcher
 from .types import BlendSegment, SegmentId
 
@@ -197,16 +197,43 @@ class PinnedChunkStore:
         key = tuple(int(t) for t in tokens)
         sid = SegmentId(model_scope, content_hash(key), source_start, len(key))
         with self._lock:
-            entry = self._entries.get(sid)
-            if entry is None:
-                self._entries[sid] = _Entry(num_layers, key)
-            else:
-                if entry.tokens != key:
-                    raise RuntimeError("content-hash collision for an existing segment id")
-                if entry.num_layers != num_layers:
-                    raise ValueError("num_layers changed for an existing segment")
-                self._entries.move_to_end(sid)
+            self._begin_locked(sid, key, num_layers)
         return sid
+
+    def begin_put_chunks(self, model_scope: str, tokens: Sequence[int], start: int, end: int,
+                         num_layers: int) -> list[SegmentId]:
+        """``begin_put`` for every ``chunk_size`` chunk of ``tokens[start:end]``
+        (source_start = the chunk's offset), hashing all of them in one
+        native call."""
+        if num_layers <= 0:
+            raise ValueError("num_layers must be positive")
+        c = self.chunk_size
+        if start < 0 or end > len(tokens) or (end - start) % c:
+            raise ValueError(f"[{start}, {end}) is not a whole number of {c}-token chunks of the prompt")
+        if end <= start:
+            return []
+        values = as_token_array(tokens[start:end])
+        hashes = rolling_hash_values(values, c)[::c].tolist()
+        span = values.tolist()  # Python ints, for the collision check
+        ids = []
+        with self._lock:
+            for i, value in enumerate(hashes):
+                key = tuple(span[i * c:(i + 1) * c])
+                sid = SegmentId(model_scope, int(value), start + i * c, c)
+                self._begin_locked(sid, key, num_layers)
+                ids.append(sid)
+        return ids
+
+    def _begin_locked(self, sid: SegmentId, key: tuple[int, ...], num_layers: int) -> None:
+        entry = self._entries.get(sid)
+        if entry is None:
+            self._entries[sid] = _Entry(num_layers, key)
+        else:
+            if entry.tokens != key:
+                raise RuntimeError("content-hash collision for an existing segment id")
+            if entry.num_layers != num_layers:
+                raise ValueError("num_layers changed for an existing segment")
+            self._entries.move_to_end(sid)
 
     def cancel_layer(self, segment_id: SegmentId, layer_id: int) -> None:
         """Give up a reserved layer: an uncommitted segment fails as a unit
@@ -236,15 +263,23 @@ class PinnedChunkStore:
 
     def reserve_layer(self, segment_id: SegmentId, layer_id: int) -> bool:
         with self._lock:
-            entry = self._entries.get(segment_id)
-            if entry is None:
-                return False
-            if not 0 <= layer_id < entry.num_layers:
-                raise ValueError(f"layer {layer_id} is outside [0, {entry.num_layers})")
-            if entry.failed or layer_id in entry.layers or layer_id in entry.reserved:
-                return False
-            entry.reserved.add(layer_id)
-            return True
+            return self._reserve_locked(segment_id, layer_id)
+
+    def reserve_layers(self, segment_ids: Sequence[SegmentId], layer_id: int) -> list[bool]:
+        """``reserve_layer`` for each segment under one lock acquisition."""
+        with self._lock:
+            return [self._reserve_locked(sid, layer_id) for sid in segment_ids]
+
+    def _reserve_locked(self, segment_id: SegmentId, layer_id: int) -> bool:
+        entry = self._entries.get(segment_id)
+        if entry is None:
+            return False
+        if not 0 <= layer_id < entry.num_layers:
+            raise ValueError(f"layer {layer_id} is outside [0, {entry.num_layers})")
+        if entry.failed or layer_id in entry.layers or layer_id in entry.reserved:
+            return False
+        entry.reserved.add(layer_id)
+        return True
 
     def put_layer_host(self, segment_id: SegmentId, layer_id: int,
                        cpu_tensor: torch.Tensor) -> bool | None:

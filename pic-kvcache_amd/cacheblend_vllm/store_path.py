@@ -108,7 +108,7 @@ class StoreStreamWriter:
         streams=CudaStreams,
         store_stream=None,
         slab=None,
-        max_workgroups: int = 128,
+        max_workgroups: int = 256,
         slab_transfer: str = "host_write",
     ):
         """``slab`` (a PinnedChunkSlab): every chunk gets its own pinned slot,
@@ -117,7 +117,8 @@ class StoreStreamWriter:
         "host_write" -- (default) the gather kernel writes the slots
                         directly over the host link: no staging, one launch
                         per layer, holding up to ``max_workgroups``
-                        workgroups for the transfer;
+                        workgroups for the transfer (zero-copy write rate
+                        grows with the CUs issuing: 256 reach about 55 GB/s);
         "dma"        -- gather into a chunk-major device staging, then one
                         hipMemcpyAsync per run of consecutive slots (HIP
                         runs it as its own copy kernel).
@@ -158,20 +159,27 @@ class StoreStreamWriter:
                 continue
             usable = min(request.save_end, len(request.token_ids), request.slot_mapping.numel())
             usable = usable // self.chunk_size * self.chunk_size
-            pending: list[tuple[SegmentId, int, int]] = []
-            slot_parts: list[torch.Tensor] = []
-            for start, segment_id in self._request_save_segments(request, usable):
-                if not self._store.reserve_layer(segment_id, layer_id):
-                    continue
-                pending.append((segment_id, layer_id, self.chunk_size))
-                slot_parts.append(request.slot_mapping[start : start + self.chunk_size])
+            segments = self._request_save_segments(request, usable)
+            reserve_many = getattr(self._store, "reserve_layers", None)
+            if reserve_many is not None:
+                reserved = reserve_many([sid for _, sid in segments], layer_id)
+            else:
+                reserved = [self._store.reserve_layer(sid, layer_id) for _, sid in segments]
+            pending: list[tuple[SegmentId, int, int]] = [
+                (sid, layer_id, self.chunk_size) for (_, sid), ok in zip(segments, reserved) if ok
+            ]
             if not pending:
                 continue
+            if len(pending) == len(segments):  # chunks 0..n-1: one slice of the slot mapping
+                slots = request.slot_mapping[: len(segments) * self.chunk_size]
+            else:
+                slots = torch.cat([request.slot_mapping[start : start + self.chunk_size]
+                                   for (start, _), ok in zip(segments, reserved) if ok])
             trace = self._trace.enabled
             started = time.monotonic_ns() if trace else 0
             try:
                 self._enqueue_store_batch(
-                    pending, kv_layer, torch.cat(slot_parts), request_id=request.request_id,
+                    pending, kv_layer, slots, request_id=request.request_id,
                     store_enqueued_ns=time.monotonic_ns() if trace else None,
                 )
                 if trace:
@@ -192,6 +200,11 @@ class StoreStreamWriter:
         """Chunk identities hashed once per request (reference connector.py:363-382)."""
         segments = self._save_segments.setdefault(request.request_id, [])
         start = len(segments) * self.chunk_size
+        begin_chunks = getattr(self._store, "begin_put_chunks", None)
+        if begin_chunks is not None and start < usable:
+            ids = begin_chunks(self.model_scope, request.token_ids, start, usable, self.num_layers)
+            segments.extend(zip(range(start, usable, self.chunk_size), ids))
+            start = usable
         while start < usable:
             end = start + self.chunk_size
             segment_id = self._store.begin_put(

@@ -147,3 +147,20 @@ def test_cancelled_and_cleared_segments_are_not_matched():
     assert len(store.match("m", tokens + tokens, 0)) == 2
     store.clear()
     assert store.match("m", tokens, 0) == () and store.committed_entries == 0
+
+
+def test_begin_put_chunks_equals_per_chunk_begin_put():
+    tokens = list(range(1000, 1000 + 4 * CH)) + [7]
+    a, b = PinnedChunkStore(CH, 1 << 20), PinnedChunkStore(CH, 1 << 20)
+    ids = a.begin_put_chunks("m", tokens, CH, 4 * CH, 2)
+    assert ids == [b.begin_put("m", s, tokens[s:s + CH], 2) for s in range(CH, 4 * CH, CH)]
+    assert [sid.content_hash for sid in ids] == [O.content_hash(tokens[s:s + CH]) for s in range(CH, 4 * CH, CH)]
+    assert a.begin_put_chunks("m", tokens, 0, 0, 2) == []
+    with pytest.raises(ValueError, match="whole number"):
+        a.begin_put_chunks("m", tokens, 0, CH + 1, 2)
+    with pytest.raises(ValueError, match="num_layers changed"):
+        a.begin_put_chunks("m", tokens, CH, 2 * CH, 3)
+    assert a.reserve_layers(ids + [SegmentId("m", 1, 0, CH)], 1) == [True, True, True, False]
+    assert a.reserve_layers(ids, 1) == [False, False, False]
+    with pytest.raises(ValueError, match="outside"):
+        a.reserve_layers(ids, 2)

@@ -123,6 +123,9 @@ def test_enqueue_store_reuses_staging_and_offloads_on_one_stream(monkeypatch):
 
     monkeypatch.setattr(SP, "gather_paged_kv", gather)
     monkeypatch.setattr(torch, "empty", unpinned_empty)
+    # the fake layer has no device planes: keep the host slot list (a GPU
+    # host would otherwise upload it next to the fake cache)
+    monkeypatch.setattr(w, "_upload_slots", lambda _rid, slots, _kv: slots)
     w._enqueue_store_batch([("segment", 0, 4)], object(), torch.arange(4), request_id="request")
     first_staging = w._store_staging_by_request["request"]
     w._enqueue_store_batch([("segment", 1, 4)], object(), torch.arange(4), request_id="request")
