@@ -336,11 +336,13 @@ def sparse_q(torch, S, synthetic, dev):
     ms = event_time_ms(torch, fn, 3)
     sel = S.BlendSelector(CacheBlendConfig.from_extra_config(
         {"selection_strategy": "sparse_q", "check_layers": [1]}), 16)
+    sel.sparse_q_select(query, key, absolute, gap, scale, 1)  # first call: workspaces, code loading
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    selected, stats = sel.sparse_q_select(query, key, absolute, gap, scale, 1)
+    for _ in range(3):
+        selected, stats = sel.sparse_q_select(query, key, absolute, gap, scale, 1)
     torch.cuda.synchronize()
-    total_ms = (time.perf_counter() - t0) * 1e3
+    total_ms = (time.perf_counter() - t0) / 3 * 1e3
     achieved = 2 * flops_pass / (ms / 1e3) / 1e12
     return {
         "queries": nq, "keys": nk, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
