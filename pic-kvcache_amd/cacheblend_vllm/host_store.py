@@ -174,6 +174,8 @@ class PinnedChunkStore:
         self._entries: OrderedDict[SegmentId, _Entry] = OrderedDict()
         self._pins: dict[str, tuple[SegmentId, ...]] = {}
         self._pin_sets: dict[str, frozenset[SegmentId]] = {}
+        # request -> (segment tuple, [(id, entry)]) for layer_chunk_addresses
+        self._pin_entries: dict[str, tuple] = {}
         self._bytes = 0
         self._lock = threading.RLock()
         # committed segments, found at any prompt offset by ``match``
@@ -381,6 +383,7 @@ class PinnedChunkStore:
     def release(self, request_id: str) -> None:
         with self._lock:
             self._pin_sets.pop(request_id, None)
+            self._pin_entries.pop(request_id, None)
             for sid in self._pins.pop(request_id, ()):
                 entry = self._entries.get(sid)
                 if entry is not None:
@@ -407,27 +410,38 @@ class PinnedChunkStore:
         one layer of pinned segments, for kernels that read the chunks over
         the host link, with their common ``(chunk_tokens, row_shape, dtype)``;
         None when any chunk is not kernel-addressable (``chunk_address``) or
-        the geometries differ. Each stored chunk is validated once."""
+        the geometries differ. Each stored chunk is validated once; the
+        segments' entries are looked up (and touched for the LRU order) once
+        per request and segment tuple: a loader asks for every layer of the
+        same plan, and pinned entries stay put until ``release``."""
         with self._lock:
-            pinned = self._pin_sets.get(request_id, ())
+            cached = self._pin_entries.get(request_id)
+            if cached is not None and cached[0] is segments:
+                entries = cached[1]
+            else:
+                pinned = self._pin_sets.get(request_id, ())
+                entries = []
+                for seg in segments:
+                    if seg.segment_id not in pinned:
+                        raise RuntimeError(f"segment {seg.segment_id} is not pinned by {request_id}")
+                    entry = self._entries.get(seg.segment_id)
+                    if entry is None or not entry.committed:
+                        raise KeyError(seg.segment_id)
+                    self._entries.move_to_end(seg.segment_id)
+                    entries.append((seg.segment_id, entry))
+                if request_id in self._pin_sets and isinstance(segments, tuple):
+                    self._pin_entries[request_id] = (segments, entries)
             flat: list[int] = []
             geometry = None
-            for seg in segments:
-                if seg.segment_id not in pinned:
-                    raise RuntimeError(f"segment {seg.segment_id} is not pinned by {request_id}")
-                entry = self._entries.get(seg.segment_id)
-                if entry is None or not entry.committed:
-                    raise KeyError(seg.segment_id)
-                if layer_id in entry.addresses:
-                    info = entry.addresses[layer_id]
-                else:
+            for sid, entry in entries:
+                info = entry.addresses.get(layer_id, False)
+                if info is False:
                     tensor = entry.layers.get(layer_id)
                     if tensor is None:
-                        raise KeyError(f"layer {layer_id} is not stored for {seg.segment_id}")
+                        raise KeyError(f"layer {layer_id} is not stored for {sid}")
                     info = entry.addresses[layer_id] = chunk_address(tensor)
                 if info is None or (geometry is not None and info[2] != geometry):
                     return None
-                self._entries.move_to_end(seg.segment_id)
                 geometry = info[2]
                 flat.append(info[0])
                 flat.append(info[1])
@@ -441,6 +455,7 @@ class PinnedChunkStore:
             self._entries.clear()
             self._pins.clear()
             self._pin_sets.clear()
+            self._pin_entries.clear()
             self._bytes = 0
 
     def _release_layers(self, entry: _Entry) -> None:

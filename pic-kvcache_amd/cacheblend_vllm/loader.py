@@ -123,6 +123,7 @@ class PagedBlendLoader:
         zero_copy: bool | str = "auto",
         max_workgroups: int = 256,
         dma_min_run_bytes: int = 1 << 20,
+        dma_staging_bytes: int = 1 << 30,
     ):
         """How hit rows cross the host link, per layer:
         DMA -- the chunks, coalesced into runs where adjacent in host
@@ -134,7 +135,10 @@ class PagedBlendLoader:
                rows in place (``max_workgroups`` bounds the CUs it holds).
         ``zero_copy``: True forces host reads where possible, False forces
         DMA, "auto" reads in place only when the runs average fewer than
-        ``dma_min_run_bytes`` per copy, where per-copy DMA cost dominates."""
+        ``dma_min_run_bytes`` per copy, where per-copy DMA cost dominates.
+        ``dma_staging_bytes`` bounds the device ring the DMA fills (at least
+        two layers' hits): with room for every layer the copies of a request
+        never wait for an assembly."""
         if zero_copy not in (True, False, "auto"):
             raise ValueError("zero_copy must be True, False or 'auto'")
         self.kv_caches = kv_caches
@@ -150,6 +154,11 @@ class PagedBlendLoader:
         self.device = key.device
         self.dtype = key.dtype
         self.row_shape = tuple(key.shape[2:])
+        self._row_bytes = int(np.prod(self.row_shape)) * key.element_size()
+        # hit bytes of each segment's plane, for the run search over host addresses
+        lengths = np.array([seg.length for seg in plan.segments], dtype=np.int64)
+        self._seg_plane_bytes = lengths * self._row_bytes
+        self._seg_row_off = np.concatenate(([0], np.cumsum(lengths)))
         if self.slot_mapping.numel() < plan.allocation_end:
             raise ValueError(
                 f"slot_mapping has {self.slot_mapping.numel()} slots for an allocation of "
@@ -169,10 +178,14 @@ class PagedBlendLoader:
         self._events: dict[int, torch.cuda.Event] = {}
         self._reuse_events: dict[int, torch.cuda.Event] = {}
         self._staging: list[torch.Tensor] = []
-        # hit staging by layer parity, so layer l + 1's DMA (on the copy
-        # stream) overlaps layer l's assembly; _hit_free[i] fences reuse
-        self._hit_stagings: list[torch.Tensor | None] = [None, None]
+        # ring of hit stagings, one slot per layer up to dma_staging_bytes:
+        # the copy stream carries no cross-stream waits (a wait between two
+        # DMA copies on one stream left the engine idle ~50-100 us per
+        # layer); the host fences a slot's reuse (_hit_free) only when the
+        # ring wraps
+        self._hit_ring: torch.Tensor | None = None
         self._hit_free: dict[int, torch.cuda.Event] = {}
+        self._dma_staging_bytes = int(dma_staging_bytes)
         self._copy_stream: torch.cuda.Stream | None = None
         self._descs: dict[int, _native.KVDesc] = {}
         self._zero_copy = zero_copy
@@ -229,34 +242,40 @@ class PagedBlendLoader:
     def _address_runs(self, flat: list[int], row_bytes: int) -> list[tuple[int, int, int, int]]:
         """Maximal runs of consecutive segments whose K (and V) planes are
         adjacent in host memory: ``(first_hit_row, tokens, k_addr, v_addr)``."""
-        runs: list[list[int]] = []
-        off = 0
-        for i, seg in enumerate(self.plan.segments):
-            k, v, n = flat[2 * i], flat[2 * i + 1], seg.length
-            if runs:
-                r = runs[-1]
-                if k == r[2] + r[1] * row_bytes and v == r[3] + r[1] * row_bytes:
-                    r[1] += n
-                    off += n
-                    continue
-            runs.append([off, n, k, v])
-            off += n
-        return [tuple(r) for r in runs]
+        kv = np.array(flat, dtype=np.uint64).reshape(-1, 2)
+        plane = self._seg_plane_bytes.astype(np.uint64)
+        # segment i + 1 continues segment i's run when both planes follow on
+        joined = (kv[1:, 0] == kv[:-1, 0] + plane[:-1]) & (kv[1:, 1] == kv[:-1, 1] + plane[:-1])
+        starts = np.flatnonzero(np.concatenate(([True], ~joined)))
+        ends = np.append(starts[1:], len(kv))
+        row_off = self._seg_row_off
+        return [(int(row_off[a]), int(row_off[b] - row_off[a]), int(kv[a, 0]), int(kv[a, 1]))
+                for a, b in zip(starts.tolist(), ends.tolist())]
+
+    def _hit_slot(self, layer_id: int) -> int:
+        return layer_id % self._hit_ring.shape[0]
 
     def _ensure_hit_staging(self, layer_id: int) -> torch.Tensor:
-        index = layer_id % 2
-        if self._hit_stagings[index] is None:
-            staging = torch.empty((2, self.plan.hit_tokens, *self.row_shape), dtype=self.dtype, device=self.device)
+        """The layer's slot of the hit ring, allocated on first use on the
+        stream that fills it (the copy stream when there is one) and kept
+        alive for the Load stream that reads it."""
+        if self._hit_ring is None:
+            per_layer = 2 * self.plan.hit_tokens * self._row_bytes
+            slots = max(2, min(len(self.kv_caches), self._dma_staging_bytes // max(1, per_layer)))
+            shape = (slots, 2, self.plan.hit_tokens, *self.row_shape)
             if self._copy_stream is not None:
-                staging.record_stream(self._copy_stream)
-            self._hit_stagings[index] = staging
-        return self._hit_stagings[index]
+                with torch.cuda.stream(self._copy_stream):
+                    self._hit_ring = torch.empty(shape, dtype=self.dtype, device=self.device)
+                self._hit_ring.record_stream(self._load_stream)
+            else:
+                self._hit_ring = torch.empty(shape, dtype=self.dtype, device=self.device)
+        return self._hit_ring[self._hit_slot(layer_id)]
 
     def _load_hits(self, layer_id: int) -> None:
         found = self._chunk_addresses(layer_id)
         if found is not None:
             chunk, flat = found
-            row_bytes = int(np.prod(self.row_shape)) * torch.empty((), dtype=self.dtype).element_size()
+            row_bytes = self._row_bytes
             runs = self._address_runs(flat, row_bytes)
             avg = self.plan.hit_tokens * row_bytes / max(1, len(runs))
             host_read = self._zero_copy is True or (self._zero_copy == "auto" and avg < self._dma_min_run_bytes)
@@ -293,14 +312,12 @@ class PagedBlendLoader:
                 _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n,
                                                              _native.stream_handle(self.device)), "hit runs H2D")
                 return
-            # DMA on the copy stream: waits only for the assembly that last
-            # read this staging, so it runs behind the previous layer's copy
-            # instead of behind its assembly
-            free = self._hit_free.pop(layer_id % 2, None)
-            if free is not None:
-                self._copy_stream.wait_event(free)
-            else:
-                self._copy_stream.wait_stream(self._load_stream)  # staging allocated there
+            # DMA on the copy stream, back to back with the previous layer's;
+            # a ring slot is refilled only after the assembly that read it
+            # (host-side fence: the host is then a full ring ahead of the copies)
+            free = self._hit_free.pop(self._hit_slot(layer_id), None)
+            if free is not None and not free.query():
+                free.synchronize()
             _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n, self._copy_stream.cuda_stream),
                           "hit runs H2D")
             copied = torch.cuda.Event()
@@ -316,7 +333,7 @@ class PagedBlendLoader:
 
     def _assemble(self, layer_id: int, buffer: torch.Tensor, rotary_emb) -> None:
         es = buffer.element_size()
-        hit = self._hit_stagings[layer_id % 2]
+        hit = self._hit_ring[self._hit_slot(layer_id)] if self._hit_ring is not None else None
         heads = int(np.prod(self.row_shape[:-1])) if len(self.row_shape) > 1 else 1
         head_dim = self.row_shape[-1]
         table = None
@@ -411,10 +428,10 @@ class PagedBlendLoader:
             if self.plan.segments:
                 self._load_hits(layer_id)
             self._assemble(layer_id, buffer, rotary_emb)
-            if self._copy_stream is not None and self._hit_stagings[index] is not None:
+            if self._copy_stream is not None and self._hit_ring is not None and layer_id not in self._zc_layers:
                 done = torch.cuda.Event()
                 done.record(self._load_stream)
-                self._hit_free[index] = done
+                self._hit_free[self._hit_slot(layer_id)] = done
             self._buffers[layer_id] = buffer
 
         if self._load_stream is None:

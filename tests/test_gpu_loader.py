@@ -205,6 +205,39 @@ def test_loader_bf16_relocation_bit_exact_vs_oracle(neox, zero_copy):
     assert (len(loader._zc_layers) > 0) == zero_copy
 
 
+@pytest.mark.parametrize("ring_slots", [2, 3, 7])
+def test_loader_dma_ring_wraps_bit_exact(ring_slots):
+    """DMA path with a hit ring shorter than the layer count: slots are
+    refilled after the host-side fence on the assembly that last read them;
+    every layer still equals the oracle."""
+    heads, dim, bs, chunk, L = 4, 128, 16, 64, 7
+    segs = [(0, 100, 128), (512, 300, 64), (64, 400, 192)]
+    layers, store, plan, slots, hosts = _blend_setup(L, 200, bs, heads, dim, 37, segs, 700,
+                                                     torch.bfloat16, chunk, seed=11)
+    rope = Rope(dim, 2048, True)
+    per_layer = 2 * plan.hit_tokens * heads * dim * 2
+    loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk),
+                              zero_copy=False, dma_staging_bytes=ring_slots * per_layer)
+    cache = rope.cos_sin_cache.cpu().numpy()
+
+    def reloc(old, new, k_bits):
+        k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
+        return O.f32_to_bf16(O.relocate_key(cache, old, new, k, dim, True, bf16=True)).reshape(k_bits.shape)
+
+    loader.prefetch(0, rope)
+    for l in range(L):
+        buf = loader.get(l)
+        loader.prefetch(l + 1, rope)
+        want = O.loader_assemble(
+            _bits(layers[l]), slots.numpy(), bs, plan.apc_prefix_tokens, plan.allocation_end,
+            [(s, t, _bits(hosts[i, l])) for i, (s, t, _) in enumerate(segs)], relocate=reloc,
+        )
+        np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
+        loader.commit(l, buf)
+    torch.cuda.synchronize()
+    assert loader._hit_ring.shape[0] == min(ring_slots, L) and not loader._zc_layers
+
+
 def test_loader_without_relocation_is_a_bit_copy():
     heads, dim, bs, chunk = 2, 64, 16, 32
     segs = [(40, 40, 64), (200, 200, 32)]  # source == target

@@ -151,3 +151,42 @@ def test_layer_chunk_addresses_requires_pins_and_addressable_chunks():
     store.release("r")
     with pytest.raises(RuntimeError, match="not pinned"):
         store.get_layer("r", seg, 0)
+
+
+def test_loader_address_runs_join_adjacent_segments():
+    """The loader's run search over host chunk addresses: segments join a
+    run exactly when both their K and V planes follow the previous
+    segment's (checked against a direct scan on random layouts)."""
+    import types
+
+    import numpy as np
+
+    from cacheblend_vllm.loader import PagedBlendLoader
+
+    rng = np.random.default_rng(4)
+    row = 1024
+    for _ in range(200):
+        lengths = rng.integers(1, 5, size=int(rng.integers(1, 12))) * 16
+        k = v = None
+        flat = []
+        for i, n in enumerate(lengths):
+            if i and rng.random() < 0.6:  # continue both planes
+                k, v = k + prev * row, v + prev * row
+            elif i and rng.random() < 0.5:  # only K continues
+                k, v = k + prev * row, v + 4096 * row
+            else:
+                k, v = int(rng.integers(1, 1 << 30)) * 64, int(rng.integers(1, 1 << 30)) * 64
+            flat += [k, v]
+            prev = int(n)
+        fake = types.SimpleNamespace(_seg_plane_bytes=lengths.astype(np.int64) * row,
+                                     _seg_row_off=np.concatenate(([0], np.cumsum(lengths))))
+        got = PagedBlendLoader._address_runs(fake, flat, row)
+        want, off = [], 0
+        for i, n in enumerate(lengths.tolist()):
+            kk, vv = flat[2 * i], flat[2 * i + 1]
+            if want and kk == want[-1][2] + want[-1][1] * row and vv == want[-1][3] + want[-1][1] * row:
+                want[-1][1] += n
+            else:
+                want.append([off, n, kk, vv])
+            off += n
+        assert got == [tuple(w) for w in want]
