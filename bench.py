@@ -715,7 +715,7 @@ def _profile_host_link(torch, synthetic, cache, src_slots, args, dev):
     lib = _native.load()
     for _ in range(args.steps):
         _native.check(lib.cbk_paged_gather_chunks(desc, slots_dev.data_ptr(), src_slots.numel(), 256, k_ptrs,
-                                                  v_ptrs, desc.row_bytes, 128, None,
+                                                  v_ptrs, desc.row_bytes, 256, None,
                                                   _native.stream_handle(dev)), "profile gather_chunks")
     torch.cuda.synchronize()
     for c in chunks:
