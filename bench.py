@@ -188,7 +188,9 @@ def main() -> int:
     }
 
     if not args.skip_extras:
-        result.update(extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev))
+        reload_slots = synthetic.block_slots(perm[1024:1536], BS, T).to(dev)
+        result.update(extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev,
+                             reload_slots))
 
     if not args.skip_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, synthetic)
@@ -196,7 +198,7 @@ def main() -> int:
     return 0
 
 
-def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev):
+def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev, reload_slots):
     out = {}
     L = len(layers)
     BS = cache.block_size
@@ -254,7 +256,7 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     log(f"sparse_q: {out['sparse_q']}")
     out["blend_attention"] = blend_attention_bench(torch, dev)
     log(f"blend attention: {out['blend_attention']}")
-    out["store_pipeline"] = store_pipeline(torch, layers, cache, src_slots, args)
+    out["store_pipeline"] = store_pipeline(torch, layers, cache, src_slots, args, reload_slots)
     log(f"store pipeline: {out['store_pipeline']}")
     out["blend_load"] = blend_load(torch, synthetic, dev, args)
     log(f"blend load: {out['blend_load']}")
@@ -387,7 +389,7 @@ def blend_attention_bench(torch, dev):
             "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4)}
 
 
-def store_pipeline(torch, layers, cache, src_slots, args):
+def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     """Qwen3-8B layerwise store: save_kv_layer for all 36 layers of the
     8192-token prompt (32 chunks of 256) through the Store stream, timed from
     the first save to the end of wait_for_save (publication of every chunk
@@ -400,7 +402,9 @@ def store_pipeline(torch, layers, cache, src_slots, args):
                   per-layer batch (the reference's scheme).
     Also timed with the saves interleaved with bf16 GEMMs on the serving
     stream (about 1.5x the per-layer transfer time per layer), as a prefill
-    would interleave them."""
+    would interleave them. Then the reload: the stored chunks scattered back
+    over the host link into fresh random blocks (``reload_slots``), one
+    ``scatter_chunks`` launch per layer, checked bit-exact."""
     from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
     from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
 
@@ -470,6 +474,45 @@ def store_pipeline(torch, layers, cache, src_slots, args):
         result["with_gemm_compute"][mode] = {
             "total_ms": round(total * 1e3, 3),
             "store_hidden_frac": round(1.0 - max(0.0, total - compute_s) / alone, 4)}
+    # reload: the stored chunks (pinned slab slots) scattered back over the
+    # host link into fresh random blocks, one scatter_chunks launch per layer
+    from cacheblend_vllm.kv_layout import scatter_chunks
+    from cacheblend_vllm.types import BlendSegment
+
+    store = PinnedChunkStore(256, 1 << 40, on_release=slab.free)
+    writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2, slab=slab)
+    request = RequestMetadata("reload", list(range(10**6, 10**6 + T)), slots_cpu, None, True, T)
+    for l in range(L):
+        writer.save_layer(l, layers[l], [request])
+    writer.wait_for_save()
+    segments = [BlendSegment(sid, start) for start, sid in writer._save_segments["reload"]]
+    store.pin("reload", segments)
+    chunks = [[store.get_layer("reload", seg, l) for seg in segments] for l in range(L)]
+
+    def reload():
+        for l in range(L):
+            scatter_chunks(chunks[l], layers[l], reload_slots, cache.block_size)
+
+    reload()
+    torch.cuda.synchronize()
+    same = all(torch.equal(cache.gather(reload_slots, layers=(l, l + 1)).view(torch.int16),
+                           cache.gather(src_slots, layers=(l, l + 1)).view(torch.int16)) for l in (0, L - 1))
+    if not same:
+        raise RuntimeError("reload round trip is not bit-exact")
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reload()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    result["reload_h2d"] = {"ms": round(best * 1e3, 3), "h2d_GBps": round(nbytes / best / 1e9, 2),
+                            "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+                            "launches": L, "bit_exact_layers_checked": [0, L - 1]}
+    store.release("reload")
+    writer.close()
+    store.clear()
     result["slab"] = slab.stats()
     slab.close()
     return result

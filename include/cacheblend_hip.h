@@ -123,6 +123,23 @@ int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int
                             int32_t* bad_slots_dev, cbk_stream_t stream);
 
 /*
+ * The inverse: scatter chunk rows into the pages. Token t of the batch is
+ * read from chunk c = t / chunk_tokens, row r = t % chunk_tokens (chunk_k[c]
+ * + r * chunk_token_stride, chunk_v[c] + ...; HOST arrays of device-
+ * addressable sources, e.g. pinned slab slots read over the host link) and
+ * written to slot slots_dev[t]; tokens with an out-of-range slot are skipped
+ * and counted in bad_slots_dev when non-NULL. Grid and alignment as for
+ * cbk_paged_gather_chunks.
+ * Replaces the reload of stored chunks: the H2D copy of the host chunk
+ * (cacheblend_vllm/ascend.py:224-278) followed by scatter_paged_kv
+ * (cacheblend_vllm/kv_layout.py:125-161), with no device staging.
+ */
+int cbk_paged_scatter_chunks(const void* const* chunk_k, const void* const* chunk_v, int64_t chunk_tokens,
+                             int64_t chunk_token_stride, const cbk_kv_desc* kv, const int64_t* slots_dev,
+                             int64_t num_tokens, int32_t max_workgroups, int32_t* bad_slots_dev,
+                             cbk_stream_t stream);
+
+/*
  * Pinned host chunk slab: fixed-size, 256-byte aligned slots carved from
  * pinned, coherent host arenas (hipHostMalloc) of chunks_per_arena slots,
  * recycled through a free list; max_bytes 0 = unbounded. Thread-safe.

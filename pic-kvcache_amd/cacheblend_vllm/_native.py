@@ -94,6 +94,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(KVDesc), c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i32, c_vp, c_vp],
     ),
+    "cbk_paged_scatter_chunks": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_i64, c_i64, ctypes.POINTER(KVDesc), c_vp, c_i64, c_i32, c_vp, c_vp],
+    ),
     "cbk_slab_create": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.POINTER(c_vp)]),
     "cbk_slab_alloc": (ctypes.c_int, [c_vp, ctypes.POINTER(c_vp)]),
     "cbk_slab_alloc_run": (ctypes.c_int, [c_vp, c_i64, ctypes.POINTER(c_vp)]),

@@ -361,6 +361,51 @@ def write_back_kv(old_kv: torch.Tensor, indices: torch.Tensor, k: torch.Tensor, 
     _native.check(rc, "write_back_kv")
 
 
+def scatter_chunks(chunks: Sequence[torch.Tensor], kv_layer: KVLayer, slot_mapping: torch.Tensor,
+                   block_size: int, max_workgroups: int = 256) -> None:
+    """Scatter chunk-format rows into a paged layer in place: token ``t`` of
+    ``slot_mapping`` is row ``t % chunk`` of ``chunks[t // chunk]``, each a
+    ``[2, chunk, *row]`` tensor with contiguous K and V planes -- the store's
+    host chunks (page-locked memory, read over the host link) or device
+    tensors. The reload of stored chunks (the reference's H2D copy then
+    ``scatter_paged_kv``, ascend.py:224-278 and kv_layout.py:125-161) in one
+    launch and without a device staging: cbk_paged_scatter_chunks.
+    ``max_workgroups`` bounds the CUs the copy holds (over the host link the
+    rate grows with them)."""
+    desc, key = kv_desc(kv_layer, block_size)
+    tokens = int(slot_mapping.numel())
+    if tokens == 0:
+        return
+    if not chunks:
+        raise ValueError("no chunks to scatter")
+    first = chunks[0]
+    chunk = int(first.shape[1]) if first.dim() >= 2 else 0
+    shape = (2, chunk, *key.shape[2:])
+    needed = (tokens + chunk - 1) // chunk if chunk else 0
+    if chunk <= 0 or len(chunks) < needed:
+        raise ValueError(f"{tokens} tokens need {needed} chunks of {chunk}, got {len(chunks)}")
+    k_ptrs = (ctypes.c_void_p * needed)()
+    v_ptrs = (ctypes.c_void_p * needed)()
+    for i, c in enumerate(chunks[:needed]):
+        if tuple(c.shape) != shape or c.dtype != key.dtype:
+            raise ValueError(f"chunk {i} is {tuple(c.shape)} {c.dtype}, expected {shape} {key.dtype}")
+        if not (c[0].is_contiguous() and c[1].is_contiguous()):
+            raise ValueError(f"chunk {i}: K and V planes must each be contiguous")
+        if c.device.type == "cpu":
+            if not _native.host_accessible(c):
+                raise ValueError(f"chunk {i} is not page-locked host memory the GPU can read")
+        elif c.device != key.device:
+            raise ValueError(f"chunk {i} is on {c.device}, the cache on {key.device}")
+        k_ptrs[i] = c[0].data_ptr()
+        v_ptrs[i] = c[1].data_ptr()
+    slots = _device_slots(slot_mapping, key.device, desc.num_blocks * block_size)
+    rc = _native.load().cbk_paged_scatter_chunks(
+        k_ptrs, v_ptrs, chunk, desc.row_bytes, desc, slots.data_ptr(), tokens, int(max_workgroups), None,
+        _native.stream_handle(key.device),
+    )
+    _native.check(rc, "scatter_chunks")
+
+
 class PagedKVCache:
     """A model's registered paged KV layers (one descriptor per layer, built
     once, as the connector's ``register_kv_caches`` receives them, reference

@@ -109,12 +109,12 @@ __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a)
   }
 }
 
-// Gather straight into host chunks: token t of a batch goes to chunk
-// t / chunk_tokens at row t % chunk_tokens, each chunk plane being a
-// [chunk_tokens, row] block at chunk_k[c] / chunk_v[c] (pinned host memory
-// addressed over PCIe). A bounded grid walks the batch with a stride: 16-64
-// workgroups already saturate the host link, leaving the CUs to the
-// serving stream.
+// Copies between pages and chunks: token t of a batch is row t % chunk_tokens
+// of chunk t / chunk_tokens, each chunk plane being a [chunk_tokens, row]
+// block at chunk_k[c] / chunk_v[c] (pinned host memory addressed over PCIe,
+// or device memory). A bounded grid walks the batch with a stride; over the
+// host link the rate grows with the CUs issuing (about 1.2-1.6 GB/s each),
+// so the caller trades link rate against CUs left to the serving stream.
 constexpr int kChunksPerLaunch = 64;
 constexpr int kChunkThreads = 256;
 constexpr int kChunkUnroll = 4;
@@ -137,8 +137,13 @@ struct ChunkArgs {
   FastDiv chunk_div;
 };
 
-template <int VEC>
-__global__ __launch_bounds__(kChunkThreads) void gather_chunks_kernel(const ChunkArgs a) {
+// One pass of the chunk copy. GATHER: page rows -> chunk rows (the store:
+// chunks in pinned host memory are written over the host link; a token with
+// an out-of-range slot gets a zero row). Scatter: chunk rows -> page rows
+// (the reload: chunks are read over the host link; out-of-range slots are
+// skipped). kChunkUnroll vectors per thread, all loads before the stores.
+template <int VEC, bool GATHER>
+__device__ __forceinline__ void chunks_body(const ChunkArgs& a) {
   using V = typename Vec<VEC>::T;
   const uint32_t total = a.num_tokens * 2u * a.row_vecs;
   const uint32_t stride = gridDim.x * uint32_t(kChunkThreads * kChunkUnroll);
@@ -158,24 +163,45 @@ __global__ __launch_bounds__(kChunkThreads) void gather_chunks_kernel(const Chun
         const uint32_t t = row - c * a.num_tokens;
         const uint32_t ck = a.chunk_div.div(t);
         const uint32_t r = t - ck * a.chunk_div.d;
-        dst[u] = (c ? a.chunk_v[ck] : a.chunk_k[ck]) + int64_t(r) * a.chunk_token_stride + int64_t(j) * VEC;
+        char* chunk = (c ? a.chunk_v[ck] : a.chunk_k[ck]) + int64_t(r) * a.chunk_token_stride + int64_t(j) * VEC;
         const int64_t slot = a.slots[t];
-        if (slot >= 0 && slot < int64_t(a.num_slots)) {
+        const bool ok = slot >= 0 && slot < int64_t(a.num_slots);
+        char* page = nullptr;
+        if (ok) {
           const uint32_t s32 = uint32_t(slot);
           const uint32_t blk = a.bs_div.div(s32);
           const uint32_t off = s32 - blk * a.bs_div.d;
-          buf[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(
-              (c ? a.v_base : a.k_base) + int64_t(blk) * a.block_stride + int64_t(off) * a.token_stride +
-              int64_t(j) * VEC));
+          page = const_cast<char*>(c ? a.v_base : a.k_base) + int64_t(blk) * a.block_stride +
+                 int64_t(off) * a.token_stride + int64_t(j) * VEC;
         } else if (a.bad != nullptr && c == 0 && j == 0) {
           atomicAdd(a.bad, 1);
+        }
+        if (GATHER) {
+          dst[u] = chunk;
+          if (ok) buf[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(page));
+        } else if (ok) {
+          dst[u] = page;
+          buf[u] = *reinterpret_cast<const V*>(chunk);
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < kChunkUnroll; ++u)
-      if (dst[u] != nullptr) *reinterpret_cast<V*>(dst[u]) = buf[u];
+    for (int u = 0; u < kChunkUnroll; ++u) {
+      if (dst[u] == nullptr) continue;
+      if (GATHER) *reinterpret_cast<V*>(dst[u]) = buf[u];
+      else __builtin_nontemporal_store(buf[u], reinterpret_cast<V*>(dst[u]));
+    }
   }
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kChunkThreads) void gather_chunks_kernel(const ChunkArgs a) {
+  chunks_body<VEC, true>(a);
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kChunkThreads) void scatter_chunks_kernel(const ChunkArgs a) {
+  chunks_body<VEC, false>(a);
 }
 
 int validate_desc(const cbk_kv_desc* kv, int planes = 2) {
@@ -273,10 +299,10 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
   return CBK_OK;
 }
 
-int launch_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots, int64_t num_tokens,
-                         int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
-                         int64_t chunk_token_stride, int32_t max_workgroups, int32_t* bad,
-                         hipStream_t stream) {
+int launch_chunks(bool gather, const cbk_kv_desc* kv, const int64_t* slots, int64_t num_tokens,
+                  int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
+                  int64_t chunk_token_stride, int32_t max_workgroups, int32_t* bad,
+                  hipStream_t stream) {
   clear_error();
   if (int rc = validate_desc(kv)) return rc;
   CBK_REQUIRE(num_tokens >= 0 && chunk_tokens > 0, "num_tokens/chunk_tokens invalid");
@@ -323,14 +349,20 @@ int launch_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots, int64_t nu
     const uint64_t total = uint64_t(n) * 2 * uint64_t(row_vecs);
     const uint32_t grid = uint32_t(std::min<uint64_t>(
         grid_cap, (total + kChunkThreads * kChunkUnroll - 1) / (kChunkThreads * kChunkUnroll)));
+#define CBK_LAUNCH_CHUNKS(V)                                                                          \
+  if (gather)                                                                                         \
+    hipLaunchKernelGGL(gather_chunks_kernel<V>, dim3(grid), dim3(kChunkThreads), 0, stream, a);       \
+  else                                                                                                \
+    hipLaunchKernelGGL(scatter_chunks_kernel<V>, dim3(grid), dim3(kChunkThreads), 0, stream, a);
     switch (vec) {
-      case 16: hipLaunchKernelGGL(gather_chunks_kernel<16>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
-      case 8: hipLaunchKernelGGL(gather_chunks_kernel<8>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
-      case 4: hipLaunchKernelGGL(gather_chunks_kernel<4>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
-      case 2: hipLaunchKernelGGL(gather_chunks_kernel<2>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
-      default: hipLaunchKernelGGL(gather_chunks_kernel<1>, dim3(grid), dim3(kChunkThreads), 0, stream, a); break;
+      case 16: CBK_LAUNCH_CHUNKS(16); break;
+      case 8: CBK_LAUNCH_CHUNKS(8); break;
+      case 4: CBK_LAUNCH_CHUNKS(4); break;
+      case 2: CBK_LAUNCH_CHUNKS(2); break;
+      default: CBK_LAUNCH_CHUNKS(1); break;
     }
-    if (int rc = launch_status("paged gather to chunks")) return rc;
+#undef CBK_LAUNCH_CHUNKS
+    if (int rc = launch_status(gather ? "paged gather to chunks" : "paged scatter from chunks")) return rc;
   }
   return CBK_OK;
 }
@@ -353,9 +385,18 @@ int cbk_paged_gather_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev, int
                             int64_t chunk_tokens, void* const* chunk_k, void* const* chunk_v,
                             int64_t chunk_token_stride, int32_t max_workgroups,
                             int32_t* bad_slots_dev, cbk_stream_t stream) {
-  return cbk::launch_gather_chunks(kv, slots_dev, num_tokens, chunk_tokens, chunk_k, chunk_v,
-                                   chunk_token_stride, max_workgroups, bad_slots_dev,
-                                   static_cast<hipStream_t>(stream));
+  return cbk::launch_chunks(true, kv, slots_dev, num_tokens, chunk_tokens, chunk_k, chunk_v,
+                            chunk_token_stride, max_workgroups, bad_slots_dev,
+                            static_cast<hipStream_t>(stream));
+}
+
+int cbk_paged_scatter_chunks(const void* const* chunk_k, const void* const* chunk_v, int64_t chunk_tokens,
+                             int64_t chunk_token_stride, const cbk_kv_desc* kv, const int64_t* slots_dev,
+                             int64_t num_tokens, int32_t max_workgroups, int32_t* bad_slots_dev,
+                             cbk_stream_t stream) {
+  return cbk::launch_chunks(false, kv, slots_dev, num_tokens, chunk_tokens, const_cast<void* const*>(chunk_k),
+                            const_cast<void* const*>(chunk_v), chunk_token_stride, max_workgroups,
+                            bad_slots_dev, static_cast<hipStream_t>(stream));
 }
 
 int cbk_paged_gather(const cbk_kv_desc* kv, const int64_t* slots_dev, int64_t num_tokens,

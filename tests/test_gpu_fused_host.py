@@ -158,3 +158,85 @@ def test_fused_store_then_host_read_load_round_trip():
     store.clear()
     writer.close()
     slab.close()
+
+
+@pytest.mark.parametrize("where", ["slab", "device"])
+@pytest.mark.parametrize("layout", ["merged_first", "merged_block", "separate"])
+def test_scatter_chunks_round_trip_bit_exact(layout, where):
+    """Chunks gathered from one set of blocks scatter back into fresh random
+    blocks: the pages equal the oracle's scatter of the concatenated chunks
+    (ragged last chunk, other pages intact); an out-of-range slot raises
+    before anything moves."""
+    from cacheblend_vllm.kv_layout import scatter_chunks
+
+    NB, BS, H, D, CH, T = 96, 16, 4, 64, 64, 200  # 4 chunks, the last one ragged
+    base = synthetic.paged_pool(NB, BS, H, D, torch.float16, DEV, seed=70)
+    if layout == "merged_first":
+        kv = base
+    elif layout == "merged_block":
+        kv = base.transpose(0, 1).contiguous()
+    else:
+        kv = [base[0].clone(), base[1].clone()]
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(3))
+    src_slots = synthetic.block_slots(perm[:13], BS, T)
+    chunks = []
+    for c in range(4):
+        rows = O.gather_paged_kv(_bits(base), src_slots[c * CH:(c + 1) * CH].numpy(), BS)
+        full = np.zeros((2, CH, H, D), dtype=np.uint16)
+        full[:, :rows.shape[1]] = rows
+        t = torch.from_numpy(full.view(np.int16)).view(torch.float16)
+        if where == "slab":
+            slot = torch.empty((2, CH, H, D), dtype=torch.float16, pin_memory=True)
+            slot.copy_(t)
+            assert _native.host_accessible(slot)
+            chunks.append(slot)
+        else:
+            chunks.append(t.to(DEV))
+    dst_slots = synthetic.block_slots(perm[13:26], BS, T)
+    expect = _bits(base).copy()
+    flat = np.concatenate([_bits(c) for c in chunks], axis=1)[:, :T]
+    O.scatter_paged_kv(flat, expect, dst_slots.numpy(), BS)
+    bad = dst_slots.clone()
+    bad[7] = NB * BS + 5
+    with pytest.raises(IndexError):  # as the reference's index_put_ would
+        scatter_chunks(chunks, kv, bad, BS)
+    scatter_chunks(chunks, kv, dst_slots, BS, max_workgroups=32)
+    torch.cuda.synchronize()
+    if layout == "merged_first":
+        got = _bits(kv)
+    elif layout == "merged_block":
+        got = _bits(kv.transpose(0, 1))
+    else:
+        got = np.stack([_bits(kv[0]), _bits(kv[1])])
+    np.testing.assert_array_equal(got, expect)
+    # device slots are not range-checked on the host: the kernel skips the
+    # out-of-range token and moves the rest
+    keep = np.ones(T, dtype=bool)
+    keep[7] = False
+    fresh = synthetic.block_slots(perm[26:39], BS, T).clone()
+    O.scatter_paged_kv(flat[:, keep], expect, fresh.numpy()[keep], BS)
+    fresh[7] = NB * BS + 5
+    scatter_chunks(chunks, kv, fresh.to(DEV), BS)
+    torch.cuda.synchronize()
+    if layout == "merged_first":
+        got = _bits(kv)
+    elif layout == "merged_block":
+        got = _bits(kv.transpose(0, 1))
+    else:
+        got = np.stack([_bits(kv[0]), _bits(kv[1])])
+    np.testing.assert_array_equal(got, expect)
+
+
+def test_scatter_chunks_rejects_pageable_and_short_inputs():
+    from cacheblend_vllm.kv_layout import scatter_chunks
+
+    kv = synthetic.paged_pool(8, 16, 2, 64, torch.bfloat16, DEV, seed=1)
+    slots = torch.arange(40)
+    pageable = [torch.zeros(2, 32, 2, 64, dtype=torch.bfloat16) for _ in range(2)]
+    with pytest.raises(ValueError, match="page-locked"):
+        scatter_chunks(pageable, kv, slots, 16)
+    with pytest.raises(ValueError, match="need 2 chunks"):
+        scatter_chunks(pageable[:1], kv, slots, 16)
+    with pytest.raises(ValueError, match="expected"):
+        scatter_chunks([torch.zeros(2, 32, 2, 32, dtype=torch.bfloat16, device=DEV)] * 2, kv, slots, 16)
+    scatter_chunks([], kv, slots[:0], 16)  # nothing to move
