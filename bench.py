@@ -397,7 +397,8 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     host_write -- (default) pinned slab slots allocated as consecutive runs,
                   written by the gather kernel directly over the host link;
     dma        -- the same slots; gather into a chunk-major device staging,
-                  then one hipMemcpyAsync per run of slots;
+                  then (copier thread, Copy stream) one hipMemcpyAsync per
+                  run of slots;
     reference  -- gather into device staging + one D2H into a freshly pinned
                   per-layer batch (the reference's scheme).
     Also timed with the saves interleaved with bf16 GEMMs on the serving

@@ -32,6 +32,7 @@ stream keeps computing.
 from __future__ import annotations
 
 import ctypes
+import queue
 import threading
 import time
 from concurrent.futures import Future, ThreadPoolExecutor
@@ -42,7 +43,7 @@ import torch
 
 from . import _native
 from .kv_layout import gather_paged_kv, kv_desc, kv_planes
-from .streams import STORE, side_stream
+from .streams import STORE, STORE_COPY, side_stream
 from .trace import PipelineTracer
 from .types import BlendPlan, SegmentId
 
@@ -91,6 +92,19 @@ class CudaStreams:
     def Stream():  # noqa: N802
         return side_stream(STORE)
 
+    @staticmethod
+    def CopyStream():  # noqa: N802
+        return side_stream(STORE_COPY)
+
+
+def _chain(inner: Future, outer: Future) -> None:
+    """Complete ``outer`` with ``inner``'s outcome."""
+    error = inner.exception()
+    if error is not None:
+        outer.set_exception(error)
+    else:
+        outer.set_result(inner.result())
+
 
 class StoreStreamWriter:
     """The save half of CacheBlendConnectorV1 (worker role)."""
@@ -109,19 +123,24 @@ class StoreStreamWriter:
         store_stream=None,
         slab=None,
         max_workgroups: int = 256,
-        slab_transfer: str = "host_write",
+        slab_transfer: str = "dma",
     ):
         """``slab`` (a PinnedChunkSlab): every chunk gets its own pinned slot,
         allocated as consecutive runs, so no pinned memory is allocated per
         layer. ``slab_transfer`` picks how the bytes get there:
-        "host_write" -- (default) the gather kernel writes the slots
-                        directly over the host link: no staging, one launch
-                        per layer, holding up to ``max_workgroups``
-                        workgroups for the transfer (zero-copy write rate
-                        grows with the CUs issuing: 256 reach about 55 GB/s);
-        "dma"        -- gather into a chunk-major device staging, then one
-                        hipMemcpyAsync per run of consecutive slots (HIP
-                        runs it as its own copy kernel).
+        "dma"        -- (default) gather into a chunk-major device staging
+                        on the Store stream; a copier thread waits for each
+                        layer's gather on the host and issues one
+                        hipMemcpyAsync per run of consecutive slots on the
+                        store's copy stream, so the DMA engine gets the
+                        layers' copies back to back with no stream waits
+                        between them, and the transfer holds no CUs (it
+                        hides behind compute that fills every CU);
+        "host_write" -- the gather kernel writes the slots directly over
+                        the host link: no staging, one launch per layer,
+                        holding up to ``max_workgroups`` workgroups for the
+                        transfer (zero-copy write rate grows with the CUs
+                        issuing: 256 reach about 55 GB/s);
         None: gather into device staging + one pinned D2H per layer into a
         freshly pinned batch, as the reference does."""
         if slab_transfer not in ("dma", "host_write"):
@@ -149,6 +168,10 @@ class StoreStreamWriter:
         # per request: (host slot list, device copy); the fused slot list is
         # normally identical for every layer, so it is uploaded once
         self._device_slots: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
+        # slab_transfer="dma": the copier thread and its stream (made on first use)
+        self._copy_jobs: queue.Queue | None = None
+        self._copier: threading.Thread | None = None
+        self._copy_stream = None
 
     # ------------------------------------------------------------- save
 
@@ -236,7 +259,7 @@ class StoreStreamWriter:
                     if self._slab_transfer == "host_write":
                         self._gather_to_chunks(kv_layer, slots, [h.data_ptr() for h in host])
                     else:
-                        self._gather_then_dma(request_id, kv_layer, slots, host)
+                        staging, runs = self._gather_for_dma(kv_layer, slots, host)
                 else:
                     staging = self._store_staging_by_request.get(request_id)
                     if staging is None or staging.shape[1] != slots.numel():
@@ -252,9 +275,15 @@ class StoreStreamWriter:
                     host.copy_(staging, non_blocking=True)
                 event = self._streams.Event()
                 event.record(self._store_stream)
-            future = self._save_pool.submit(
-                self._publish_after_event, event, pending, host, request_id, store_enqueued_ns
-            )
+            if self._slab is not None and self._slab_transfer == "dma":
+                future = Future()
+                self._copier_queue().put((event, staging, runs, pending, host, request_id,
+                                          store_enqueued_ns, future))
+                del staging
+            else:
+                future = self._save_pool.submit(
+                    self._publish_after_event, event, pending, host, request_id, store_enqueued_ns
+                )
         except Exception:
             self._save_slots.release()
             if self._slab is not None and isinstance(locals().get("host"), list):
@@ -299,20 +328,16 @@ class StoreStreamWriter:
         )
         _native.check(rc, "gather to chunks")
 
-    def _gather_then_dma(self, request_id: str, kv_layer: Any, slots: torch.Tensor,
-                         host: list[torch.Tensor]) -> None:
-        """Gather into a chunk-major device staging laid out like the slots
-        (``chunk_bytes`` apart), then one D2H copy per run of consecutive
-        slots, all on the current (Store) stream."""
+    def _gather_for_dma(self, kv_layer: Any, slots: torch.Tensor,
+                        host: list[torch.Tensor]) -> tuple[torch.Tensor, tuple]:
+        """Gather the layer's chunks into a fresh chunk-major device staging
+        laid out like the slots (``chunk_bytes`` apart) on the current
+        (Store) stream; returns it with the D2H runs (host dst, device src,
+        bytes) that the copier issues once the gather is done."""
         stride = self._slab.chunk_bytes
         n = len(host)
-        staging = self._store_staging_by_request.get(request_id)
-        if staging is None or staging.numel() != n * stride:
-            if staging is not None:
-                self._retired_store_staging.append(staging)  # an earlier copy may still read it
-            key, _ = kv_planes(kv_layer)
-            staging = torch.empty(n * stride, dtype=torch.uint8, device=key.device)
-            self._store_staging_by_request[request_id] = staging
+        key, _ = kv_planes(kv_layer)
+        staging = torch.empty(n * stride, dtype=torch.uint8, device=key.device)
         base = staging.data_ptr()
         self._gather_to_chunks(kv_layer, slots, [base + i * stride for i in range(n)])
         runs: list[list[int]] = []
@@ -323,11 +348,48 @@ class StoreStreamWriter:
             else:
                 runs.append([p, base + i * stride, stride])
         m = len(runs)
-        dst = (ctypes.c_uint64 * m)(*[r[0] for r in runs])
-        src = (ctypes.c_uint64 * m)(*[r[1] for r in runs])
-        nbytes = (ctypes.c_uint64 * m)(*[r[2] for r in runs])
-        _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, m, _native.stream_handle(staging.device)),
-                      "chunk runs D2H")
+        return staging, ((ctypes.c_uint64 * m)(*[r[0] for r in runs]),
+                         (ctypes.c_uint64 * m)(*[r[1] for r in runs]),
+                         (ctypes.c_uint64 * m)(*[r[2] for r in runs]), m)
+
+    def _copier_queue(self) -> queue.Queue:
+        if self._copier is None:
+            self._copy_stream = self._streams.CopyStream()
+            self._copy_jobs = queue.Queue()
+            self._copier = threading.Thread(target=self._copier_loop, name="cacheblend-copier", daemon=True)
+            self._copier.start()
+        return self._copy_jobs
+
+    def _copier_loop(self) -> None:
+        """Copier thread: per layer, in order, wait (host side) for the
+        gather, issue the runs' D2H copies on the Copy stream, hand the
+        publication to the save pool. A wait between two copies on one
+        stream left the DMA engine idle ~50-100 us whenever the submitting
+        thread was busy between them; here the copies follow each other."""
+        while True:
+            job = self._copy_jobs.get()
+            if job is None:
+                return
+            gathered, staging, (dst, src, nbytes, m), pending, host, request_id, enqueued_ns, future = job
+            try:
+                gathered.synchronize()
+                _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, m, self._copy_stream.cuda_stream),
+                              "chunk runs D2H")
+                staging.record_stream(self._copy_stream)
+                copied = self._streams.Event()
+                copied.record(self._copy_stream)
+            except BaseException as error:  # the batch fails as a unit
+                for segment_id, _, _ in pending:
+                    self._store.abort_put(segment_id)
+                for chunk in host:
+                    self._slab.free(chunk)
+                future.set_exception(error)
+                continue
+            finally:
+                del staging
+            inner = self._save_pool.submit(self._publish_after_event, copied, pending, host, request_id,
+                                           enqueued_ns)
+            inner.add_done_callback(lambda f, out=future: _chain(f, out))
 
     def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host, accepted=None) -> bool:
         """Per-chunk host tensors into the store (connector.py:449-466): views
@@ -439,6 +501,10 @@ class StoreStreamWriter:
                 with self._save_lock:
                     self._save_futures.difference_update(futures)
         finally:
+            if self._copier is not None:
+                self._copy_jobs.put(None)
+                self._copier.join()
+                self._copier = None
             self._store_staging_by_request.clear()
             self._retired_store_staging.clear()
             self._save_pool.shutdown(wait=True, cancel_futures=False)

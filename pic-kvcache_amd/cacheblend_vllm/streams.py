@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import logging
+import os
 import threading
 
 import torch
@@ -23,16 +24,22 @@ from . import _native
 
 logger = logging.getLogger(__name__)
 
-# roles, in the order the streams are picked
-LOAD, COPY, STORE = 0, 1, 2
-_ROLES = 3
+# roles, in the order the streams are picked: the loader's assembly (LOAD)
+# and its H2D copies (COPY), the store's gathers (STORE) and its D2H copies
+# (STORE_COPY)
+LOAD, COPY, STORE, STORE_COPY = 0, 1, 2, 3
+_ROLES = 4
+# a role left without a hardware queue of its own shares this role's stream
+# (a fresh stream could land on the serving stream's queue); with the
+# default 4 queues the store's copies share the loader's copy stream
+_SHARE = {STORE_COPY: COPY}
 
 _picked: dict[tuple[int, int], list] = {}
 _lock = threading.Lock()
 
 
 def side_stream(role: int, device: torch.device | int | None = None):
-    """The side stream for ``role`` (LOAD, COPY or STORE) on ``device``,
+    """The side stream for ``role`` (LOAD, COPY, STORE or STORE_COPY) on ``device``,
     concurrent with the device's current stream; picked once per (device,
     serving stream) and kept for the life of the process."""
     device = torch.device("cuda", torch.cuda.current_device() if device is None else
@@ -48,14 +55,23 @@ def side_stream(role: int, device: torch.device | int | None = None):
 
 
 def _pick(device: torch.device, serving) -> list:
-    out = (ctypes.c_void_p * _ROLES)()
+    # one queue per process goes to the serving stream; asking for more
+    # streams than the other queues can hold only lengthens the search
+    queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+    want = max(1, min(_ROLES, queues - 1))
+    out = (ctypes.c_void_p * want)()
     found = ctypes.c_int32()
     with torch.cuda.device(device):
-        _native.check(_native.load().cbk_side_streams(serving.cuda_stream, _ROLES, 24, 0.5, out,
+        _native.check(_native.load().cbk_side_streams(serving.cuda_stream, want, 24, 0.5, out,
                                                       ctypes.byref(found)), "side streams")
     streams = [torch.cuda.ExternalStream(out[i], device=device) for i in range(found.value)]
-    if len(streams) < _ROLES:
-        logger.warning("only %d of %d side streams run concurrently with the serving stream; "
-                       "the rest share hardware queues (raise GPU_MAX_HW_QUEUES)", len(streams), _ROLES)
-        streams += [torch.cuda.Stream(device) for _ in range(_ROLES - len(streams))]
+    missing = [r for r in range(len(streams), _ROLES) if _SHARE.get(r, _ROLES) >= len(streams)]
+    if missing:
+        logger.warning("only %d side streams run concurrently with the serving stream; roles %s "
+                       "share hardware queues (raise GPU_MAX_HW_QUEUES)", len(streams), missing)
+    while len(streams) < _ROLES:
+        role = len(streams)
+        shared = _SHARE.get(role)
+        streams.append(streams[shared] if shared is not None and shared < len(streams)
+                       else torch.cuda.Stream(device))
     return streams

@@ -6,7 +6,7 @@ import time
 import pytest
 import torch
 
-from cacheblend_vllm.streams import COPY, LOAD, STORE, side_stream
+from cacheblend_vllm.streams import COPY, LOAD, STORE, STORE_COPY, side_stream
 
 pytestmark = pytest.mark.gpu
 
@@ -37,6 +37,10 @@ def test_side_streams_overlap_serving_and_each_other():
     streams = [side_stream(r) for r in (LOAD, COPY, STORE)]
     assert len({s.cuda_stream for s in streams}) == 3
     assert side_stream(LOAD) is streams[0]  # picked once, then reused
+    # with the box's 4 hardware queues the store's copies share the
+    # loader's copy stream rather than a queue of the serving stream
+    store_copy = side_stream(STORE_COPY)
+    assert store_copy is streams[1] or store_copy.cuda_stream not in {s.cuda_stream for s in streams}
     cycles = int(10 * _cycles_per_ms())  # 10 ms spins
     serving = torch.cuda.current_stream()
     pairs = [(serving, s) for s in streams] + [(streams[0], streams[1]), (streams[0], streams[2]),
