@@ -692,6 +692,36 @@ def blend_load(torch, synthetic, dev, args):
     fragmented.release("blend")
     fragmented.clear()
     slab.close()
+
+    # the commit's device scatter alone (loader.commit: [2, apc:A] of the
+    # layer buffer into the pages), one launch per layer as the loader issues
+    # it, timed with HIP events over back-to-back C-ABI calls
+    from cacheblend_vllm import _native
+    from cacheblend_vllm.kv_layout import kv_desc
+
+    buf = torch.randn((2, A, H, D), device=dev).to(torch.bfloat16)
+    src = buf[:, APC:]
+    commit_slots = slots[APC:].to(dev)
+    n = commit_slots.numel()
+    lib = _native.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    descs = [kv_desc(layers[l], BS)[0] for l in range(L)]
+    es = buf.element_size()
+
+    calls = [(src[0].data_ptr(), src[1].data_ptr(), src.stride(1) * es, descs[l], commit_slots.data_ptr(), n,
+              None, stream) for l in range(L)]
+    scatter = lib.cbk_paged_scatter
+
+    def commit_all():
+        for c in calls:
+            if scatter(*c):
+                _native.check(scatter(*c), "commit scatter")
+
+    ms = event_time_ms(torch, commit_all, 5)
+    commit_bytes = 2 * 2 * n * H * D * es  # read + written, K and V
+    out["commit_scatter"] = {"tokens_per_layer": n, "us_per_layer": round(ms * 1e3 / L, 2),
+                             "GBps": round(L * commit_bytes / (ms / 1e3) / 1e9, 1),
+                             "frac_of_hbm_peak": round(L * commit_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
     return out
 
 
