@@ -13,9 +13,11 @@
 //   pass2   histogram of key[19:8] inside that bin; last block narrows
 //   pass3   histogram of key[7:0]; last block fixes the k-th key T exactly
 //           and `need` = how many keys equal to T are taken (lowest index)
-//   ties    per-tile count of key == T; last block: exclusive scan
-//   count   per-tile count of selected; last block: exclusive scan, total
+//   tiecount per-tile counts of key == T and of sure picks; last block:
+//           tie offsets, output offsets, total
 //   write   per-tile ordered compaction of selected indices
+// (the fused K-deviation launch clears the counters in its first block, so
+// the zero launch is skipped there)
 // Every tile is 1024 consecutive tokens (4 per thread), so tile order is
 // index order and ties resolve to the lower index deterministically.
 #include "cbk_common.hpp"
@@ -40,8 +42,12 @@ template <typename T, int VE>
 __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
     const T* __restrict__ fresh, int64_t fs, const T* __restrict__ cached, int64_t cs,
     int64_t cached_rows_total, const int64_t* __restrict__ rows, int64_t row0, uint32_t n,
-    uint32_t width, float* __restrict__ scores) {
+    uint32_t width, float* __restrict__ scores, uint32_t* __restrict__ zero_words, uint32_t nzero) {
   typedef T VecT __attribute__((ext_vector_type(VE)));
+  // the fused score + select launch: block 0 also clears the selection's
+  // counters (the selection kernels run after this launch on the stream)
+  if (zero_words != nullptr && blockIdx.x == 0)
+    for (uint32_t i = threadIdx.x; i < nzero; i += kKdevThreads) zero_words[i] = 0u;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = blockIdx.x * (kKdevThreads / 64) + (threadIdx.x >> 6);
   const uint32_t r0 = wave * kRowsPerWave;
@@ -97,7 +103,7 @@ __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
 template <typename T>
 int launch_kdev_t(const void* fresh, int64_t fs, const void* cached, int64_t cs, int64_t total_rows,
                   const int64_t* rows, int64_t row0, int64_t n, int64_t width, float* scores,
-                  hipStream_t stream) {
+                  uint32_t* zero_words, uint32_t nzero, hipStream_t stream) {
   const int64_t eb = sizeof(T);
   int64_t vals[5] = {fs * eb, cs * eb, width * eb, int64_t(reinterpret_cast<uintptr_t>(fresh)),
                      int64_t(reinterpret_cast<uintptr_t>(cached))};
@@ -108,7 +114,7 @@ int launch_kdev_t(const void* fresh, int64_t fs, const void* cached, int64_t cs,
   const T* c = static_cast<const T*>(cached);
 #define CBK_KDEV(VE)                                                                        \
   hipLaunchKernelGGL((kdev_kernel<T, VE>), grid, dim3(kKdevThreads), 0, stream, f, fs, c, cs, \
-                     total_rows, rows, row0, uint32_t(n), uint32_t(width), scores)
+                     total_rows, rows, row0, uint32_t(n), uint32_t(width), scores, zero_words, nzero)
   switch (vec_bytes / int(eb)) {
     case 8: CBK_KDEV(8); break;
     case 4: CBK_KDEV(4); break;
@@ -121,7 +127,7 @@ int launch_kdev_t(const void* fresh, int64_t fs, const void* cached, int64_t cs,
 
 int launch_kdev(const void* fresh, int64_t fs, const void* cached, int64_t cs, int64_t total_rows,
                 const int64_t* rows, int64_t row0, int64_t n, int64_t width, int32_t dtype,
-                float* scores, hipStream_t stream) {
+                float* scores, hipStream_t stream, uint32_t* zero_words = nullptr, uint32_t nzero = 0) {
   CBK_REQUIRE(n >= 0 && width >= 0, "n and width must be non-negative");
   CBK_REQUIRE(n < (int64_t(1) << 31) && width < (int64_t(1) << 31), "n or width too large");
   if (n == 0) return CBK_OK;
@@ -130,11 +136,14 @@ int launch_kdev(const void* fresh, int64_t fs, const void* cached, int64_t cs, i
   CBK_REQUIRE(total_rows > 0, "cached tensor has no rows");
   switch (dtype) {
     case CBK_DTYPE_F32:
-      return launch_kdev_t<float>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores, stream);
+      return launch_kdev_t<float>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores,
+                                  zero_words, nzero, stream);
     case CBK_DTYPE_BF16:
-      return launch_kdev_t<uint16_t>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores, stream);
+      return launch_kdev_t<uint16_t>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores,
+                                     zero_words, nzero, stream);
     case CBK_DTYPE_F16:
-      return launch_kdev_t<_Float16>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores, stream);
+      return launch_kdev_t<_Float16>(fresh, fs, cached, cs, total_rows, rows, row0, n, width, scores,
+                                     zero_words, nzero, stream);
     default:
       return set_error(CBK_ERR_UNSUPPORTED, "dtype %d", int(dtype));
   }
@@ -399,39 +408,11 @@ __device__ __forceinline__ SelState load_state(const SelArgs& a) {
   return s;
 }
 
-__global__ __launch_bounds__(kSelThreads) void sel_ties_kernel(const SelArgs a) {
-  __shared__ uint32_t scan[8];
-  __shared__ uint32_t flag;
-  const SelState st = load_state(a);
-  uint32_t ties = 0;
-  if (st.topk) {
-    const uint32_t i0 = blockIdx.x * kSelTile + threadIdx.x * kSelItems;
-#pragma unroll
-    for (int e = 0; e < kSelItems; ++e) {
-      const uint32_t i = i0 + e;
-      if (i < a.n && a.keys[i] == st.thresh) ++ties;
-    }
-  }
-  uint32_t total;
-  block_exclusive_scan<kSelThreads>(ties, scan, &total);
-  if (threadIdx.x == 0) a.blk_ties[blockIdx.x] = total;
-  if (!last_block(&a.ws[kCtrl + C_T_TIES], a.nblocks, &flag)) return;
-  // exclusive scan of per-tile tie counts, in tile (= index) order
-  uint32_t carry = 0;
-  for (uint32_t b0 = 0; b0 < a.nblocks; b0 += kSelThreads) {
-    const uint32_t b = b0 + threadIdx.x;
-    const uint32_t v = b < a.nblocks ? ld_acq(&a.blk_ties[b]) : 0u;
-    uint32_t chunk;
-    const uint32_t ex = block_exclusive_scan<kSelThreads>(v, scan, &chunk);
-    if (b < a.nblocks) a.blk_ties[b] = carry + ex;
-    carry += chunk;
-  }
-}
-
-// Selected flags of this thread's kSelItems tokens, as a bit mask.
-__device__ __forceinline__ uint32_t selected_bits(const SelArgs& a, const SelState& st,
-                                                  uint32_t* scan) {
-  const uint32_t i0 = blockIdx.x * kSelTile + threadIdx.x * kSelItems;
+// Tile b's selected flags for this thread, with the tile's first tie rank
+// given; *ties_out receives the tile's tie count.
+__device__ __forceinline__ uint32_t tile_selected_bits(const SelArgs& a, const SelState& st, uint32_t b,
+                                                       uint32_t rank0, uint32_t* scan, uint32_t* ties_out) {
+  const uint32_t i0 = b * kSelTile + threadIdx.x * kSelItems;
   uint32_t keys[kSelItems];
   uint32_t tie_bits = 0, ties = 0;
 #pragma unroll
@@ -443,8 +424,7 @@ __device__ __forceinline__ uint32_t selected_bits(const SelArgs& a, const SelSta
       ++ties;
     }
   }
-  uint32_t tile_ties;
-  uint32_t rank = a.blk_ties[blockIdx.x] + block_exclusive_scan<kSelThreads>(ties, scan, &tile_ties);
+  uint32_t rank = rank0 + block_exclusive_scan<kSelThreads>(ties, scan, ties_out);
   uint32_t bits = 0;
 #pragma unroll
   for (int e = 0; e < kSelItems; ++e) {
@@ -463,34 +443,77 @@ __device__ __forceinline__ uint32_t selected_bits(const SelArgs& a, const SelSta
   return bits;
 }
 
-__global__ __launch_bounds__(kSelThreads) void sel_count_kernel(const SelArgs a) {
+// Per tile: the ties (key == T) and the tokens taken for sure (base, or key
+// above T); the last block turns them into exclusive tie offsets and output
+// offsets and the total. A tile takes its ties whose index-order rank is
+// below `need`: clamp(need - tie_offset, 0, ties). Base tokens carry the key
+// of -inf, so they tie only when T is that key; then the last block counts
+// tile by tile, token by token.
+__global__ __launch_bounds__(kSelThreads) void sel_tiecount_kernel(const SelArgs a) {
   __shared__ uint32_t scan[8];
   __shared__ uint32_t flag;
   const SelState st = load_state(a);
-  const uint32_t bits = selected_bits(a, st, scan);
-  uint32_t total;
-  block_exclusive_scan<kSelThreads>(__popc(bits), scan, &total);
-  if (threadIdx.x == 0) a.blk_sel[blockIdx.x] = total;
-  if (!last_block(&a.ws[kCtrl + C_T_COUNT], a.nblocks, &flag)) return;
-  uint32_t carry = 0;
-  for (uint32_t b0 = 0; b0 < a.nblocks; b0 += kSelThreads) {
-    const uint32_t b = b0 + threadIdx.x;
-    const uint32_t v = b < a.nblocks ? ld_acq(&a.blk_sel[b]) : 0u;
-    uint32_t chunk;
-    const uint32_t ex = block_exclusive_scan<kSelThreads>(v, scan, &chunk);
-    if (b < a.nblocks) a.blk_sel[b] = carry + ex;
-    carry += chunk;
+  uint32_t ties = 0, sure = 0;
+  const uint32_t i0 = blockIdx.x * kSelTile + threadIdx.x * kSelItems;
+#pragma unroll
+  for (int e = 0; e < kSelItems; ++e) {
+    const uint32_t i = i0 + e;
+    if (i < a.n) {
+      const uint32_t key = a.keys[i];
+      if (st.topk && key == st.thresh) ++ties;
+      if (a.base[i] != 0 || (st.topk && key > st.thresh)) ++sure;
+    }
+  }
+  uint32_t tile_ties, tile_sure;
+  block_exclusive_scan<kSelThreads>(ties, scan, &tile_ties);
+  block_exclusive_scan<kSelThreads>(sure, scan, &tile_sure);
+  if (threadIdx.x == 0) {
+    a.blk_ties[blockIdx.x] = tile_ties;
+    a.blk_sel[blockIdx.x] = tile_sure;
+  }
+  if (!last_block(&a.ws[kCtrl + C_T_TIES], a.nblocks, &flag)) return;
+  uint32_t carry_t = 0, carry_s = 0;
+  if (st.topk && st.thresh == kKeyNegInf) {
+    for (uint32_t b = 0; b < a.nblocks; ++b) {
+      uint32_t tt, ts;
+      const uint32_t bits = tile_selected_bits(a, st, b, carry_t, scan, &tt);
+      block_exclusive_scan<kSelThreads>(__popc(bits), scan, &ts);
+      if (threadIdx.x == 0) {
+        a.blk_ties[b] = carry_t;
+        a.blk_sel[b] = carry_s;
+      }
+      carry_t += tt;
+      carry_s += ts;
+    }
+  } else {
+    for (uint32_t b0 = 0; b0 < a.nblocks; b0 += kSelThreads) {
+      const uint32_t b = b0 + threadIdx.x;
+      const uint32_t t = b < a.nblocks ? ld_acq(&a.blk_ties[b]) : 0u;
+      const uint32_t su = b < a.nblocks ? ld_acq(&a.blk_sel[b]) : 0u;
+      uint32_t chunk_t, chunk_s;
+      const uint32_t tie_off = carry_t + block_exclusive_scan<kSelThreads>(t, scan, &chunk_t);
+      const int64_t left = int64_t(st.need) - int64_t(tie_off);
+      const uint32_t taken = !st.topk || left <= 0 ? 0u : (left < int64_t(t) ? uint32_t(left) : t);
+      const uint32_t out_off = carry_s + block_exclusive_scan<kSelThreads>(su + taken, scan, &chunk_s);
+      if (b < a.nblocks) {
+        a.blk_ties[b] = tie_off;
+        a.blk_sel[b] = out_off;
+      }
+      carry_t += chunk_t;
+      carry_s += chunk_s;
+    }
   }
   if (threadIdx.x == 0) {
-    a.ws[kCtrl + C_TOTAL] = carry;
-    *a.out_count = int64_t(carry);
+    a.ws[kCtrl + C_TOTAL] = carry_s;
+    *a.out_count = int64_t(carry_s);
   }
 }
 
 __global__ __launch_bounds__(kSelThreads) void sel_write_kernel(const SelArgs a) {
   __shared__ uint32_t scan[8];
   const SelState st = load_state(a);
-  const uint32_t bits = selected_bits(a, st, scan);
+  uint32_t tile_ties;
+  const uint32_t bits = tile_selected_bits(a, st, blockIdx.x, a.blk_ties[blockIdx.x], scan, &tile_ties);
   uint32_t total;
   uint32_t pos = a.blk_sel[blockIdx.x] + block_exclusive_scan<kSelThreads>(__popc(bits), scan, &total);
   const uint32_t i0 = blockIdx.x * kSelTile + threadIdx.x * kSelItems;
@@ -502,24 +525,34 @@ __global__ __launch_bounds__(kSelThreads) void sel_write_kernel(const SelArgs a)
 
 __global__ void write_zero_count_kernel(int64_t* out_count) { *out_count = 0; }
 
-int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced, int64_t n,
-                  int64_t radius, double ratio, int64_t* out_idx, int64_t* out_count, void* ws,
-                  size_t ws_bytes, hipStream_t stream) {
+int check_select(const float* scores, const uint8_t* gap, int64_t n, int64_t radius, double ratio,
+                 int64_t* out_idx, int64_t* out_count, void* ws, size_t ws_bytes) {
   CBK_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "n out of range");
   CBK_REQUIRE(out_count != nullptr, "out_count is NULL");
   CBK_REQUIRE(radius >= 0 && radius <= CBK_MAX_DILATION_RADIUS,
               "dilation radius %lld outside [0, %d]", (long long)radius, CBK_MAX_DILATION_RADIUS);
   CBK_REQUIRE(ratio == ratio, "ratio is NaN");
-  if (n == 0) {
-    hipLaunchKernelGGL(write_zero_count_kernel, dim3(1), dim3(1), 0, stream, out_count);
-    return launch_status("select (empty)");
-  }
+  if (n == 0) return CBK_OK;
   CBK_REQUIRE(scores && gap && out_idx && ws, "NULL pointer");
   const SelLayout L = sel_layout(n);
   if (ws_bytes < L.bytes)
     return set_error(CBK_ERR_WORKSPACE, "select workspace %zu < %llu bytes", ws_bytes,
                      (unsigned long long)L.bytes);
   CBK_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "workspace must be 16-byte aligned");
+  return CBK_OK;
+}
+
+// header_zeroed: an earlier launch on the stream cleared the kHeader counter
+// words (the fused K-deviation launch does)
+int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced, int64_t n,
+                  int64_t radius, double ratio, int64_t* out_idx, int64_t* out_count, void* ws,
+                  size_t ws_bytes, hipStream_t stream, bool header_zeroed = false) {
+  if (int rc = check_select(scores, gap, n, radius, ratio, out_idx, out_count, ws, ws_bytes)) return rc;
+  if (n == 0) {
+    hipLaunchKernelGGL(write_zero_count_kernel, dim3(1), dim3(1), 0, stream, out_count);
+    return launch_status("select (empty)");
+  }
+  const SelLayout L = sel_layout(n);
   SelArgs a;
   a.scores = scores;
   a.gap = gap;
@@ -537,12 +570,11 @@ int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced
   a.out_count = out_count;
   const dim3 grid(L.nblocks), block(kSelThreads);
   const size_t prep_lds = (4096 + 16 + kSelTile + 2 * size_t(radius) + 1) * sizeof(uint32_t);
-  hipLaunchKernelGGL(sel_zero_kernel, dim3(1), block, 0, stream, a.ws);
+  if (!header_zeroed) hipLaunchKernelGGL(sel_zero_kernel, dim3(1), block, 0, stream, a.ws);
   hipLaunchKernelGGL(sel_prepare_kernel, grid, block, prep_lds, stream, a);
   hipLaunchKernelGGL(sel_pass_kernel<2>, grid, block, 0, stream, a);
   hipLaunchKernelGGL(sel_pass_kernel<3>, grid, block, 0, stream, a);
-  hipLaunchKernelGGL(sel_ties_kernel, grid, block, 0, stream, a);
-  hipLaunchKernelGGL(sel_count_kernel, grid, block, 0, stream, a);
+  hipLaunchKernelGGL(sel_tiecount_kernel, grid, block, 0, stream, a);
   hipLaunchKernelGGL(sel_write_kernel, grid, block, 0, stream, a);
   return launch_status("select");
 }
@@ -619,12 +651,18 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                     cbk_stream_t stream) {
   cbk::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = cbk::check_select(scores_dev, gap_dev, n, radius, ratio, out_idx_dev, out_count_dev,
+                                 workspace_dev, workspace_bytes))
+    return rc;
+  const bool zero = n > 0;  // the score launch clears the selection counters
   if (int rc = cbk::launch_kdev(fresh_dev, fresh_row_stride_elems, cached_dev,
                                 cached_row_stride_elems, cached_num_rows, cached_rows_dev,
-                                cached_row0, n, width, dtype, scores_dev, s))
+                                cached_row0, n, width, dtype, scores_dev, s,
+                                zero ? static_cast<uint32_t*>(workspace_dev) : nullptr,
+                                zero ? cbk::kHeader : 0u))
     return rc;
   return cbk::launch_select(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
-                            out_count_dev, workspace_dev, workspace_bytes, s);
+                            out_count_dev, workspace_dev, workspace_bytes, s, zero);
 }
 
 int cbk_dilate(const uint8_t* gap_dev, int64_t n, int64_t radius, uint8_t* forced_dev,

@@ -69,6 +69,25 @@ def test_select_bit_exact_vs_oracle_random(n):
         np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("n", [300, 5000, 70000])
+def test_select_budget_reaching_minus_inf_ties_with_base(n):
+    """The k-th largest score is -inf, the key base tokens carry too: ties
+    then include base tokens and are taken in index order across tiles (the
+    tile counts come from a token-by-token pass)."""
+    rng = np.random.default_rng(n + 1)
+    scores = np.full(n, -np.inf, dtype=np.float32)
+    finite = rng.random(n) < 0.3
+    scores[finite] = rng.random(int(finite.sum())).astype(np.float32)
+    gap = rng.random(n) < 0.2
+    forced = rng.random(n) < 0.05
+    for ratio, radius in ((0.9, 0), (0.6, 4), (0.31, 0)):
+        fc = forced | (O.dilate(gap, radius) if radius else False)
+        want = O.select(scores, gap, ratio, fc)
+        got = S.select(torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV), ratio,
+                       torch.from_numpy(forced).to(DEV), radius=radius)
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"ratio {ratio} radius {radius}")
+
+
 def test_select_dilation_equals_forced_mask_composition():
     # cbk_select(radius=r) == _select(gap, forced=dilate(gap, r))
     rng = np.random.default_rng(9)
