@@ -113,3 +113,27 @@ def test_blend_attention_gaussian_inputs_rounding_boundary_bound():
     print(f"gaussian: {outside.mean():.2e} of elements outside, max ratio {ratio.max():.3e}", flush=True)
     assert outside.mean() < 1e-4
     assert ratio.max() < 5e-2
+
+
+def test_blend_attention_full_blend_layer_properties():
+    """The blend-layer shape (7000 selected queries over 32,767 keys, 32 query
+    heads on 4 KV heads of 128 bf16): with every key's value equal to one
+    vector c per KV head, each output row is c exactly (the probabilities sum
+    to one); with values +c / -c split by key parity the output stays within
+    [-|c|, |c|]; and the launch is deterministic."""
+    nq, nk, hq, hkv, d = 7000, 32767, 32, 4, 128
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q = (torch.randn((nq, hq, d), generator=g, device=DEV) / d ** 0.25).to(torch.bfloat16)
+    k = (torch.randn((nk, hkv, d), generator=g, device=DEV) / d ** 0.25).to(torch.bfloat16)
+    pos = torch.from_numpy(np.sort(np.random.default_rng(5).choice(np.arange(2048, nk), nq, replace=False))).to(DEV)
+    c = (torch.randn((hkv, d), generator=g, device=DEV)).to(torch.bfloat16)
+    v = c[None].expand(nk, hkv, d).contiguous()
+    out = blend_attention(q, k, v, pos, d ** -0.5)
+    want = c.repeat_interleave(hq // hkv, dim=0)[None].expand(nq, hq, d)
+    assert torch.equal(out, want)
+    sign = torch.where(torch.arange(nk, device=DEV) % 2 == 0, 1.0, -1.0).to(torch.bfloat16)
+    v2 = (v * sign[:, None, None]).contiguous()
+    out2 = blend_attention(q, k, v2, pos, d ** -0.5)
+    bound = want.float().abs() * (1 + 2 ** -7)
+    assert bool((out2.float().abs() <= bound).all())
+    assert torch.equal(out2, blend_attention(q, k, v2, pos, d ** -0.5))

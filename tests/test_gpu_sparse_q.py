@@ -147,3 +147,28 @@ def test_sparse_q_tail_fallback_no_gaps():
     assert stats["tail_fallback"] and stats["sparse_query_tokens"] == 64
     assert forced.cpu().numpy().tolist() == want_forced.tolist()
     np.testing.assert_allclose(scores.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
+
+
+def test_sparse_q_full_layer6_properties():
+    """The layer-6 Sparse-Q shape (4096 gap queries over a 98,304-key causal
+    context, 32 query heads on 4 KV heads of 128 bf16): the column sums add up
+    to queries x heads (every softmax row sums to one), scores are finite and
+    non-negative, keys after the last query position get nothing, and the
+    launch is deterministic."""
+    from cacheblend_vllm import synthetic
+
+    nk, hq, hkv, d, nq = 98304, 32, 4, 128, 4096
+    g = torch.Generator(device=DEV).manual_seed(0)
+    query = (torch.randn((nk, hq, d), generator=g, device=DEV) / d ** 0.5).to(torch.bfloat16)
+    key = (torch.randn((nk, hkv, d), generator=g, device=DEV) / d ** 0.5).to(torch.bfloat16)
+    gap = synthetic.sparse_q_layout(nk, nq, seed=0)
+    rows = torch.from_numpy(np.flatnonzero(gap)).to(DEV)
+    absolute = torch.arange(nk, device=DEV)
+    _, full = S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, want_full=True)
+    full = full.cpu().numpy().astype(np.float64)
+    assert np.isfinite(full).all() and (full >= 0).all()
+    assert abs(full.sum() - nq * hq) < 1e-3 * nq * hq
+    last = int(rows.max())
+    assert (full[last + 1:] == 0).all()
+    _, again = S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, want_full=True)
+    assert np.array_equal(again.cpu().numpy().astype(np.float64), full)
