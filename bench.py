@@ -569,21 +569,29 @@ def blend_load(torch, synthetic, dev, args):
         h.copy_(torch.randn(h.shape, device=dev, dtype=torch.bfloat16))
     slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=256)
 
-    def make_store(fragmented):
-        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if fragmented else None)
+    def make_store(layout):
+        """layout "views": per-layer [2, hit] host tensors sliced per chunk;
+        "slab_runs": one slab run per layer over all chunks, as the store
+        path allocates a layer's chunks (consecutive slots); "slab_chunks":
+        one slab slot per (chunk, layer) in chunk-major order, so a layer's
+        chunks lie 48 slots apart and break at every arena."""
+        store = PinnedChunkStore(256, 1 << 40, on_release=None if layout == "views" else slab.free)
+        runs = [slab.alloc_run(hit // 256) for _ in range(L)] if layout == "slab_runs" else None
         blend_segments = []
         off = 0
+        k = 0
         for i, (s0, t0, n) in enumerate(segs):
             for c in range(0, n, 256):
                 sid = store.begin_put("bench", s0 + c, list(range(s0 + c + 7 * i, s0 + c + 7 * i + 256)), L)
                 for l in range(L):
                     view = hosts[l][:, off + c : off + c + 256]
-                    if fragmented:
-                        slot = slab.alloc()
+                    if layout != "views":
+                        slot = runs[l][k] if runs is not None else slab.alloc()
                         slot.copy_(view)
                         view = slot
                     store.put_layer_host(sid, l, view)
                 blend_segments.append(BlendSegment(sid, t0 + c))
+                k += 1
             off += n
         store.pin("blend", blend_segments)
         return store, BlendPlan(APC, A, hit, tuple(blend_segments))
@@ -621,7 +629,7 @@ def blend_load(torch, synthetic, dev, args):
         results = [run(store, plan, zero_copy, compute) for _ in range(reps)]
         return min(r[0] for r in results), results[0][1]
 
-    contiguous, plan_c = make_store(False)
+    contiguous, plan_c = make_store("views")
     dma_s, dma_host_read = best(contiguous, plan_c, "auto")
     read_s, _ = best(contiguous, plan_c, True)
     assert not dma_host_read
@@ -679,18 +687,23 @@ def blend_load(torch, synthetic, dev, args):
     }
     contiguous.release("blend")
     del contiguous
-    fragmented, plan_f = make_store(True)
-    frag_s, frag_host_read = best(fragmented, plan_f, "auto")
-    frag_dma_s, _ = best(fragmented, plan_f, False)
-    out["slab_chunks"] = {
-        "auto_mode": "host_read" if frag_host_read else "dma",
-        "load_only_ms": round(frag_s * 1e3, 3), "h2d_GBps": round(h2d_bytes / frag_s / 1e9, 2),
-        "host_link_frac": round(h2d_bytes / frag_s / 1e9 / HOST_LINK_PEAK_GBPS, 4),
-        "dma_per_chunk_GBps": round(h2d_bytes / frag_dma_s / 1e9, 2),
-        "busy_wait": overlap(frag_s, best(fragmented, plan_f, "auto", busy)[0], busy_s),
-    }
-    fragmented.release("blend")
-    fragmented.clear()
+    for layout in ("slab_runs", "slab_chunks"):
+        store, plan_s = make_store(layout)
+        auto_s, auto_host_read = best(store, plan_s, "auto")
+        dma_s2, _ = best(store, plan_s, False)
+        read_s2, _ = best(store, plan_s, True)
+        out[layout] = {
+            "auto_mode": "host_read" if auto_host_read else "dma",
+            "load_only_ms": round(auto_s * 1e3, 3), "h2d_GBps": round(h2d_bytes / auto_s / 1e9, 2),
+            "host_link_frac": round(h2d_bytes / auto_s / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+            "dma_GBps": round(h2d_bytes / dma_s2 / 1e9, 2),
+            "host_read_GBps": round(h2d_bytes / read_s2 / 1e9, 2),
+            "busy_wait": overlap(auto_s, best(store, plan_s, "auto", busy)[0], busy_s),
+            "gemm": overlap(auto_s, best(store, plan_s, "auto", gemms)[0], gemm_s),
+        }
+        log(f"blend load {layout}: {out[layout]}")
+        store.release("blend")
+        store.clear()
     slab.close()
 
     # the commit's device scatter alone (loader.commit: [2, apc:A] of the

@@ -182,14 +182,26 @@ int cbk_stream_destroy(cbk_stream_t stream);
 
 /*
  * n asynchronous copies dst[i] <- src[i] of bytes[i] bytes on `stream`
- * (hipMemcpyAsync, direction from the addresses), issued in order; the
- * tables are host arrays. The DMA path of the layerwise loads and stores:
- * one call per layer for the coalesced pinned runs that the reference
- * copies with one non_blocking torch copy each (cacheblend_vllm/ascend.py:
- * 358-370, connector.py:425-429).
+ * (direction from the addresses); the tables are host arrays and the runs
+ * must not overlap. The DMA path of the layerwise loads and stores: one
+ * call per layer for the pinned runs that the reference copies with one
+ * non_blocking torch copy each (cacheblend_vllm/ascend.py:358-370,
+ * connector.py:425-429). Consecutive runs are folded into as few DMA
+ * commands as their addresses allow: runs adjacent in dst and in src into
+ * one hipMemcpyAsync, runs of one size at constant dst and src pitches
+ * into one hipMemcpy2DAsync.
  */
 int cbk_memcpy_runs(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n,
                     cbk_stream_t stream);
+
+/*
+ * The number of DMA commands cbk_memcpy_runs issues for these runs (no GPU
+ * call). The loader compares bytes per command against its threshold to
+ * choose DMA or in-place host reads (the reference always copies,
+ * cacheblend_vllm/ascend.py:358-370).
+ */
+int cbk_memcpy_runs_commands(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n,
+                             int64_t* commands);
 
 /*
  * K-deviation scores: scores[i] = sum_j (f32(fresh[i, j]) - f32(cached[r_i, j]))^2

@@ -10,6 +10,7 @@ import ctypes
 import os
 import threading
 
+import numpy as np
 import torch
 
 LIB_NAME = "libcacheblend_hip.so"
@@ -109,6 +110,7 @@ _SIGNATURES = {
     "cbk_slab_destroy": (ctypes.c_int, [c_vp]),
     "cbk_host_accessible": (ctypes.c_int, [c_vp, ctypes.c_size_t, ctypes.POINTER(c_i32)]),
     "cbk_memcpy_runs": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "cbk_memcpy_runs_commands": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, ctypes.POINTER(c_i64)]),
     "cbk_side_streams": (ctypes.c_int, [c_vp, c_i32, c_i32, ctypes.c_float, ctypes.POINTER(c_vp),
                                         ctypes.POINTER(c_i32)]),
     "cbk_stream_destroy": (ctypes.c_int, [c_vp]),
@@ -207,6 +209,28 @@ def require_device(tensor: torch.Tensor, what: str) -> None:
 
 def ptr(tensor: torch.Tensor | None) -> int | None:
     return None if tensor is None else tensor.data_ptr()
+
+
+def _run_table(dst: np.ndarray, src: np.ndarray, nbytes: np.ndarray) -> tuple[np.ndarray, ...]:
+    tables = tuple(np.ascontiguousarray(a, dtype=np.uint64) for a in (dst, src, nbytes))
+    if not tables[0].shape == tables[1].shape == tables[2].shape or tables[0].ndim != 1:
+        raise ValueError("dst, src and bytes must be 1-D tables of one length")
+    return tables
+
+
+def memcpy_runs(dst: np.ndarray, src: np.ndarray, nbytes: np.ndarray, stream: int, what: str) -> None:
+    """cbk_memcpy_runs over uint64 tables (addresses and sizes in bytes)."""
+    d, s, b = _run_table(dst, src, nbytes)
+    check(load().cbk_memcpy_runs(d.ctypes.data, s.ctypes.data, b.ctypes.data, d.shape[0], stream), what)
+
+
+def memcpy_commands(dst: np.ndarray, src: np.ndarray, nbytes: np.ndarray) -> int:
+    """DMA commands cbk_memcpy_runs would issue for these runs."""
+    d, s, b = _run_table(dst, src, nbytes)
+    out = c_i64()
+    check(load().cbk_memcpy_runs_commands(d.ctypes.data, s.ctypes.data, b.ctypes.data, d.shape[0],
+                                           ctypes.byref(out)), "memcpy_runs_commands")
+    return out.value
 
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}

@@ -13,9 +13,10 @@
 
 Per layer, on the Load stream (a default-priority side stream):
   1. the hit chunks cross the host link: either DMA (``cbk_memcpy_runs``:
-     chunks adjacent in pinned host memory coalesced into one copy per run
-     and plane, into a reusable device hit staging ``[2, hit_tokens, H, D]``)
-     or, for fragmented chunks, in place -- the assembly kernel reads them
+     chunks adjacent in pinned host memory folded into one copy per run and
+     plane, chunks at a constant slot pitch into one 2D copy per plane, into
+     a ring of device hit stagings ``[2, hit_tokens, H, D]``) or, for chunks
+     scattered over the slab, in place -- the assembly kernel reads them
      from pinned host memory through a per-layer address table;
   2. ``cbk_blend_assemble`` (``_chunks`` for in-place reads) writes the
      layer buffer in one pass: APC prefix from the pages, zeros for gaps,
@@ -134,8 +135,9 @@ class PagedBlendLoader:
                16-byte aligned planes), the assembly kernel can read the hit
                rows in place (``max_workgroups`` bounds the CUs it holds).
         ``zero_copy``: True forces host reads where possible, False forces
-        DMA, "auto" reads in place only when the runs average fewer than
-        ``dma_min_run_bytes`` per copy, where per-copy DMA cost dominates.
+        DMA, "auto" reads in place only when the DMA commands would average
+        fewer than ``dma_min_run_bytes`` each, where per-command DMA cost
+        (about 9 us, the time of 0.5 MB) dominates.
         ``dma_staging_bytes`` bounds the device ring the DMA fills (at least
         two layers' hits): with room for every layer the copies of a request
         never wait for an assembly."""
@@ -239,18 +241,18 @@ class PagedBlendLoader:
             return None
         return chunk, flat
 
-    def _address_runs(self, flat: list[int], row_bytes: int) -> list[tuple[int, int, int, int]]:
-        """Maximal runs of consecutive segments whose K (and V) planes are
-        adjacent in host memory: ``(first_hit_row, tokens, k_addr, v_addr)``."""
+    def _hit_copies(self, flat: list[int]) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """DMA run table of the layer's hits as uint64 arrays ``(dst offset in
+        the hit staging, host src, bytes)``: every segment's K plane, then
+        every V plane. ``cbk_memcpy_runs`` folds runs adjacent on both sides,
+        and equal runs at constant pitches (consecutive slab slots), into
+        single DMA commands."""
         kv = np.array(flat, dtype=np.uint64).reshape(-1, 2)
+        off = self._seg_row_off[:-1].astype(np.uint64) * np.uint64(self._row_bytes)
+        v_plane = np.uint64(self.plan.hit_tokens * self._row_bytes)
         plane = self._seg_plane_bytes.astype(np.uint64)
-        # segment i + 1 continues segment i's run when both planes follow on
-        joined = (kv[1:, 0] == kv[:-1, 0] + plane[:-1]) & (kv[1:, 1] == kv[:-1, 1] + plane[:-1])
-        starts = np.flatnonzero(np.concatenate(([True], ~joined)))
-        ends = np.append(starts[1:], len(kv))
-        row_off = self._seg_row_off
-        return [(int(row_off[a]), int(row_off[b] - row_off[a]), int(kv[a, 0]), int(kv[a, 1]))
-                for a, b in zip(starts.tolist(), ends.tolist())]
+        return (np.concatenate((off, off + v_plane)), np.ascontiguousarray(kv.T).reshape(-1),
+                np.concatenate((plane, plane)))
 
     def _hit_slot(self, layer_id: int) -> int:
         return layer_id % self._hit_ring.shape[0]
@@ -275,10 +277,11 @@ class PagedBlendLoader:
         found = self._chunk_addresses(layer_id)
         if found is not None:
             chunk, flat = found
-            row_bytes = self._row_bytes
-            runs = self._address_runs(flat, row_bytes)
-            avg = self.plan.hit_tokens * row_bytes / max(1, len(runs))
-            host_read = self._zero_copy is True or (self._zero_copy == "auto" and avg < self._dma_min_run_bytes)
+            dst_off, src, nbytes = self._hit_copies(flat)
+            host_read = self._zero_copy is True
+            if self._zero_copy == "auto":
+                commands = _native.memcpy_commands(dst_off, src, nbytes)
+                host_read = int(nbytes.sum()) / max(1, commands) < self._dma_min_run_bytes
             if host_read:
                 # publish the layer's chunk addresses; the assembly kernel
                 # reads the hit rows over the host link
@@ -294,23 +297,9 @@ class PagedBlendLoader:
                 return
             self._zc_layers.discard(layer_id)
             hit = self._ensure_hit_staging(layer_id)
-            kb, vb = hit[0].data_ptr(), hit[1].data_ptr()
-            copies: list[list[int]] = []  # [dst, src, bytes]; K runs, then V runs
-            for plane_base, which in ((kb, 2), (vb, 3)):
-                for run in runs:
-                    dst, src, nb = plane_base + run[0] * row_bytes, run[which], run[1] * row_bytes
-                    last = copies[-1] if copies else None
-                    if last is not None and last[0] + last[2] == dst and last[1] + last[2] == src:
-                        last[2] += nb  # adjacent on both sides (e.g. K plane end = V plane start)
-                    else:
-                        copies.append([dst, src, nb])
-            n = len(copies)
-            dst = (ctypes.c_uint64 * n)(*[c[0] for c in copies])
-            src = (ctypes.c_uint64 * n)(*[c[1] for c in copies])
-            nbytes = (ctypes.c_uint64 * n)(*[c[2] for c in copies])
+            dst = dst_off + np.uint64(hit.data_ptr())
             if self._load_stream is None:
-                _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n,
-                                                             _native.stream_handle(self.device)), "hit runs H2D")
+                _native.memcpy_runs(dst, src, nbytes, _native.stream_handle(self.device), "hit runs H2D")
                 return
             # DMA on the copy stream, back to back with the previous layer's;
             # a ring slot is refilled only after the assembly that read it
@@ -318,8 +307,7 @@ class PagedBlendLoader:
             free = self._hit_free.pop(self._hit_slot(layer_id), None)
             if free is not None and not free.query():
                 free.synchronize()
-            _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, n, self._copy_stream.cuda_stream),
-                          "hit runs H2D")
+            _native.memcpy_runs(dst, src, nbytes, self._copy_stream.cuda_stream, "hit runs H2D")
             copied = torch.cuda.Event()
             copied.record(self._copy_stream)
             self._load_stream.wait_event(copied)

@@ -39,6 +39,7 @@ from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass, field
 from typing import Any
 
+import numpy as np
 import torch
 
 from . import _native
@@ -332,25 +333,19 @@ class StoreStreamWriter:
                         host: list[torch.Tensor]) -> tuple[torch.Tensor, tuple]:
         """Gather the layer's chunks into a fresh chunk-major device staging
         laid out like the slots (``chunk_bytes`` apart) on the current
-        (Store) stream; returns it with the D2H runs (host dst, device src,
-        bytes) that the copier issues once the gather is done."""
+        (Store) stream; returns it with the D2H run table (host dst, device
+        src, bytes: one run per chunk, which ``cbk_memcpy_runs`` folds into
+        one copy for consecutive slots) that the copier issues once the
+        gather is done."""
         stride = self._slab.chunk_bytes
         n = len(host)
         key, _ = kv_planes(kv_layer)
         staging = torch.empty(n * stride, dtype=torch.uint8, device=key.device)
         base = staging.data_ptr()
         self._gather_to_chunks(kv_layer, slots, [base + i * stride for i in range(n)])
-        runs: list[list[int]] = []
-        for i, h in enumerate(host):
-            p = h.data_ptr()
-            if runs and p == runs[-1][0] + runs[-1][2]:
-                runs[-1][2] += stride
-            else:
-                runs.append([p, base + i * stride, stride])
-        m = len(runs)
-        return staging, ((ctypes.c_uint64 * m)(*[r[0] for r in runs]),
-                         (ctypes.c_uint64 * m)(*[r[1] for r in runs]),
-                         (ctypes.c_uint64 * m)(*[r[2] for r in runs]), m)
+        dst = np.array([h.data_ptr() for h in host], dtype=np.uint64)
+        src = np.uint64(base) + np.arange(n, dtype=np.uint64) * np.uint64(stride)
+        return staging, (dst, src, np.full(n, stride, dtype=np.uint64))
 
     def _copier_queue(self) -> queue.Queue:
         if self._copier is None:
@@ -370,11 +365,10 @@ class StoreStreamWriter:
             job = self._copy_jobs.get()
             if job is None:
                 return
-            gathered, staging, (dst, src, nbytes, m), pending, host, request_id, enqueued_ns, future = job
+            gathered, staging, (dst, src, nbytes), pending, host, request_id, enqueued_ns, future = job
             try:
                 gathered.synchronize()
-                _native.check(_native.load().cbk_memcpy_runs(dst, src, nbytes, m, self._copy_stream.cuda_stream),
-                              "chunk runs D2H")
+                _native.memcpy_runs(dst, src, nbytes, self._copy_stream.cuda_stream, "chunk runs D2H")
                 staging.record_stream(self._copy_stream)
                 copied = self._streams.Event()
                 copied.record(self._copy_stream)

@@ -90,6 +90,48 @@ struct Slab {
   }
 };
 
+// One DMA command of a run table: `rows` copies of `width` bytes whose
+// destinations and sources advance by dpitch and spitch bytes (rows == 1: a
+// plain copy of width bytes).
+struct CopyCommand {
+  uint64_t dst, src, width, rows, dpitch, spitch;
+};
+
+// Farthest row pitch folded into one 2D copy.
+constexpr uint64_t kMaxCopyPitch = uint64_t(1) << 31;
+
+// The command that starts at run i (bytes[i] > 0) and the number of runs it
+// covers. Each DMA command costs the engine about as long as moving 0.5 MB,
+// so runs are folded: runs that each start where the previous one ends, in
+// dst and in src, become one copy; failing that, runs of one size whose dst
+// and src both advance by a constant pitch no smaller than that size (rows
+// that cannot overlap) become one 2D copy, which the engine runs as a single
+// command -- e.g. one layer's chunks in consecutive [2, chunk, H, D] slab
+// slots, whose K planes lie one slot apart.
+int64_t next_command(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n, int64_t i,
+                     CopyCommand* cmd) {
+  int64_t j = i + 1;
+  uint64_t total = bytes[i];
+  while (j < n && dst[j] == dst[j - 1] + bytes[j - 1] && src[j] == src[j - 1] + bytes[j - 1]) total += bytes[j++];
+  if (j - i >= 2) {
+    *cmd = {dst[i], src[i], total, 1, 0, 0};
+    return j - i;
+  }
+  const uint64_t w = bytes[i];
+  if (i + 1 < n && bytes[i + 1] == w) {
+    // unsigned differences: a backward step wraps far above kMaxCopyPitch
+    const uint64_t dp = dst[i + 1] - dst[i], sp = src[i + 1] - src[i];
+    if (dp >= w && sp >= w && dp <= kMaxCopyPitch && sp <= kMaxCopyPitch) {
+      j = i + 2;
+      while (j < n && bytes[j] == w && dst[j] - dst[j - 1] == dp && src[j] - src[j - 1] == sp) ++j;
+      *cmd = {dst[i], src[i], w, uint64_t(j - i), dp, sp};
+      return j - i;
+    }
+  }
+  *cmd = {dst[i], src[i], w, 1, 0, 0};
+  return 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -195,13 +237,46 @@ int cbk_memcpy_runs(const uint64_t* dst, const uint64_t* src, const uint64_t* by
   CBK_REQUIRE(n >= 0, "negative run count");
   if (n == 0) return CBK_OK;
   CBK_REQUIRE(dst != nullptr && src != nullptr && bytes != nullptr, "NULL run table");
-  for (int64_t i = 0; i < n; ++i) {
-    if (bytes[i] == 0) continue;
-    CBK_REQUIRE(dst[i] != 0 && src[i] != 0, "run %lld has a NULL address", (long long)i);
-    const hipError_t err = hipMemcpyAsync(reinterpret_cast<void*>(dst[i]), reinterpret_cast<const void*>(src[i]),
-                                          size_t(bytes[i]), hipMemcpyDefault, static_cast<hipStream_t>(stream));
+  for (int64_t i = 0; i < n; ++i)
+    CBK_REQUIRE(bytes[i] == 0 || (dst[i] != 0 && src[i] != 0), "run %lld has a NULL address", (long long)i);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int64_t i = 0; i < n;) {
+    if (bytes[i] == 0) {
+      ++i;
+      continue;
+    }
+    CopyCommand c;
+    const int64_t covered = next_command(dst, src, bytes, n, i, &c);
+    void* d = reinterpret_cast<void*>(c.dst);
+    const void* from = reinterpret_cast<const void*>(c.src);
+    const hipError_t err = c.rows == 1
+                               ? hipMemcpyAsync(d, from, size_t(c.width), hipMemcpyDefault, s)
+                               : hipMemcpy2DAsync(d, size_t(c.dpitch), from, size_t(c.spitch), size_t(c.width),
+                                                  size_t(c.rows), hipMemcpyDefault, s);
     if (err != hipSuccess)
-      return cbk::set_error(CBK_ERR_LAUNCH, "hipMemcpyAsync of run %lld: %s", (long long)i, hipGetErrorString(err));
+      return cbk::set_error(CBK_ERR_LAUNCH, "copy of runs %lld..%lld: %s", (long long)i,
+                            (long long)(i + covered - 1), hipGetErrorString(err));
+    i += covered;
+  }
+  return CBK_OK;
+}
+
+int cbk_memcpy_runs_commands(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n,
+                             int64_t* commands) {
+  cbk::clear_error();
+  CBK_REQUIRE(commands != nullptr, "commands is NULL");
+  CBK_REQUIRE(n >= 0, "negative run count");
+  *commands = 0;
+  if (n == 0) return CBK_OK;
+  CBK_REQUIRE(dst != nullptr && src != nullptr && bytes != nullptr, "NULL run table");
+  for (int64_t i = 0; i < n;) {
+    if (bytes[i] == 0) {
+      ++i;
+      continue;
+    }
+    CopyCommand c;
+    i += next_command(dst, src, bytes, n, i, &c);
+    ++*commands;
   }
   return CBK_OK;
 }

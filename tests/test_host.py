@@ -153,40 +153,51 @@ def test_layer_chunk_addresses_requires_pins_and_addressable_chunks():
         store.get_layer("r", seg, 0)
 
 
-def test_loader_address_runs_join_adjacent_segments():
-    """The loader's run search over host chunk addresses: segments join a
-    run exactly when both their K and V planes follow the previous
-    segment's (checked against a direct scan on random layouts)."""
-    import types
-
+def _slot_layout_runs(n, plane, slot_pitch, base=1 << 32):
+    """The loader's hit run table for n full chunks whose [2, chunk, H, D]
+    slots start slot_pitch bytes apart: K planes, then V planes."""
     import numpy as np
 
-    from cacheblend_vllm.loader import PagedBlendLoader
+    k = base + np.arange(n, dtype=np.uint64) * np.uint64(slot_pitch)
+    dst = np.arange(2 * n, dtype=np.uint64) * np.uint64(plane)
+    return dst, np.concatenate((k, k + np.uint64(plane))), np.full(2 * n, plane, dtype=np.uint64)
 
-    rng = np.random.default_rng(4)
-    row = 1024
-    for _ in range(200):
-        lengths = rng.integers(1, 5, size=int(rng.integers(1, 12))) * 16
-        k = v = None
-        flat = []
-        for i, n in enumerate(lengths):
-            if i and rng.random() < 0.6:  # continue both planes
-                k, v = k + prev * row, v + prev * row
-            elif i and rng.random() < 0.5:  # only K continues
-                k, v = k + prev * row, v + 4096 * row
-            else:
-                k, v = int(rng.integers(1, 1 << 30)) * 64, int(rng.integers(1, 1 << 30)) * 64
-            flat += [k, v]
-            prev = int(n)
-        fake = types.SimpleNamespace(_seg_plane_bytes=lengths.astype(np.int64) * row,
-                                     _seg_row_off=np.concatenate(([0], np.cumsum(lengths))))
-        got = PagedBlendLoader._address_runs(fake, flat, row)
-        want, off = [], 0
-        for i, n in enumerate(lengths.tolist()):
-            kk, vv = flat[2 * i], flat[2 * i + 1]
-            if want and kk == want[-1][2] + want[-1][1] * row and vv == want[-1][3] + want[-1][1] * row:
-                want[-1][1] += n
-            else:
-                want.append([off, n, kk, vv])
-            off += n
-        assert got == [tuple(w) for w in want]
+
+def test_memcpy_runs_commands_known_answers():
+    """How many DMA commands cbk_memcpy_runs folds a run table into (host
+    arithmetic, no GPU call): runs adjacent on both sides make one copy,
+    equal runs at constant ascending pitches >= their size one 2D copy."""
+    import numpy as np
+
+    from cacheblend_vllm import _native
+
+    u = lambda *v: np.array(v, dtype=np.uint64)  # noqa: E731
+    count = _native.memcpy_commands
+    assert count(u(), u(), u()) == 0
+    assert count(u(64), u(128), u(0)) == 0  # zero-byte runs are skipped
+    assert count(u(64), u(128), u(32)) == 1
+    # adjacent on both sides, sizes differ: one copy
+    assert count(u(0, 10, 40, 41), u(100, 110, 140, 141), u(10, 30, 1, 7)) == 1
+    # adjacent in dst only: not a chain, and unequal sizes: one copy each
+    assert count(u(0, 10), u(100, 200), u(10, 30)) == 2
+    # the store's layout: consecutive slots (pitch 2 planes) -> one 2D copy per plane
+    for n in (1, 2, 5, 109):
+        assert count(*_slot_layout_runs(n, 4096, 8192)) == (1 if n == 1 else 2)
+        assert count(*_slot_layout_runs(n, 4096, 48 * 8192)) == (1 if n == 1 else 2)
+    # slots back to back with the K and V planes of each slot contiguous in the
+    # destination too ([2, T] host views of one tensor): one copy in all
+    k = u(*range(0, 8 * 1000, 1000))
+    assert count(np.concatenate((k, k + 8000)), np.concatenate((k, k + 8000)) + 7, np.full(16, 1000, np.uint64)) == 1
+    # a pitch below the size (rows would overlap) or a backward step never folds
+    assert count(u(0, 100, 200), u(0, 50, 100), u(80, 80, 80)) == 3
+    assert count(u(200, 100, 0), u(0, 100, 200), u(80, 80, 80)) == 3
+    # pitches beyond 2^31 are issued row by row
+    far = np.uint64(1 << 32)
+    assert count(u(0, 1 << 32, 2 << 32), u(0, 100, 200), u(80, 80, 80)) == 3
+    assert count(u(0, 100, 200), np.array([0, far, 2 * far], dtype=np.uint64), u(80, 80, 80)) == 3
+    # a group ends where the size or a pitch changes, or at a zero-byte run
+    assert count(u(0, 100, 200, 300, 400), u(0, 200, 400, 600, 900), u(50, 50, 50, 50, 50)) == 2
+    assert count(u(0, 100, 200, 300), u(0, 200, 400, 600), u(50, 50, 60, 50)) == 3
+    assert count(u(0, 100, 200, 300, 400), u(0, 200, 400, 600, 800), u(50, 50, 0, 50, 50)) == 2
+    with pytest.raises(ValueError, match="one length"):
+        count(u(0, 1), u(0), u(8))
