@@ -41,7 +41,6 @@ constexpr int kQTile = 16;
 constexpr int kKeyBlock1 = 64;        // keys per LDS block in rowstats
 constexpr int kColTiles = 4;          // 16-key column tiles per wave in colsum
 constexpr int kKeyBlock2 = 4 * 16 * kColTiles;  // 256 keys per colsum workgroup
-constexpr int kMaxHeadsInLds = 8;     // query heads staged per colsum LDS load
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
 
