@@ -73,6 +73,28 @@ def profiled_traffic() -> int | None:
     return None
 
 
+def queued_time_ms(torch, fn, reps: int, cycles_per_us: float) -> tuple[float, float]:
+    """(device ms per call, host enqueue ms per call) of ``reps`` calls of fn
+    on the current stream. The calls are enqueued behind a spin kernel that
+    outlasts their enqueueing, so the events time the device back to back
+    from a full queue, whatever the host's speed."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int((2.0 * host_ms + 1.0) * 1e3 * cycles_per_us))
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps, host_ms / reps
+
+
 def event_time_ms(torch, fn, reps: int) -> float:
     """Average device time of fn() measured with HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -234,7 +256,8 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     lib_sel = lambda: S.kdev_select(fresh, cached, None, gap, 0.15, radius=16)  # noqa: E731
     selected, _ = lib_sel()
     reps = 50
-    dev_ms = event_time_ms(torch, lambda: _kdev_async(torch, S, fresh, cached, gap), reps)
+    dev_ms, enqueue_ms = queued_time_ms(torch, lambda: _kdev_async(torch, S, fresh, cached, gap), reps,
+                                        _sleep_cycles_per_us(torch))
     t0 = time.perf_counter()
     for _ in range(reps):
         lib_sel()
@@ -243,6 +266,7 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     score_ms = event_time_ms(torch, lambda: S.kdev_scores(fresh, cached), reps)
     out["kdev_select"] = {
         "us_per_64k_tokens": round(dev_ms * 1e3, 2),
+        "host_enqueue_us": round(enqueue_ms * 1e3, 2),
         "wall_us_with_count_readback": round(wall_ms * 1e3, 2),
         "score_kernel_us": round(score_ms * 1e3, 2),
         "score_kernel_GBps": round(read_bytes / (score_ms / 1e3) / 1e9, 1),
