@@ -191,10 +191,11 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
       // scale > 0 preserves order
       const float bm2 = fmaxf(fmaxf(raw[0], raw[1]), fmaxf(raw[2], raw[3])) * a.c2;
       const float mn = fmaxf(m[t][i], bm2);
-      const float ms = mn == kNegInf ? 0.f : mn;
-      float sum = 0.f;
+      // an unmasked block's dots are finite, so is its maximum
+      const float ms = (MASK && mn == kNegInf) ? 0.f : mn;
+      float sum = __builtin_amdgcn_exp2f(fmaf(r[0], a.c2, -ms));
 #pragma unroll
-      for (int c = 0; c < kColTiles; ++c) sum += __builtin_amdgcn_exp2f(fmaf(r[c], a.c2, -ms));
+      for (int c = 1; c < kColTiles; ++c) sum += __builtin_amdgcn_exp2f(fmaf(r[c], a.c2, -ms));
       l[t][i] = fmaf(l[t][i], __builtin_amdgcn_exp2f(m[t][i] - ms), sum);
       m[t][i] = mn;
     }
