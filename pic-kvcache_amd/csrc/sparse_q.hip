@@ -38,6 +38,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kQTile = 16;
+constexpr int kTileWords = 32;        // per query tile: 16 positions, min, max, unused
 constexpr int kKeyBlock1 = 64;        // keys per LDS block in rowstats
 constexpr int kColTiles = 4;          // 16-key column tiles per wave in colsum
 constexpr int kKeyBlock2 = 4 * 16 * kColTiles;  // 256 keys per colsum workgroup
@@ -55,8 +56,9 @@ struct SqArgs {
   float c2;               // scale * log2(e)
   int32_t round_mode;     // 0 none, 1 bf16, 2 f16
   float2* stats;          // [hq][nq_pad] (m2 + log2(l), unused)
-  int32_t* tile_pos;      // [ntiles][2] (min, max) position per query tile
+  int32_t* tiles;         // [ntiles][32]: the 16 query positions (-1 past nq), min, max, unused
   float* partial;         // [hkv][nk]
+  uint16_t* qdense;       // [ntiles][hkv][groups][16][D]: query rows in colsum's unit order
   uint32_t nq_pad;
 };
 
@@ -228,8 +230,8 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
     s_minmax[0] = lo;
     s_minmax[1] = hi;
     if (g == 0) {
-      a.tile_pos[2 * qt] = lo;
-      a.tile_pos[2 * qt + 1] = hi;
+      a.tiles[kTileWords * qt + kQTile] = lo;
+      a.tiles[kTileWords * qt + kQTile + 1] = hi;
     }
   }
   __syncthreads();
@@ -252,7 +254,14 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
       afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (32 * s + 8 * rgrp) * 2) : V(0);
+    // the dense copy colsum streams (zeros past nq)
+    if (t < ntiles_w) {
+      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wave + 4 * t) * (kQTile * D) + col * D;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) *reinterpret_cast<V*>(dst + 32 * s + 8 * rgrp) = afrag[t][s];
+    }
   }
+  if (g == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
   const int32_t nkb = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
   u32x4 pre[PIECES];
   if (nkb > 0) {
@@ -284,57 +293,92 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
         const float lo = __shfl_xor(ll, off, 64);
         stats_merge(mm, ll, mo, lo);
       }
-      const uint32_t q = q0 + 4 * rgrp + i;
-      if (col == 0 && q < a.nq) a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
+      const uint32_t q = q0 + 4 * rgrp + i;  // rows past nq too: colsum reads whole tiles
+      if (col == 0) a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
     }
   }
 }
 
 // -------------------------------------------------------------- colsum
+//
+// Query units (16-query tile x up to 4 heads of the KV head's group) stream
+// through three LDS buffers filled by global_load_lds_dwordx4 from the dense
+// copy rowstats wrote: one unit is computed while the next has landed and the
+// one after is in flight, with no registers held for it. The DMA requests are
+// inline asm, so the compiler adds no waits of its own for these LDS writes
+// (it would wait for every request in flight before each read, not knowing
+// which buffer a request fills); the kernel waits for them with explicit
+// vmcnt counts, and the barrier is a plain s_barrier (a __syncthreads fence
+// would wait for the request just issued). Vector memory ops complete in
+// order, so the counts the compiler computes for its own loads stay safe.
 
-constexpr int kHeadChunk = 4;  // query heads staged per LDS buffer
+constexpr int kHeadChunk = 4;  // query heads per unit
+constexpr int kQBuffers = 3;   // units in LDS: computed, landed, requested
 
-template <int PIECES, int D>
-__device__ __forceinline__ void load_q_unit(const SqArgs& a, uint32_t g, uint32_t q0, uint32_t h0,
-                                            uint32_t nh, u32x4 (&pre)[PIECES]) {
-#pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    const uint32_t hl = idx / (kQTile * (D / 8));
-    const uint32_t rem = idx % (kQTile * (D / 8));
-    const uint32_t r = rem / (D / 8), piece = rem % (D / 8);
-    pre[p] = u32x4(0);
-    if (hl < nh && q0 + r < a.nq)
-      pre[p] = *reinterpret_cast<const u32x4*>(query_row(a, q0 + r, g * a.groups + h0 + hl, 2) + piece * 16);
-  }
+// Rows of a unit sit in LDS unpadded, D / 8 pieces of 16 bytes per row, piece
+// p of row R at position p ^ swz(R): the 16 lanes that read one piece of 16
+// consecutive rows then hit distinct bank groups.
+template <int D>
+__device__ __forceinline__ uint32_t q_swizzle(uint32_t row) {
+  constexpr uint32_t P = D / 8;
+  return (row / (16 / P)) % P;
 }
 
-template <int PIECES, int D, int LROW>
-__device__ __forceinline__ void store_q_unit(uint16_t* lds, const u32x4 (&pre)[PIECES]) {
-#pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    const uint32_t hl = idx / (kQTile * (D / 8));
-    const uint32_t rem = idx % (kQTile * (D / 8));
-    const uint32_t r = rem / (D / 8), piece = rem % (D / 8);
-    *reinterpret_cast<u32x4*>(&lds[(hl * kQTile + r) * LROW + piece * 8]) = pre[p];
-  }
+// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding)
+#define CBK_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// A wave-uniform 64-bit value in SGPRs (readfirstlane returns a signed int:
+// each half is widened as unsigned).
+__device__ __forceinline__ uint64_t uniform64(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
+  return uint64_t(lo) | (uint64_t(hi) << 32);
+}
+
+// global_load_lds_dword{,x4}: lane l's 4 or 16 bytes at base + off land at
+// LDS address lds + l * size (base and lds wave-uniform). The LDS address
+// goes through M0, which the asm saves and restores. The compiler's hazard
+// checks do not look inside inline asm, so the asm pads for them itself:
+// s_nop 4 gives the 5 wait states a VMEM read of an SGPR needs after a VALU
+// wrote it (the base and M0 come from v_readfirstlane) and the 1 an M0 write
+// needs before an LDS DMA; s_nop 0 separates the DMA from the M0 restore.
+#define CBK_LDS_DMA(op)                                                                           \
+  "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 4\n\t" op " %1, %2\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dwordx4")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dword")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
 }
 
 template <typename V, int KSTEPS, int RMODE, bool MASK>
-__device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2 (*st)[kQTile],
+__device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
                                             uint32_t nh, int32_t kw0, const int32_t (&rpos)[4],
                                             const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
                                             uint32_t col, uint32_t rgrp) {
-  constexpr int LROW = 32 * KSTEPS + 8;
+  constexpr int D = 32 * KSTEPS;
   for (uint32_t hl = 0; hl < nh; ++hl) {
+    const uint32_t row = hl * kQTile + col;
     V afrag[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      afrag[s] = *reinterpret_cast<const V*>(&qlds[(hl * kQTile + col) * LROW + 32 * s + 8 * rgrp]);
+      afrag[s] = *reinterpret_cast<const V*>(&qlds[row * D + ((4 * s + rgrp) ^ q_swizzle<D>(row)) * 8]);
     float mrow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mrow[i] = st[hl][4 * rgrp + i].x;
+    for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
 #pragma unroll
     for (int c = 0; c < kColTiles; ++c) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -356,14 +400,18 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
   }
 }
 
+// three waves per SIMD: the LDS holds three workgroups' buffers
 template <typename V, int KSTEPS, int RMODE>
-__global__ __launch_bounds__(kThreads) void sq_colsum_kernel(const SqArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_colsum_kernel(
+    const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
-  constexpr int LROW = D + 8;
-  constexpr int PIECES = kHeadChunk * kQTile * (D / 8) / kThreads;
-  __shared__ __attribute__((aligned(16))) uint16_t qblk[2][kHeadChunk * kQTile * LROW];
-  __shared__ float2 s_stats[2][kHeadChunk][kQTile];
-  __shared__ int32_t s_pos[2][kQTile];
+  constexpr uint32_t P = D / 8;                   // 16-byte pieces per row
+  constexpr uint32_t kInsts = P / 4;              // Q requests per wave per unit (1 KiB each)
+  constexpr uint32_t kRowsPerInst = 64 / P;
+  constexpr int kQElems = kHeadChunk * kQTile * D;
+  __shared__ __attribute__((aligned(16))) uint16_t qbuf[kQBuffers][kQElems];
+  __shared__ __attribute__((aligned(16))) float2 sbuf[kQBuffers][128];  // 64 used, lanes 32-63 repeat
+  __shared__ __attribute__((aligned(16))) int32_t tbuf[kQBuffers][64];  // tile record, repeated
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t g = blockIdx.y;
   const int32_t kw0 = int32_t(blockIdx.x) * kKeyBlock2 + int32_t(wave) * 16 * kColTiles;
@@ -384,62 +432,84 @@ __global__ __launch_bounds__(kThreads) void sq_colsum_kernel(const SqArgs a) {
   float acc_col[kColTiles];
 #pragma unroll
   for (int c = 0; c < kColTiles; ++c) acc_col[c] = 0.f;
+  // the K fragments have landed before any request is issued (the compiler,
+  // blind to the requests, would otherwise wait for everything in flight
+  // wherever it first needs them)
+  CBK_WAIT_VM_LGKM0(0);
 
-  // units (query tile, head chunk) whose tile sees at least one key of the block
-  const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
+  // Units: tiles from the last down to the lowest tile whose latest query
+  // sees a key of this block (tiles in between that see none skip their
+  // compute), each tile's head chunks in order. Latest tiles first: every key
+  // block sees them, so the workgroups resident together stream the same
+  // units at about the same time and find them in L2.
+  const int32_t ntiles = int32_t((a.nq + kQTile - 1) / kQTile);
   const uint32_t nchunks = (a.groups + kHeadChunk - 1) / kHeadChunk;
-  auto next_tile = [&](uint32_t qt) {
-    while (qt < ntiles && a.tile_pos[2 * qt + 1] < kb0) ++qt;
-    return qt;
-  };
-  uint32_t qt = next_tile(0), hc = 0;
-  u32x4 pre[PIECES];
-  float2 pre_st = make_float2(0.f, 0.f);
-  int32_t pre_pos = -1;
-  auto fetch = [&](uint32_t t, uint32_t c) {
-    const uint32_t h0 = c * kHeadChunk, nh = min(uint32_t(kHeadChunk), a.groups - h0);
-    load_q_unit<PIECES, D>(a, g, t * kQTile, h0, nh, pre);
-    if (threadIdx.x < kHeadChunk * kQTile) {
-      const uint32_t hl = threadIdx.x / kQTile, r = threadIdx.x % kQTile;
-      const uint32_t q = t * kQTile + r;
-      pre_st = (hl < nh && q < a.nq) ? a.stats[int64_t(g * a.groups + h0 + hl) * a.nq_pad + q]
-                                     : make_float2(0.f, 0.f);
+  int32_t tlo = ntiles;
+  for (int32_t t0 = 0; t0 < ntiles; t0 += 64) {
+    const int32_t u = t0 + int32_t(lane);
+    const uint64_t hits = __ballot(u < ntiles && a.tiles[kTileWords * u + kQTile + 1] >= kb0);
+    if (hits) {
+      tlo = t0 + int32_t(__builtin_ctzll(hits));
+      break;
     }
-    if (threadIdx.x < kQTile) pre_pos = query_pos(a, t * kQTile + threadIdx.x);
-  };
-  auto commit = [&](int buf) {
-    store_q_unit<PIECES, D, LROW>(qblk[buf], pre);
-    if (threadIdx.x < kHeadChunk * kQTile) s_stats[buf][threadIdx.x / kQTile][threadIdx.x % kQTile] = pre_st;
-    if (threadIdx.x < kQTile) s_pos[buf][threadIdx.x] = pre_pos;
-  };
-  if (qt < ntiles) {
-    fetch(qt, hc);
-    commit(0);
   }
-  for (int it = 0; qt < ntiles; ++it) {
-    // the unit after (qt, hc)
-    uint32_t nqt = qt, nhc = hc + 1;
-    if (nhc == nchunks) {
-      nhc = 0;
-      nqt = next_tile(qt + 1);
-    }
-    if (nqt < ntiles) fetch(nqt, nhc);  // in flight during the compute below
-    __syncthreads();
-    const int buf = it & 1;
-    const int32_t tmax = a.tile_pos[2 * qt + 1], tmin = a.tile_pos[2 * qt];
-    if (tmax >= kw0) {
-      int32_t rpos[4];
+  const int32_t nunits = (ntiles - tlo) * int32_t(nchunks);
+
+  // Per-lane byte offsets of the requests. A unit's Q rows are contiguous in
+  // the dense copy; rows of heads past the group (a partial last chunk) read
+  // the next rows, never used (the copy is padded by a unit at its end).
+  uint32_t qoff[kInsts];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rpos[i] = s_pos[buf][4 * rgrp + i];
+  for (uint32_t j = 0; j < kInsts; ++j) {
+    const uint32_t row = (wave * kInsts + j) * kRowsPerInst + lane / P;
+    qoff[j] = (row * D + ((lane % P) ^ q_swizzle<D>(row)) * 8) * 2;
+  }
+  const uint32_t toff = (lane % kTileWords) * 4;
+  // Issues unit i (clamped: a request past the end repeats the last unit, so
+  // every iteration issues the same number of requests) into buffer b: the
+  // Q rows, and on wave 0 the row statistics and the tile record.
+  auto request = [&](int32_t i, int b) {
+    i = min(i, nunits - 1);
+    const uint32_t qt = uint32_t(ntiles - 1 - i / int32_t(nchunks)), hc = uint32_t(i) % nchunks;
+    const uint16_t* unit = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + hc * kHeadChunk) * (kQTile * D);
+    const uint32_t lq = lds_address(qbuf[b]);
+#pragma unroll
+    for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(unit, qoff[j], lq + (wave * kInsts + j) * 1024);
+    if (wave == 0) {
       const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
-      if (kw0 + 16 * kColTiles - 1 > tmin || qt * kQTile + kQTile > a.nq)
-        colsum_unit<V, KSTEPS, RMODE, true>(a, qblk[buf], s_stats[buf], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
-      else
-        colsum_unit<V, KSTEPS, RMODE, false>(a, qblk[buf], s_stats[buf], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+      const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // 8 lanes (128 bytes) per head
+      const float2* st = a.stats + int64_t(g * a.groups + hc * kHeadChunk) * a.nq_pad + qt * kQTile;
+      lds_dma16(st, (hl * a.nq_pad + (lane % 8) * 2) * 8, lds_address(sbuf[b]));
+      lds_dma4(a.tiles + kTileWords * qt, toff, lds_address(tbuf[b]));
     }
-    if (nqt < ntiles) commit(buf ^ 1);
-    qt = nqt;
-    hc = nhc;
+  };
+  if (nunits > 0) {
+    request(0, 0);
+    request(1, 1);
+    for (int32_t it = 0; it < nunits; ++it) {
+      // unit it has landed once at most the newest unit's requests are pending
+      if (wave == 0)
+        CBK_WAIT_VM_LGKM0(kInsts + 2);
+      else
+        CBK_WAIT_VM_LGKM0(kInsts);
+      asm volatile("s_barrier" ::: "memory");
+      request(it + 2, (it + 2) % kQBuffers);  // into the buffer computed one unit ago
+      const int b = it % kQBuffers;
+      const int32_t qt = ntiles - 1 - it / int32_t(nchunks);
+      const uint32_t hc = uint32_t(it) % nchunks;
+      const int32_t tmin = tbuf[b][kQTile], tmax = tbuf[b][kQTile + 1];
+      if (tmax >= kw0) {
+        int32_t rpos[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rpos[i] = tbuf[b][4 * rgrp + i];
+        const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
+        if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt) * kQTile + kQTile > a.nq)
+          colsum_unit<V, KSTEPS, RMODE, true>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+        else
+          colsum_unit<V, KSTEPS, RMODE, false>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+      }
+    }
+    CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends
   }
   // column totals: the 4 lane groups hold the same column
 #pragma unroll
@@ -525,9 +595,12 @@ __global__ void sq_zero_kernel(float* p, uint64_t n) {
     p[i] = 0.f;
 }
 
+// Largest head_dim of the MFMA path: the dense query copy is sized for it.
+constexpr int64_t kMaxHeadDim = 128;
+
 struct SqLayout {
   uint32_t nq_pad, ntiles;
-  uint64_t stats, tile_pos, partial, bytes;  // byte offsets
+  uint64_t stats, tiles, partial, qdense, bytes;  // byte offsets
 };
 
 __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
@@ -535,9 +608,11 @@ __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   L.ntiles = uint32_t((nq + kQTile - 1) / kQTile);
   L.nq_pad = L.ntiles * kQTile;
   L.stats = 0;
-  L.tile_pos = (L.stats + uint64_t(hq) * L.nq_pad * 8 + 255) & ~uint64_t(255);
-  L.partial = (L.tile_pos + uint64_t(L.ntiles) * 8 + 255) & ~uint64_t(255);
-  L.bytes = (L.partial + uint64_t(hkv) * nk * 4 + 255) & ~uint64_t(255);
+  L.tiles = (L.stats + uint64_t(hq) * L.nq_pad * 8 + 255) & ~uint64_t(255);
+  L.partial = (L.tiles + uint64_t(L.ntiles) * kTileWords * 4 + 255) & ~uint64_t(255);
+  L.qdense = (L.partial + uint64_t(hkv) * nk * 4 + 255) & ~uint64_t(255);
+  // padded by one unit: a partial head chunk's requests read past its group
+  L.bytes = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
   return L;
 }
 
@@ -618,8 +693,9 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
   a.c2 = scale * kLog2e;
   a.round_mode = round_logits;
   a.stats = reinterpret_cast<float2*>(ws + L.stats);
-  a.tile_pos = reinterpret_cast<int32_t*>(ws + L.tile_pos);
+  a.tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
   a.partial = reinterpret_cast<float*>(ws + L.partial);
+  a.qdense = reinterpret_cast<uint16_t*>(ws + L.qdense);
   a.nq_pad = L.nq_pad;
   if (nq == 0) {
     const uint64_t n = uint64_t(hkv) * nk;
@@ -642,6 +718,8 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
                 "the MFMA path rounds logits to the input dtype (round_logits %d)",
                 dtype == CBK_DTYPE_BF16 ? 1 : 2);
     CBK_REQUIRE(scale > 0.f, "scale must be positive");
+    // colsum's per-lane 32-bit DMA offsets span 4 rows of the statistics
+    CBK_REQUIRE(nq <= (int64_t(1) << 26), "the MFMA path takes at most 2^26 queries, got %lld", (long long)nq);
     const int ks = int(head_dim / 32);
     int rc = dtype == CBK_DTYPE_BF16 ? launch_mfma<s16x8, 1>(a, ks, s) : launch_mfma<h16x8, 2>(a, ks, s);
     if (rc) return rc;
