@@ -121,31 +121,59 @@ __device__ __forceinline__ void round_pair(float& x, float& y) {
   }
 }
 
+// ------------------------------------------------------ LDS DMA helpers
+
+// Tiles that the DMA below fills (K blocks in rowstats, query units in
+// colsum) sit in LDS unpadded, D / 8 pieces of 16 bytes per row, piece p of
+// row R at position p ^ swz(R): the 16 lanes that read one piece of 16
+// consecutive rows then hit distinct bank groups.
+template <int D>
+__device__ __forceinline__ uint32_t q_swizzle(uint32_t row) {
+  constexpr uint32_t P = D / 8;
+  return (row / (16 / P)) % P;
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding)
+#define CBK_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// A wave-uniform 64-bit value in SGPRs (readfirstlane returns a signed int:
+// each half is widened as unsigned).
+__device__ __forceinline__ uint64_t uniform64(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
+  return uint64_t(lo) | (uint64_t(hi) << 32);
+}
+
+// global_load_lds_dword{,x4}: lane l's 4 or 16 bytes at base + off land at
+// LDS address lds + l * size (base and lds wave-uniform). The LDS address
+// goes through M0, which the asm saves and restores. The compiler's hazard
+// checks do not look inside inline asm, so the asm pads for them itself:
+// s_nop 4 gives the 5 wait states a VMEM read of an SGPR needs after a VALU
+// wrote it (the base and M0 come from v_readfirstlane) and the 1 an M0 write
+// needs before an LDS DMA; s_nop 0 separates the DMA from the M0 restore.
+#define CBK_LDS_DMA(op)                                                                           \
+  "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 4\n\t" op " %1, %2\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dwordx4")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dword")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
+}
+
 // ------------------------------------------------------------ rowstats
-
-template <int PIECES, int D>
-__device__ __forceinline__ void load_key_block(const SqArgs& a, uint32_t g, int32_t k0, u32x4 (&pre)[PIECES]) {
-#pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    const uint32_t kr = idx / (D / 8), piece = idx % (D / 8);
-    const int32_t key = k0 + int32_t(kr);
-    pre[p] = u32x4(0);
-    if (key < int32_t(a.nk))
-      pre[p] = *reinterpret_cast<const u32x4*>(
-          a.k + ((int64_t(key) * a.k_stride) + int64_t(g) * a.d + piece * 8) * 2);
-  }
-}
-
-template <int PIECES, int D, int LROW>
-__device__ __forceinline__ void store_block(uint16_t* lds, const u32x4 (&pre)[PIECES]) {
-#pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    const uint32_t kr = idx / (D / 8), piece = idx % (D / 8);
-    *reinterpret_cast<u32x4*>(&lds[kr * LROW + piece * 8]) = pre[p];
-  }
-}
 
 // One 64-key block against MAXT row tiles: MFMA, round, (mask), online stats.
 template <typename V, int KSTEPS, int MAXT, int RMODE, bool MASK>
@@ -153,13 +181,15 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
                                                const V (&afrag)[MAXT][KSTEPS], int ntiles_w,
                                                const int32_t (&rpos)[4], float (&m)[MAXT][4],
                                                float (&l)[MAXT][4], uint32_t col, uint32_t rgrp) {
-  constexpr int LROW = 32 * KSTEPS + 8;
+  constexpr int D = 32 * KSTEPS;
   V bfrag[kColTiles][KSTEPS];
 #pragma unroll
-  for (int c = 0; c < kColTiles; ++c)
+  for (int c = 0; c < kColTiles; ++c) {
+    const uint32_t row = c * 16 + col;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      bfrag[c][s] = *reinterpret_cast<const V*>(&blk[(c * 16 + col) * LROW + 32 * s + 8 * rgrp]);
+      bfrag[c][s] = *reinterpret_cast<const V*>(&blk[row * D + ((4 * s + rgrp) ^ q_swizzle<D>(row)) * 8]);
+  }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     if (t >= ntiles_w) break;
@@ -204,12 +234,16 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
   }
 }
 
+// K blocks of 64 keys stream through three LDS buffers by DMA, as the query
+// units do in colsum (see there for the wait and barrier scheme).
 template <typename V, int KSTEPS, int MAXT, int RMODE>
 __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
-  constexpr int LROW = D + 8;  // padded LDS row (elements) against bank conflicts
-  constexpr int PIECES = kKeyBlock1 * (D / 8) / kThreads;
-  __shared__ __attribute__((aligned(16))) uint16_t kblk[2][kKeyBlock1 * LROW];
+  constexpr uint32_t P = D / 8;                   // 16-byte pieces per key row
+  constexpr uint32_t kInsts = P / 4;              // requests per wave per block (1 KiB each)
+  constexpr uint32_t kRowsPerInst = 64 / P;
+  constexpr int kBuffers = 3;
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[kBuffers][kKeyBlock1 * D];
   __shared__ int32_t s_pos[kQTile];
   __shared__ int32_t s_minmax[2];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -262,22 +296,53 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
     }
   }
   if (g == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
+  // nothing of the compiler's own in flight once the requests start
+  CBK_WAIT_VM_LGKM0(0);
+
   const int32_t nkb = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
-  u32x4 pre[PIECES];
-  if (nkb > 0) {
-    load_key_block<PIECES, D>(a, g, 0, pre);
-    store_block<PIECES, D, LROW>(kblk[0], pre);
+  // per-lane byte offsets of a block's requests (key row, swizzled piece)
+  uint32_t koff[kInsts];
+  uint32_t krow[kInsts];
+#pragma unroll
+  for (uint32_t j = 0; j < kInsts; ++j) {
+    krow[j] = (wave * kInsts + j) * kRowsPerInst + lane / P;
+    const uint32_t piece = (lane % P) ^ q_swizzle<D>(krow[j]);
+    koff[j] = (krow[j] * a.k_stride + g * a.d + piece * 8) * 2;
   }
-  for (int32_t kb = 0; kb < nkb; ++kb) {
+  // block kb (clamped: a request past the end repeats the last block) into buffer b;
+  // rows past nk of the last block read its last key (masked)
+  auto request = [&](int32_t kb, int b) {
+    kb = min(kb, nkb - 1);
     const int32_t k0 = kb * kKeyBlock1;
-    if (kb + 1 < nkb) load_key_block<PIECES, D>(a, g, k0 + kKeyBlock1, pre);  // in flight
-    __syncthreads();
-    const uint16_t* blk = kblk[kb & 1];
-    if (k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk))
-      rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-    else
-      rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-    if (kb + 1 < nkb) store_block<PIECES, D, LROW>(kblk[(kb + 1) & 1], pre);
+    const char* base = a.k + int64_t(k0) * a.k_stride * 2;
+    const uint32_t lk = lds_address(kbuf[b]);
+    if (k0 + kKeyBlock1 <= int32_t(a.nk)) {
+#pragma unroll
+      for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(base, koff[j], lk + (wave * kInsts + j) * 1024);
+    } else {
+      const uint32_t last = uint32_t(int32_t(a.nk) - 1 - k0);
+#pragma unroll
+      for (uint32_t j = 0; j < kInsts; ++j) {
+        const uint32_t r = min(krow[j], last);
+        lds_dma16(base, koff[j] - (krow[j] - r) * a.k_stride * 2, lk + (wave * kInsts + j) * 1024);
+      }
+    }
+  };
+  if (nkb > 0) {
+    request(0, 0);
+    request(1, 1);
+    for (int32_t kb = 0; kb < nkb; ++kb) {
+      CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
+      asm volatile("s_barrier" ::: "memory");
+      request(kb + 2, (kb + 2) % kBuffers);  // into the buffer computed one block ago
+      const int32_t k0 = kb * kKeyBlock1;
+      const uint16_t* blk = kbuf[kb % kBuffers];
+      if (k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk))
+        rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+      else
+        rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+    }
+    CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends
   }
   // merge the 16 lanes that hold the same rows, then publish m2 + log2(l)
 #pragma unroll
@@ -314,55 +379,6 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 
 constexpr int kHeadChunk = 4;  // query heads per unit
 constexpr int kQBuffers = 3;   // units in LDS: computed, landed, requested
-
-// Rows of a unit sit in LDS unpadded, D / 8 pieces of 16 bytes per row, piece
-// p of row R at position p ^ swz(R): the 16 lanes that read one piece of 16
-// consecutive rows then hit distinct bank groups.
-template <int D>
-__device__ __forceinline__ uint32_t q_swizzle(uint32_t row) {
-  constexpr uint32_t P = D / 8;
-  return (row / (16 / P)) % P;
-}
-
-// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding)
-#define CBK_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
-
-// A wave-uniform 64-bit value in SGPRs (readfirstlane returns a signed int:
-// each half is widened as unsigned).
-__device__ __forceinline__ uint64_t uniform64(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
-  return uint64_t(lo) | (uint64_t(hi) << 32);
-}
-
-// global_load_lds_dword{,x4}: lane l's 4 or 16 bytes at base + off land at
-// LDS address lds + l * size (base and lds wave-uniform). The LDS address
-// goes through M0, which the asm saves and restores. The compiler's hazard
-// checks do not look inside inline asm, so the asm pads for them itself:
-// s_nop 4 gives the 5 wait states a VMEM read of an SGPR needs after a VALU
-// wrote it (the base and M0 come from v_readfirstlane) and the 1 an M0 write
-// needs before an LDS DMA; s_nop 0 separates the DMA from the M0 restore.
-#define CBK_LDS_DMA(op)                                                                           \
-  "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 4\n\t" op " %1, %2\n\ts_nop 0\n\ts_mov_b32 m0, %0"
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(CBK_LDS_DMA("global_load_lds_dwordx4")
-               : "=&s"(saved)
-               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
-               : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(CBK_LDS_DMA("global_load_lds_dword")
-               : "=&s"(saved)
-               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
-               : "memory");
-}
 
 template <typename V, int KSTEPS, int RMODE, bool MASK>
 __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
@@ -718,8 +734,10 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
                 "the MFMA path rounds logits to the input dtype (round_logits %d)",
                 dtype == CBK_DTYPE_BF16 ? 1 : 2);
     CBK_REQUIRE(scale > 0.f, "scale must be positive");
-    // colsum's per-lane 32-bit DMA offsets span 4 rows of the statistics
+    // the DMA requests' per-lane 32-bit offsets span 64 key rows and 4 rows
+    // of the statistics
     CBK_REQUIRE(nq <= (int64_t(1) << 26), "the MFMA path takes at most 2^26 queries, got %lld", (long long)nq);
+    CBK_REQUIRE(k_row_stride_elems < (int64_t(1) << 24), "the MFMA path takes K row strides below 2^24 elements");
     const int ks = int(head_dim / 32);
     int rc = dtype == CBK_DTYPE_BF16 ? launch_mfma<s16x8, 1>(a, ks, s) : launch_mfma<h16x8, 2>(a, ks, s);
     if (rc) return rc;
