@@ -17,10 +17,10 @@
 //                   over its 4 lane groups (two xor shuffles)
 //   O += P . V      v_mfma_f32_16x16x16_{bf16,f16}: the S^T registers are
 //                   exactly the A operand (row lane%16, keys 4*(lane/16)..+3);
-//                   B needs 4 consecutive keys of one dim, so V is staged
-//                   transposed in LDS ([dim][key], key pairs per 32-bit word)
-// K/V blocks are double-buffered through LDS with a register prefetch; the
-// row tiles with the latest positions (most keys) are scheduled first.
+//                   B needs 4 consecutive keys of one dim, which
+//                   ds_read_tr16_b64 gathers from the row-major V block
+// K/V blocks stream through three LDS buffers each by DMA (global_load_lds);
+// the row tiles with the latest positions (most keys) are scheduled first.
 // MFMA layouts (checked on gfx950): 16x16x32 A[i][k] in lane i+16*(k/8)
 // element k%8, B[k][j] in lane j+16*(k/8); 16x16x16 A[i][k] in lane
 // i+16*(k/4) element k%4, B[k][j] in lane j+16*(k/4); D[i][j] in lane
@@ -48,7 +48,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kRowTiles = 1;  // 16-row tiles per wave (2 needs ~290 registers: one wave per SIMD, slower)
 constexpr int kKeyBlock = 32;
-constexpr int kVtWords = 18;  // words per transposed V row (32 keys + 4 pad), conflict-free stores
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kRescale = 8.f;  // log2 headroom of the lazy softmax rescaling
@@ -112,98 +111,16 @@ __device__ __forceinline__ void round2(float& x, float& y) {
   y = Ops<F16>::hi(u);
 }
 
-template <int D>
-struct KvRegs {
-  static constexpr int KPIECES = kKeyBlock * (D / 8) / kThreads;  // 16-byte K pieces per thread
-  static constexpr int VJOBS = 16 * (D / 8);                     // (key pair, dim chunk) jobs
-  u32x4 k[KPIECES];
-  u32x4 v0, v1;
-};
-
-// This thread's K/V sources for key block 0; advanced by one block per call.
-template <int D>
-struct KvSrc {
-  const uint16_t* k[KvRegs<D>::KPIECES];
-  const uint16_t* v0;
-  int32_t kkey[KvRegs<D>::KPIECES];
-  int32_t vkey;
-};
-
-template <int D>
-__device__ __forceinline__ void init_kv_src(const AttnArgs& a, uint32_t kvh, KvSrc<D>& src) {
-#pragma unroll
-  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    src.kkey[p] = int32_t(idx / (D / 8));
-    src.k[p] = a.k + int64_t(src.kkey[p]) * a.k_stride + int64_t(kvh) * D + (idx % (D / 8)) * 8;
-  }
-  const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
-  src.vkey = int32_t(2 * kp);
-  src.v0 = a.v + int64_t(src.vkey) * a.v_stride + int64_t(kvh) * D + dc * 8;
-}
-
-// Loads key block k0 (= b * kKeyBlock) into registers; blocks entirely inside
-// the context load without per-key checks, the last one zero-fills.
-template <int D, bool EDGE>
-__device__ __forceinline__ void load_kv_block(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
-  const int32_t k0 = b * kKeyBlock;
-  const int64_t koff = int64_t(k0) * a.k_stride, voff = int64_t(k0) * a.v_stride;
-  constexpr bool inside = !EDGE;
-#pragma unroll
-  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
-    r.k[p] = u32x4(0u);
-    if (inside || k0 + src.kkey[p] < int32_t(a.nk)) r.k[p] = *reinterpret_cast<const u32x4*>(src.k[p] + koff);
-  }
-  r.v0 = u32x4(0u);
-  r.v1 = u32x4(0u);
-  if (threadIdx.x < uint32_t(KvRegs<D>::VJOBS)) {
-    const int32_t key = k0 + src.vkey;
-    if (inside || key < int32_t(a.nk)) r.v0 = *reinterpret_cast<const u32x4*>(src.v0 + voff);
-    if (inside || key + 1 < int32_t(a.nk)) r.v1 = *reinterpret_cast<const u32x4*>(src.v0 + voff + a.v_stride);
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void load_kv(const AttnArgs& a, const KvSrc<D>& src, int32_t b, KvRegs<D>& r) {
-  if ((b + 1) * kKeyBlock <= int32_t(a.nk))  // uniform: k0 and nk are scalars
-    load_kv_block<D, false>(a, src, b, r);
-  else
-    load_kv_block<D, true>(a, src, b, r);
-}
-
-// K rows [32][D + 8] (padded); V transposed as words [D][kVtWords], word
-// (dim, kp) = {V[2kp][dim], V[2kp+1][dim]}.
-template <int D>
-__device__ __forceinline__ void store_kv(uint16_t* ks, uint32_t* vt, const KvRegs<D>& r) {
-  constexpr int LK = D + 8;
-#pragma unroll
-  for (int p = 0; p < KvRegs<D>::KPIECES; ++p) {
-    const uint32_t idx = threadIdx.x + p * kThreads;
-    *reinterpret_cast<u32x4*>(&ks[(idx / (D / 8)) * LK + (idx % (D / 8)) * 8]) = r.k[p];
-  }
-  if (threadIdx.x < uint32_t(KvRegs<D>::VJOBS)) {
-    const uint32_t kp = threadIdx.x % 16, dc = threadIdx.x / 16;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t a0 = r.v0[w], a1 = r.v1[w];  // dims 8dc+2w (low), 8dc+2w+1 (high)
-      // v_perm_b32: {a0.lo16, a1.lo16} and {a0.hi16, a1.hi16}
-      vt[(dc * 8 + 2 * w) * kVtWords + kp] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-      vt[(dc * 8 + 2 * w + 1) * kVtWords + kp] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-    }
-  }
-}
-
 // bf16 / f16 1.0 in both halves of a word: the B operand of the "ones"
 // column whose MFMA accumulates each row's sum of (rounded) probabilities
 template <bool F16> constexpr uint32_t kOnesPair = F16 ? 0x3c003c00u : 0x3f803f80u;
 
 template <bool F16, int D, int RT, bool MASK>
-__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t* vt, int32_t k0, float scale,
+__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t* vs, int32_t k0, float scale,
                                              const typename Ops<F16>::A8 (&qf)[RT][D / 32],
                                              const int32_t (&rpos)[RT], float (&m)[RT],
                                              f32x4 (&o)[RT][D / 16], f32x4 (&ol)[RT], uint32_t lane) {
   using O = Ops<F16>;
-  constexpr int LK = D + 8;
   const uint32_t row = lane & 15, grp = lane >> 4;
   // S^T = K . Q^T for every row tile; each K fragment is read from LDS once
   f32x4 s[RT][2];
@@ -213,8 +130,9 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int st = 0; st < D / 32; ++st) {
-      const typename O::A8 kf =
-          *reinterpret_cast<const typename O::A8*>(&ks[(16 * h + row) * LK + 32 * st + 8 * grp]);
+      const uint32_t key = 16 * h + row;
+      const typename O::A8 kf = *reinterpret_cast<const typename O::A8*>(
+          &ks[key * D + ((4 * st + grp) ^ lds_swizzle<D>(key)) * 8]);
 #pragma unroll
       for (int t = 0; t < RT; ++t) s[t][h] = O::mma32(kf, qf[t][st], s[t][h]);
     }
@@ -283,9 +201,17 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
   const typename O::A4 ones = __builtin_bit_cast(typename O::A4, u32x2{kOnesPair<F16>, kOnesPair<F16>});
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    // lane (row, grp) addresses key 16h + 4 grp + row / 4, dims 16c + 4 (row % 4) .. + 3 of
+    // the row-major V block; ds_read_tr16_b64 hands lane j of each 16-lane group element i of
+    // its group's lane 4i + j / 4, i.e. V[16h + 4 grp + i][16c + j]: the 16x16x16 B fragment
+    const uint32_t vkey = 16 * h + 4 * grp + (row >> 2);
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      const u32x2 w = *reinterpret_cast<const u32x2*>(&vt[(16 * c + row) * kVtWords + 8 * h + 2 * grp]);
+      const uint32_t dim = 16 * c + 4 * (row & 3);
+      const uint16_t* vp = &vs[vkey * D + (((dim / 8) ^ lds_swizzle<D>(vkey)) * 8) + (dim & 4)];
+      typedef short s16x4v __attribute__((ext_vector_type(4)));
+      const s16x4v w = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4v*)((__attribute__((address_space(3))) const void*)vp));
       const typename O::A4 vb = __builtin_bit_cast(typename O::A4, w);
 #pragma unroll
       for (int t = 0; t < RT; ++t) o[t][c] = O::mma16(pa[t][h], vb, o[t][c]);
@@ -295,12 +221,18 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint32_t*
   }
 }
 
+// K and V blocks of 32 keys stream through three LDS buffers each by DMA
+// (global_load_lds, explicit vmcnt waits, plain s_barrier; see the LDS DMA
+// helpers): the block computed, the next (landed), the one after (in flight).
 template <bool F16, int D, int RT>
 __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
-  constexpr int LK = D + 8;
   constexpr int kRows = 4 * 16 * RT;  // rows per workgroup
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeyBlock * LK];
-  __shared__ __attribute__((aligned(16))) uint32_t vt[2][D * kVtWords];
+  constexpr uint32_t P = D / 8;                      // 16-byte pieces per key row
+  constexpr uint32_t kInsts = kKeyBlock * P / 64 / 4; // requests per wave per block, each of K and V
+  constexpr uint32_t kRowsPerInst = 64 / P;
+  constexpr int kBuffers = 3;
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[kBuffers][kKeyBlock * D];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[kBuffers][kKeyBlock * D];
   __shared__ int32_t s_max[4];
   using O = Ops<F16>;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -341,7 +273,9 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   __syncthreads();
   // workgroup-uniform: a scalar loop bound
   const int32_t gmax = __builtin_amdgcn_readfirstlane(max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
-  const int32_t nblocks = gmax < 0 ? 0 : (gmax + kKeyBlock) / kKeyBlock;
+  // blocks up to the latest position, within the context
+  const int32_t nblocks =
+      gmax < 0 ? 0 : min((gmax + kKeyBlock) / kKeyBlock, (int32_t(a.nk) + kKeyBlock - 1) / kKeyBlock);
 
   float m[RT];
   f32x4 o[RT][D / 16], ol[RT];
@@ -352,32 +286,57 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) o[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  // nothing of the compiler's own in flight once the requests start
+  CBK_WAIT_VM_LGKM0(0);
 
-  KvRegs<D> pre;
-  KvSrc<D> src;
-  init_kv_src<D>(a, kvh, src);
-  if (nblocks > 0) {
-    load_kv<D>(a, src, 0, pre);
-    store_kv<D>(ks[0], vt[0], pre);
+  // per-lane request offsets (key row of the block, swizzled piece), bytes
+  uint32_t krow[kInsts], koff[kInsts], voff[kInsts];
+#pragma unroll
+  for (uint32_t j = 0; j < kInsts; ++j) {
+    krow[j] = (wave * kInsts + j) * kRowsPerInst + lane / P;
+    const uint32_t piece = (lane % P) ^ lds_swizzle<D>(krow[j]);
+    koff[j] = uint32_t((krow[j] * a.k_stride + kvh * D + piece * 8) * 2);
+    voff[j] = uint32_t((krow[j] * a.v_stride + kvh * D + piece * 8) * 2);
   }
-  __syncthreads();
-  for (int32_t b = 0; b < nblocks; ++b) {
+  // block b (clamped: a request past the end repeats the last block) into
+  // buffer buf; rows past nk of the last block repeat its last key (masked)
+  auto request = [&](int32_t b, int buf) {
+    b = min(b, nblocks - 1);
     const int32_t k0 = b * kKeyBlock;
-    const int buf = b & 1;
-    if (b + 1 < nblocks) load_kv<D>(a, src, b + 1, pre);
-    if (k0 <= wmax) {
-      if (k0 + kKeyBlock - 1 > wmin)
-        attend_block<F16, D, RT, true>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
-      else
-        attend_block<F16, D, RT, false>(ks[buf], vt[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
+    const uint16_t* kb = a.k + int64_t(k0) * a.k_stride;
+    const uint16_t* vb = a.v + int64_t(k0) * a.v_stride;
+    const uint32_t lk = lds_address(kbuf[buf]), lv = lds_address(vbuf[buf]);
+    const uint32_t last = uint32_t(min(int32_t(a.nk) - 1 - k0, kKeyBlock - 1));
+#pragma unroll
+    for (uint32_t j = 0; j < kInsts; ++j) {
+      const uint32_t back = krow[j] - min(krow[j], last);  // rows to step back past nk
+      lds_dma16(kb, koff[j] - uint32_t(back * a.k_stride * 2), lk + (wave * kInsts + j) * 1024);
+      lds_dma16(vb, voff[j] - uint32_t(back * a.v_stride * 2), lv + (wave * kInsts + j) * 1024);
     }
-    if (b + 1 < nblocks) store_kv<D>(ks[buf ^ 1], vt[buf ^ 1], pre);
-    __syncthreads();
+  };
+  if (nblocks > 0) {
+    request(0, 0);
+    request(1, 1);
+    for (int32_t b = 0; b < nblocks; ++b) {
+      CBK_WAIT_VM_LGKM0(2 * kInsts);  // block b has landed; the newest block may be pending
+      asm volatile("s_barrier" ::: "memory");
+      request(b + 2, (b + 2) % kBuffers);  // into the buffers computed one block ago
+      const int32_t k0 = b * kKeyBlock;
+      const int buf = b % kBuffers;
+      if (k0 <= wmax) {
+        if (k0 + kKeyBlock - 1 > wmin)
+          attend_block<F16, D, RT, true>(kbuf[buf], vbuf[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
+        else
+          attend_block<F16, D, RT, false>(kbuf[buf], vbuf[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
+      }
+    }
+    CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight past this point
   }
+  __syncthreads();  // every wave is done with the K buffers the output staging reuses
 
   // normalize and write, one row tile at a time through the wave's LDS
   // staging area (the K buffers are free now): whole 16-byte pieces per row
-  uint16_t* os = &ks[0][0] + wave * 16 * D;
+  uint16_t* os = &kbuf[0][0] + wave * 16 * D;
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     // row sums of the rounded probabilities, already in O's layout
@@ -506,6 +465,9 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
                             int64_t(reinterpret_cast<uintptr_t>(q_dev)), int64_t(reinterpret_cast<uintptr_t>(k_dev)),
                             int64_t(reinterpret_cast<uintptr_t>(v_dev)), int64_t(reinterpret_cast<uintptr_t>(out_dev))};
   CBK_REQUIRE(common_vec_bytes(align, 8) == 16, "q/k/v/out pointers and row strides must be 16-byte aligned");
+  // the K/V requests' per-lane 32-bit byte offsets span a 32-key block
+  CBK_REQUIRE(k_row_stride_elems < (int64_t(1) << 24) && v_row_stride_elems < (int64_t(1) << 24),
+              "K/V row strides must stay below 2^24 elements");
   AttnArgs a;
   a.q = static_cast<const uint16_t*>(q_dev);
   a.pos = q_pos_dev;

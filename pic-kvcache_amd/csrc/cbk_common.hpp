@@ -66,6 +66,58 @@ __host__ inline int common_vec_bytes(const int64_t* values, int count) {
   return vec;
 }
 
+// ------------------------------------------- LDS DMA (global_load_lds)
+
+// Tiles that the DMA below fills sit in LDS unpadded, D / 8 pieces of 16
+// bytes per row of D 16-bit elements, piece p of row R at position
+// p ^ swz(R): the 16 lanes that read one piece of 16 consecutive rows then
+// hit distinct bank groups.
+template <int D>
+__device__ __forceinline__ uint32_t lds_swizzle(uint32_t row) {
+  constexpr uint32_t P = D / 8;
+  return (row / (16 / P)) % P;
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding)
+#define CBK_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+
+// A wave-uniform 64-bit value in SGPRs (readfirstlane returns a signed int:
+// each half is widened as unsigned).
+__device__ __forceinline__ uint64_t uniform64(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
+  return uint64_t(lo) | (uint64_t(hi) << 32);
+}
+
+// global_load_lds_dword{,x4}: lane l's 4 or 16 bytes at base + off land at
+// LDS address lds + l * size (base and lds wave-uniform). The LDS address
+// goes through M0, which the asm saves and restores. The compiler's hazard
+// checks do not look inside inline asm, so the asm pads for them itself:
+// s_nop 4 gives the 5 wait states a VMEM read of an SGPR needs after a VALU
+// wrote it (the base and M0 come from v_readfirstlane) and the 1 an M0 write
+// needs before an LDS DMA; s_nop 0 separates the DMA from the M0 restore.
+#define CBK_LDS_DMA(op)                                                                           \
+  "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 4\n\t" op " %1, %2\n\ts_nop 0\n\ts_mov_b32 m0, %0"
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dwordx4")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(CBK_LDS_DMA("global_load_lds_dword")
+               : "=&s"(saved)
+               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
+               : "memory");
+}
+
 // ------------------------------------------------------- reductions
 
 __device__ __forceinline__ float wave_sum(float v) {

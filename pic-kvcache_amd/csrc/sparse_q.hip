@@ -121,58 +121,6 @@ __device__ __forceinline__ void round_pair(float& x, float& y) {
   }
 }
 
-// ------------------------------------------------------ LDS DMA helpers
-
-// Tiles that the DMA below fills (K blocks in rowstats, query units in
-// colsum) sit in LDS unpadded, D / 8 pieces of 16 bytes per row, piece p of
-// row R at position p ^ swz(R): the 16 lanes that read one piece of 16
-// consecutive rows then hit distinct bank groups.
-template <int D>
-__device__ __forceinline__ uint32_t q_swizzle(uint32_t row) {
-  constexpr uint32_t P = D / 8;
-  return (row / (16 / P)) % P;
-}
-
-// s_waitcnt vmcnt(n) lgkmcnt(0), expcnt untouched (gfx9 encoding)
-#define CBK_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (((n) >> 4) << 14))
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
-}
-
-// A wave-uniform 64-bit value in SGPRs (readfirstlane returns a signed int:
-// each half is widened as unsigned).
-__device__ __forceinline__ uint64_t uniform64(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
-  return uint64_t(lo) | (uint64_t(hi) << 32);
-}
-
-// global_load_lds_dword{,x4}: lane l's 4 or 16 bytes at base + off land at
-// LDS address lds + l * size (base and lds wave-uniform). The LDS address
-// goes through M0, which the asm saves and restores. The compiler's hazard
-// checks do not look inside inline asm, so the asm pads for them itself:
-// s_nop 4 gives the 5 wait states a VMEM read of an SGPR needs after a VALU
-// wrote it (the base and M0 come from v_readfirstlane) and the 1 an M0 write
-// needs before an LDS DMA; s_nop 0 separates the DMA from the M0 restore.
-#define CBK_LDS_DMA(op)                                                                           \
-  "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 4\n\t" op " %1, %2\n\ts_nop 0\n\ts_mov_b32 m0, %0"
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(CBK_LDS_DMA("global_load_lds_dwordx4")
-               : "=&s"(saved)
-               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
-               : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(CBK_LDS_DMA("global_load_lds_dword")
-               : "=&s"(saved)
-               : "v"(off), "s"(uniform64(base)), "s"(__builtin_amdgcn_readfirstlane(int(lds)))
-               : "memory");
-}
-
 // ------------------------------------------------------------ rowstats
 
 // One 64-key block against MAXT row tiles: MFMA, round, (mask), online stats.
@@ -188,7 +136,7 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
     const uint32_t row = c * 16 + col;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      bfrag[c][s] = *reinterpret_cast<const V*>(&blk[row * D + ((4 * s + rgrp) ^ q_swizzle<D>(row)) * 8]);
+      bfrag[c][s] = *reinterpret_cast<const V*>(&blk[row * D + ((4 * s + rgrp) ^ lds_swizzle<D>(row)) * 8]);
   }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
@@ -306,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 #pragma unroll
   for (uint32_t j = 0; j < kInsts; ++j) {
     krow[j] = (wave * kInsts + j) * kRowsPerInst + lane / P;
-    const uint32_t piece = (lane % P) ^ q_swizzle<D>(krow[j]);
+    const uint32_t piece = (lane % P) ^ lds_swizzle<D>(krow[j]);
     koff[j] = (krow[j] * a.k_stride + g * a.d + piece * 8) * 2;
   }
   // block kb (clamped: a request past the end repeats the last block) into buffer b;
@@ -391,7 +339,7 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
     V afrag[KSTEPS];
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      afrag[s] = *reinterpret_cast<const V*>(&qlds[row * D + ((4 * s + rgrp) ^ q_swizzle<D>(row)) * 8]);
+      afrag[s] = *reinterpret_cast<const V*>(&qlds[row * D + ((4 * s + rgrp) ^ lds_swizzle<D>(row)) * 8]);
     float mrow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
@@ -478,7 +426,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 #pragma unroll
   for (uint32_t j = 0; j < kInsts; ++j) {
     const uint32_t row = (wave * kInsts + j) * kRowsPerInst + lane / P;
-    qoff[j] = (row * D + ((lane % P) ^ q_swizzle<D>(row)) * 8) * 2;
+    qoff[j] = (row * D + ((lane % P) ^ lds_swizzle<D>(row)) * 8) * 2;
   }
   const uint32_t toff = (lane % kTileWords) * 4;
   // Issues unit i (clamped: a request past the end repeats the last unit, so
