@@ -302,7 +302,8 @@ int cbk_blend_assemble_chunks(const cbk_kv_desc* kv, const int64_t* slots_dev,
  * Qwen3BlendExecutor._attention (cacheblend_vllm/ascend.py:798-846:
  * npu_fused_infer_attention_score or the einsum path) with the causal mask
  * q_pos < k_pos evaluated in the kernel. bf16/f16: head_dim 64 or 128,
- * 16-byte aligned pointers and row strides; float32: head_dim <= 128.
+ * 16-byte aligned pointers and row strides, K/V row strides < 2^24
+ * elements; float32: head_dim <= 128.
  */
 int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems, const int64_t* q_pos_dev, int64_t nq,
                         const void* k_dev, int64_t k_row_stride_elems, const void* v_dev,
@@ -310,7 +311,10 @@ int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems, const int
                         float scale, int32_t dtype, void* out_dev, int64_t out_row_stride_elems,
                         cbk_stream_t stream);
 
-/* Workspace bytes cbk_sparse_q_scores needs. */
+/* Workspace bytes cbk_sparse_q_scores needs: row statistics, a record per
+ * 16-query tile, per-KV-head partial column sums and a dense copy of the
+ * query rows (sized for head_dim 128): about nq * hq * 264 + nk * hkv * 4
+ * bytes. */
 size_t cbk_sparse_q_workspace_bytes(int64_t nq, int64_t nk, int64_t hq, int64_t hkv);
 
 /*
@@ -324,7 +328,8 @@ size_t cbk_sparse_q_workspace_bytes(int64_t nq, int64_t nk, int64_t hq, int64_t 
  * out_scores_dev[i] = full[out_index_dev[i]] (i < n_out; out_index NULL:
  * identity) and, when non-NULL, full_scores_dev[0 .. nk).
  * bf16/f16 run on MFMA (head_dim 64 or 128, up to 16 query heads per KV
- * head); f32 runs exact float32 dots. Deterministic (no float atomics).
+ * head, nq <= 2^26, K row stride < 2^24 elements); f32 runs exact float32
+ * dots. Deterministic (no float atomics).
  * Replaces Qwen3BlendExecutor._sparse_q_scores' score loop and its
  * index_select (cacheblend_vllm/ascend.py:683-701).
  */
