@@ -137,3 +137,15 @@ def test_blend_attention_full_blend_layer_properties():
     bound = want.float().abs() * (1 + 2 ** -7)
     assert bool((out2.float().abs() <= bound).all())
     assert torch.equal(out2, blend_attention(q, k, v2, pos, d ** -0.5))
+
+
+@pytest.mark.parametrize("nq,nk,d", [(1, 1, 128), (3, 5, 64), (20, 31, 128), (40, 32, 128), (50, 33, 64),
+                                     (64, 65, 128), (7, 97, 64)])
+def test_blend_attention_partial_key_blocks(nq, nk, d):
+    """Contexts of 1 to 97 keys: the last 32-key block is partial, its rows
+    past the context repeat the last key in LDS and must stay masked."""
+    hq, hkv = 8, 2
+    q, k, v, pos = _case(min(nq, nk), nk, hq, hkv, d, torch.bfloat16, seed=nq * 131 + nk)
+    print(f"nq={q.shape[0]} nk={nk} d={d}", flush=True)
+    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, 0.7)
+    _check(got, _oracle(q, k, v, pos, 0.7, "bf16"), f"nq={q.shape[0]} nk={nk} d={d}")

@@ -178,3 +178,25 @@ def test_sparse_q_full_layer6_properties():
     assert (full[last + 1:] == 0).all()
     _, again = S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, want_full=True)
     assert np.array_equal(again.cpu().numpy().astype(np.float64), full)
+
+
+@pytest.mark.parametrize("n_active,prefix,d", [(1, 0, 128), (5, 0, 64), (17, 40, 128), (63, 1, 64),
+                                                (64, 0, 128), (65, 63, 128), (200, 3, 64)])
+def test_sparse_q_small_contexts(n_active, prefix, d):
+    """1 to 265 keys and 1 to 200 queries: partial 64-key blocks (rows past
+    the context repeat the last key and are masked), single and partial
+    16-query tiles (rows past the queries are zeros, masked in the column
+    pass)."""
+    hq, hkv = 8, 2
+    g = torch.Generator().manual_seed(n_active * 7 + prefix)
+    nk = prefix + n_active
+    q = (torch.randn(n_active, hq, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    k = (torch.randn(nk, hkv, d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    absolute = torch.arange(prefix, nk)
+    rows = torch.arange(0, n_active, 1 if n_active < 20 else 3)
+    print(f"queries={rows.numel()} keys={nk} d={d}", flush=True)
+    _, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, d ** -0.5, want_full=True)
+    want = O.sparse_q_full_scores(q.float().numpy()[rows.numpy()], k.float().numpy(),
+                                  absolute.numpy()[rows.numpy()], d ** -0.5, True)
+    np.testing.assert_allclose(full.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
+    assert abs(float(full.sum()) - rows.numel() * hq) < 1e-3 * rows.numel() * hq
