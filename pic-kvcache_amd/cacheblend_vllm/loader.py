@@ -30,7 +30,6 @@ host once and uploaded once.
 
 from __future__ import annotations
 
-import ctypes
 import time
 
 import numpy as np

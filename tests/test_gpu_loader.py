@@ -15,7 +15,7 @@ from cacheblend_vllm.config import CacheBlendConfig
 from cacheblend_vllm.host_store import PinnedChunkStore
 from cacheblend_vllm.loader import PagedBlendLoader, build_source_map
 from cacheblend_vllm.rope import relocate_key, validate_rope_support
-from cacheblend_vllm.types import BlendPlan, BlendSegment, SegmentId
+from cacheblend_vllm.types import BlendPlan, BlendSegment
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
