@@ -15,16 +15,17 @@
 //                   holds key 4*(lane/16)+i of row lane%16 in register i
 //   online softmax  per row in the log2 domain, the row's 32 keys spread
 //                   over its 4 lane groups (two xor shuffles)
-//   O += P . V      v_mfma_f32_16x16x16_{bf16,f16}: the S^T registers are
-//                   exactly the A operand (row lane%16, keys 4*(lane/16)..+3);
-//                   B needs 4 consecutive keys of one dim, which
-//                   ds_read_tr16_b64 gathers from the row-major V block
+//   O += P . V      v_mfma_f32_16x16x32_{bf16,f16}: the two halves' S^T
+//                   registers, concatenated, are the A operand (row lane%16,
+//                   keys 4*(lane/16)..+3 and 16+4*(lane/16)..+3: the
+//                   contraction runs in that key order); B needs those keys
+//                   of one dim, which two ds_read_tr16_b64 gather from the
+//                   row-major V block
 // K/V blocks stream through three LDS buffers each by DMA (global_load_lds);
 // the row tiles with the latest positions (most keys) are scheduled first.
-// MFMA layouts (checked on gfx950): 16x16x32 A[i][k] in lane i+16*(k/8)
-// element k%8, B[k][j] in lane j+16*(k/8); 16x16x16 A[i][k] in lane
-// i+16*(k/4) element k%4, B[k][j] in lane j+16*(k/4); D[i][j] in lane
-// j+16*(i/4), register i%4.
+// MFMA layout (checked on gfx950): 16x16x32 A[i][k] in lane i+16*(k/8)
+// element k%8, B[k][j] in lane j+16*(k/8); D[i][j] in lane j+16*(i/4),
+// register i%4.
 //
 // float32 inputs take an exact float32 path (one wave per (query, head)).
 #include <hip/hip_bf16.h>
@@ -70,9 +71,6 @@ template <> struct Ops<false> {  // bf16
   static __device__ __forceinline__ f32x4 mma32(const A8& a, const A8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ f32x4 mma16(const A4& a, const A4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-  }
   // two floats -> two bf16 (round to nearest even) packed low/high
   static __device__ __forceinline__ uint32_t pack(float x, float y) {
     typedef float f2 __attribute__((ext_vector_type(2)));
@@ -87,9 +85,6 @@ template <> struct Ops<true> {  // f16
   typedef h16x4 A4;
   static __device__ __forceinline__ f32x4 mma32(const A8& a, const A8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 mma16(const A4& a, const A4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint32_t pack(float x, float y) {
     const __half2 h = __floats2half2_rn(x, y);
@@ -196,29 +191,39 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
       pa[t][h] = __builtin_bit_cast(typename O::A4, pk);
     }
   }
-  // O += P . V (each transposed V fragment read from LDS once), and the row
-  // sums l += P . 1 in the same layout as O
-  const typename O::A4 ones = __builtin_bit_cast(typename O::A4, u32x2{kOnesPair<F16>, kOnesPair<F16>});
+  // O += P . V and the row sums l += P . 1, one 16x16x32 MFMA per 16-dim column
+  // tile for the block's 32 keys (two 16x16x16 MFMAs cost as much each). The
+  // contraction runs in this lane layout's key order: k-slot 8 grp + e holds
+  // key 4 grp + e for e < 4 and 16 + 4 grp + e - 4 after, in P (the S^T
+  // registers of the two 16-key halves, concatenated) and in V (two
+  // transposing reads, one per half, concatenated).
+  typedef short s16x4v __attribute__((ext_vector_type(4)));
+  typename O::A8 pa8[RT];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int t = 0; t < RT; ++t) pa8[t] = __builtin_shufflevector(pa[t][0], pa[t][1], 0, 1, 2, 3, 4, 5, 6, 7);
+  const typename O::A8 ones = __builtin_bit_cast(
+      typename O::A8, u32x4{kOnesPair<F16>, kOnesPair<F16>, kOnesPair<F16>, kOnesPair<F16>});
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
     // lane (row, grp) addresses key 16h + 4 grp + row / 4, dims 16c + 4 (row % 4) .. + 3 of
     // the row-major V block; ds_read_tr16_b64 hands lane j of each 16-lane group element i of
-    // its group's lane 4i + j / 4, i.e. V[16h + 4 grp + i][16c + j]: the 16x16x16 B fragment
-    const uint32_t vkey = 16 * h + 4 * grp + (row >> 2);
+    // its group's lane 4i + j / 4, i.e. V[16h + 4 grp + i][16c + j]
+    const uint32_t dim = 16 * c + 4 * (row & 3);
+    s16x4v w[2];
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      const uint32_t dim = 16 * c + 4 * (row & 3);
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t vkey = 16 * h + 4 * grp + (row >> 2);
       const uint16_t* vp = &vs[vkey * D + (((dim / 8) ^ lds_swizzle<D>(vkey)) * 8) + (dim & 4)];
-      typedef short s16x4v __attribute__((ext_vector_type(4)));
-      const s16x4v w = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      w[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s16x4v*)((__attribute__((address_space(3))) const void*)vp));
-      const typename O::A4 vb = __builtin_bit_cast(typename O::A4, w);
-#pragma unroll
-      for (int t = 0; t < RT; ++t) o[t][c] = O::mma16(pa[t][h], vb, o[t][c]);
     }
+    const typename O::A8 vb =
+        __builtin_bit_cast(typename O::A8, __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-    for (int t = 0; t < RT; ++t) ol[t] = O::mma16(pa[t][h], ones, ol[t]);
+    for (int t = 0; t < RT; ++t) o[t][c] = O::mma32(pa8[t], vb, o[t][c]);
   }
+#pragma unroll
+  for (int t = 0; t < RT; ++t) ol[t] = O::mma32(pa8[t], ones, ol[t]);
 }
 
 // K and V blocks of 32 keys stream through three LDS buffers each by DMA
