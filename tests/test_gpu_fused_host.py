@@ -105,9 +105,12 @@ def test_fused_store_writes_chunks_bit_exact(layout, transfer):
     slab.close()
 
 
-def test_fused_store_then_host_read_load_round_trip():
-    """Store with the fused gather, blend-load with host reads and RoPE
-    relocation, commit: every stage bit-exact against the oracle."""
+@pytest.mark.parametrize("order,zero_copy", [("apart", "auto"), ("apart", False), ("adjacent", False)])
+def test_fused_store_then_load_round_trip(order, zero_copy):
+    """Store with the fused gather, blend-load (host reads, or DMA of the
+    run table -- segments in adjacent slab slots fold into one 2D copy per
+    plane) with RoPE relocation, commit: every stage bit-exact against the
+    oracle."""
     L, NB, BS, H, D, CH = 2, 192, 16, 4, 128, 256
     layers = [synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=60 + l) for l in range(L)]
     perm = torch.randperm(NB)
@@ -119,7 +122,8 @@ def test_fused_store_then_host_read_load_round_trip():
     writer.save_layer(1, layers[1], [RequestMetadata("a", list(range(1024)), slots, None, True, 1024)])
     writer.wait_for_save()
     segs = writer._save_segments["a"]
-    blend = [BlendSegment(segs[3][1], 260), BlendSegment(segs[1][1], 700)]
+    src = (3, 1) if order == "apart" else (1, 2)  # chunks 1 and 2 sit in consecutive slots
+    blend = [BlendSegment(segs[src[0]][1], 260), BlendSegment(segs[src[1]][1], 700)]
     store.pin("b", blend)
     plan = BlendPlan(40, 1100, 512, tuple(blend))
     new_slots = synthetic.block_slots(perm[64:64 + 70], BS, 1100)
@@ -139,13 +143,14 @@ def test_fused_store_then_host_read_load_round_trip():
         return O.f32_to_bf16(O.relocate_key(cache, old, new, k, D, True, bf16=True)).reshape(k_bits.shape)
 
     before = [_bits(l) for l in layers]
-    loader = PagedBlendLoader(layers, store, "b", plan, new_slots, BS, CacheBlendConfig.from_extra_config({}))
+    loader = PagedBlendLoader(layers, store, "b", plan, new_slots, BS, CacheBlendConfig.from_extra_config({}),
+                              zero_copy=zero_copy)
     loader.prefetch(0, rope)
     for l in range(L):
         buf = loader.get(l)
         loader.prefetch(l + 1, rope)
-        hosts = [(768, 260, O.gather_paged_kv(before[l], slots[768:1024].numpy(), BS)),
-                 (256, 700, O.gather_paged_kv(before[l], slots[256:512].numpy(), BS))]
+        hosts = [(256 * c, t, O.gather_paged_kv(before[l], slots[256 * c:256 * c + 256].numpy(), BS))
+                 for c, t in zip(src, (260, 700))]
         want = O.loader_assemble(before[l], new_slots.numpy(), BS, 40, 1100, hosts, relocate=reloc)
         np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
         loader.commit(l, buf)
@@ -153,7 +158,7 @@ def test_fused_store_then_host_read_load_round_trip():
         expect = before[l].copy()
         O.loader_commit(want, expect, new_slots.numpy(), BS, 40, 1100)
         np.testing.assert_array_equal(_bits(layers[l]), expect)
-    assert loader._zc_layers == {0, 1}
+    assert loader._zc_layers == ({0, 1} if zero_copy == "auto" else set())
     store.release("b")
     store.clear()
     writer.close()
