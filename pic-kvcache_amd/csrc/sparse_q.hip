@@ -328,38 +328,56 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 constexpr int kHeadChunk = 4;  // query heads per unit
 constexpr int kQBuffers = 3;   // units in LDS: computed, landed, requested
 
+template <typename V, int KSTEPS>
+__device__ __forceinline__ void colsum_mfma(const uint16_t* qlds, uint32_t hl, const V (&bfrag)[kColTiles][KSTEPS],
+                                            f32x4 (&acc)[kColTiles], uint32_t col, uint32_t rgrp) {
+  constexpr int D = 32 * KSTEPS;
+  const uint32_t row = hl * kQTile + col;
+  V afrag[KSTEPS];
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s)
+    afrag[s] = *reinterpret_cast<const V*>(&qlds[row * D + ((4 * s + rgrp) ^ lds_swizzle<D>(row)) * 8]);
+#pragma unroll
+  for (int c = 0; c < kColTiles; ++c) {
+    acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) acc[c] = mfma16<V>(afrag[s], bfrag[c][s], acc[c]);
+  }
+}
+
+// Software-pipelined over the unit's 4 head slots: the MFMAs of head hl + 1
+// are issued before the VALU work of head hl, which they do not depend on.
+// Slots past the group (nh < 4) compute on rows that are never used.
 template <typename V, int KSTEPS, int RMODE, bool MASK>
 __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
                                             uint32_t nh, int32_t kw0, const int32_t (&rpos)[4],
                                             const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
                                             uint32_t col, uint32_t rgrp) {
-  constexpr int D = 32 * KSTEPS;
-  for (uint32_t hl = 0; hl < nh; ++hl) {
-    const uint32_t row = hl * kQTile + col;
-    V afrag[KSTEPS];
+  f32x4 acc[2][kColTiles];
+  colsum_mfma<V, KSTEPS>(qlds, 0, bfrag, acc[0], col, rgrp);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      afrag[s] = *reinterpret_cast<const V*>(&qlds[row * D + ((4 * s + rgrp) ^ lds_swizzle<D>(row)) * 8]);
-    float mrow[4];
+  for (uint32_t hl = 0; hl < kHeadChunk; ++hl) {
+    if (hl + 1 < kHeadChunk) colsum_mfma<V, KSTEPS>(qlds, hl + 1, bfrag, acc[(hl + 1) & 1], col, rgrp);
+    if (hl < nh) {
+      float mrow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
+      for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
 #pragma unroll
-    for (int c = 0; c < kColTiles; ++c) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < kColTiles; ++c) {
+        const f32x4 v = acc[hl & 1][c];
+        float r[4] = {v[0], v[1], v[2], v[3]};
+        round_pair<RMODE>(r[0], r[1]);
+        round_pair<RMODE>(r[2], r[3]);
+        const int32_t key = kw0 + c * 16 + int32_t(col);
+        float sum = acc_col[c];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) acc = mfma16<V>(afrag[s], bfrag[c][s], acc);
-      float r[4] = {acc[0], acc[1], acc[2], acc[3]};
-      round_pair<RMODE>(r[0], r[1]);
-      round_pair<RMODE>(r[2], r[3]);
-      const int32_t key = kw0 + c * 16 + int32_t(col);
-      float sum = acc_col[c];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i]));
-        if constexpr (MASK) p = key > rpos[i] ? 0.f : p;
-        sum += p;
+        for (int i = 0; i < 4; ++i) {
+          float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i]));
+          if constexpr (MASK) p = key > rpos[i] ? 0.f : p;
+          sum += p;
+        }
+        acc_col[c] = sum;
       }
-      acc_col[c] = sum;
     }
   }
 }
