@@ -56,7 +56,11 @@ struct PagedArgs {
   PagedGeom g;
 };
 
-template <int VEC, bool GATHER, int kThreads>
+// kWaveRow: every row is a whole number of 64-lane waves (row_vecs % 64 ==
+// 0), so a wave's token, plane and slot are wave-uniform: the slot comes
+// through the scalar cache instead of a 64-lane vector load, which shortens
+// the slot -> data dependent-load chain each one-shot wave waits on.
+template <int VEC, bool GATHER, int kThreads, bool kWaveRow>
 __device__ __forceinline__ void paged_copy_body(const PagedGeom& a, const char* kb, const char* vb, char* cb) {
   using V = typename Vec<VEC>::T;
   const uint32_t total = a.num_tokens * a.planes * a.row_vecs;
@@ -74,11 +78,16 @@ __device__ __forceinline__ void paged_copy_body(const PagedGeom& a, const char* 
     page[u] = nullptr;
     cont[u] = nullptr;
     if (live[u]) {
-      const uint32_t row = a.row_div.div(f);
+      uint32_t row = a.row_div.div(f);
       const uint32_t j = f - row * a.row_vecs;
+      // kWaveRow: f - lane is a multiple of 64 and so of row_vecs' factor
+      // 64, so lane 0's row is every lane's
+      if (kWaveRow) row = __builtin_amdgcn_readfirstlane(row);
       const uint32_t c = row >= a.num_tokens ? 1u : 0u;
       const uint32_t t = row - c * a.num_tokens;
-      const int64_t slot = a.slots[t];
+      // a scalar load runs even where exec is 0: keep its address inside
+      // slots[] for a dead wave past the end (t is in range for live ones)
+      const int64_t slot = a.slots[kWaveRow ? min(t, a.num_tokens - 1) : t];
       valid[u] = slot >= 0 && slot < int64_t(a.num_slots);
       if (valid[u]) {
         const uint32_t s32 = uint32_t(slot);
@@ -113,19 +122,19 @@ __device__ __forceinline__ void paged_copy_body(const PagedGeom& a, const char* 
 }
 
 // blockIdx.y selects the layer
-template <int VEC, bool GATHER, int kThreads>
+template <int VEC, bool GATHER, int kThreads, bool kWaveRow>
 __global__ __launch_bounds__(kThreads) void paged_copy_kernel(const PagedArgs a) {
   const uint32_t layer = blockIdx.y;
-  paged_copy_body<VEC, GATHER, kThreads>(a.g, a.k_base[layer], a.v_base[layer],
-                                         a.g.c_base + int64_t(layer) * a.g.c_layer_stride);
+  paged_copy_body<VEC, GATHER, kThreads, kWaveRow>(a.g, a.k_base[layer], a.v_base[layer],
+                                                   a.g.c_base + int64_t(layer) * a.g.c_layer_stride);
 }
 
 // One layer: a ~100-byte argument block instead of the 1 KiB table, which
 // every short-lived wave would otherwise fetch (measured 4% on a one-layer
 // 30,719-token scatter).
-template <int VEC, bool GATHER, int kThreads>
+template <int VEC, bool GATHER, int kThreads, bool kWaveRow>
 __global__ __launch_bounds__(kThreads) void paged_copy1_kernel(const PagedGeom g, const char* kb, const char* vb) {
-  paged_copy_body<VEC, GATHER, kThreads>(g, kb, vb, g.c_base);
+  paged_copy_body<VEC, GATHER, kThreads, kWaveRow>(g, kb, vb, g.c_base);
 }
 
 // Copies between pages and chunks: token t of a batch is row t % chunk_tokens
@@ -287,17 +296,26 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
   const uint64_t total = uint64_t(num_tokens) * uint64_t(planes) * uint64_t(row_vecs);
   const int threads = gather ? kGatherThreads : kScatterThreads;
   const uint32_t grid_x = uint32_t((total + threads * kUnroll - 1) / (threads * kUnroll));
+  // whole waves per row (workgroups and unroll steps are whole waves)
+  static_assert(kGatherThreads % 64 == 0 && kScatterThreads % 64 == 0, "threads in whole waves");
+  const bool wave_row = row_vecs % 64 == 0;
 
   if (num_layers == 1) {
     const char* kb = static_cast<const char*>(kv->k_base);
     const char* vb = static_cast<const char*>(kv->v_base);
     dim3 grid(grid_x);
 #define CBK_LAUNCH_PAGED1(V)                                                             \
-  if (gather)                                                                            \
-    hipLaunchKernelGGL((paged_copy1_kernel<V, true, kGatherThreads>), grid,              \
+  if (gather && wave_row)                                                                \
+    hipLaunchKernelGGL((paged_copy1_kernel<V, true, kGatherThreads, true>), grid,        \
                        dim3(kGatherThreads), 0, stream, g, kb, vb);                      \
+  else if (gather)                                                                       \
+    hipLaunchKernelGGL((paged_copy1_kernel<V, true, kGatherThreads, false>), grid,       \
+                       dim3(kGatherThreads), 0, stream, g, kb, vb);                      \
+  else if (wave_row)                                                                     \
+    hipLaunchKernelGGL((paged_copy1_kernel<V, false, kScatterThreads, true>), grid,      \
+                       dim3(kScatterThreads), 0, stream, g, kb, vb);                     \
   else                                                                                   \
-    hipLaunchKernelGGL((paged_copy1_kernel<V, false, kScatterThreads>), grid,            \
+    hipLaunchKernelGGL((paged_copy1_kernel<V, false, kScatterThreads, false>), grid,     \
                        dim3(kScatterThreads), 0, stream, g, kb, vb);
     switch (vec) {
       case 16: CBK_LAUNCH_PAGED1(16); break;
@@ -321,11 +339,17 @@ int launch_paged(bool gather, const cbk_kv_desc* kv, int32_t num_layers, const i
     al.g.c_base = c_base + int64_t(l0) * c_layer_stride;
     dim3 grid(grid_x, uint32_t(nl));
 #define CBK_LAUNCH_PAGED(V)                                                              \
-  if (gather)                                                                            \
-    hipLaunchKernelGGL((paged_copy_kernel<V, true, kGatherThreads>), grid,               \
+  if (gather && wave_row)                                                                \
+    hipLaunchKernelGGL((paged_copy_kernel<V, true, kGatherThreads, true>), grid,         \
                        dim3(kGatherThreads), 0, stream, al);                             \
+  else if (gather)                                                                       \
+    hipLaunchKernelGGL((paged_copy_kernel<V, true, kGatherThreads, false>), grid,        \
+                       dim3(kGatherThreads), 0, stream, al);                             \
+  else if (wave_row)                                                                     \
+    hipLaunchKernelGGL((paged_copy_kernel<V, false, kScatterThreads, true>), grid,       \
+                       dim3(kScatterThreads), 0, stream, al);                            \
   else                                                                                   \
-    hipLaunchKernelGGL((paged_copy_kernel<V, false, kScatterThreads>), grid,             \
+    hipLaunchKernelGGL((paged_copy_kernel<V, false, kScatterThreads, false>), grid,      \
                        dim3(kScatterThreads), 0, stream, al);
     switch (vec) {
       case 16: CBK_LAUNCH_PAGED(16); break;
