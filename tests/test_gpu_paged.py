@@ -64,6 +64,10 @@ CASES = [
     ("merged_first", torch.float16, 40, 16, 3, 5, 333),    # 30-byte rows -> 2-byte vectors
     ("separate", torch.bfloat16, 33, 32, 1, 64, 1),
     ("merged_first", torch.float32, 10, 8, 5, 7, 80),      # 140-byte rows -> 4-byte vectors
+    # 1 KiB rows are whole waves (scalar slot loads); 3 and 37 tokens leave
+    # dead waves in the last workgroup of both launch shapes
+    ("merged_first", torch.bfloat16, 64, 16, 4, 128, 3),
+    ("separate", torch.bfloat16, 40, 16, 8, 64, 37),
 ]
 
 
@@ -131,6 +135,15 @@ def test_out_of_range_slots():
     # device slots are not read back: a bad row gathers zeros, never faults
     got = KL.gather_paged_kv(paged, torch.tensor([1, 99, 2], device=DEV), 16)
     assert got[:, 1].abs().sum().item() == 0 and got[:, 0].sum().item() == 16
+    # the same with 1 KiB rows, whose slot is one wave-uniform load
+    wide = torch.ones(2, 4, 16, 4, 128, dtype=torch.bfloat16, device=DEV)
+    got = KL.gather_paged_kv(wide, torch.tensor([1, 99, 2, -5], device=DEV), 16)
+    assert got[:, 1].abs().sum().item() == 0 and got[:, 3].abs().sum().item() == 0
+    assert got[:, 0].float().sum().item() == 2 * 512 and got[:, 2].float().sum().item() == 2 * 512
+    KL.scatter_paged_kv(torch.zeros(2, 2, 4, 128, dtype=torch.bfloat16, device=DEV), wide,
+                        torch.tensor([3, 640], device=DEV), 16)
+    flat = wide.view(2, 64, 512)
+    assert flat[:, 3].abs().sum().item() == 0 and flat.float().sum().item() == 2 * 63 * 512
 
 
 def test_multi_layer_gather_scatter_round_trip():
