@@ -22,24 +22,30 @@ Contract differences from the reference, on purpose:
 Pinning (what checks each function, all in tests/test_oracle.py):
 
 * slot_mapping, gather/scatter, layout dispatch: reference known answers
-  (tests/test_connector_scheduler.py:58-90, tests/test_kv_layout.py:7-40),
+  (tests/test_connector_scheduler.py:58-90, tests/test_kv_layout.py:8-40),
   brute-force loops, round trips.
-* select / budget: reference known answers (tests/test_ascend.py:184-194,
-  296-307), brute force over every subset order on tiny inputs, tie cases.
+* select / budget: reference known answers (tests/test_ascend.py:144-154,
+  256-267), brute force over every subset order on tiny inputs, tie cases.
 * dilate / sparse_q_masks: reference known answers (tests/test_ascend.py:
-  255-293), brute-force window scan.
+  215-253), brute-force window scan.
 * sparse_q_full_scores: reference closed-form test (tests/test_ascend.py:
-  197-252), float64 dense softmax, column sums equal query count (softmax rows
+  157-212), float64 dense softmax, column sums equal query count (softmax rows
   sum to one).
 * kdev_scores: float64 closed form on integer-valued data where float32 is
   exact, zero on identical inputs.
 * relocate_key: reference known answer against fresh RoPE
-  (tests/test_ascend.py:91-100), group property R(a)R(b)^-1.
+  (tests/test_ascend.py:52-60), group property R(a)R(b)^-1; the bf16 path
+  bit-exact against torch's CPU bf16 elementwise kernels run in the order
+  of ascend.py:76-103 (the reference's third-party arithmetic).
 * loader_assemble / loader_commit: reference known answer
-  (tests/test_ascend.py:136-181).
+  (tests/test_ascend.py:96-141).
 * blend_attention: float64 closed forms -- identical keys give the mean of
   the visible values, a one-key context returns that value, uniform logits
-  average the visible rows, and a brute-force per-query softmax loop.
+  average the visible rows, two visible keys weigh sigmoid(scale * (q.k1 -
+  q.k0)); a float64 brute-force per-(query, head) causal softmax with
+  non-constant logits and scales 0.37 and 1.7; the bf16 and f16 rounding
+  sequence bit-exact against torch's CPU kernels run in the order of
+  ascend.py:834-846.
 * content_hash / window_hashes / match_tokens: reference known answers
   (tests/test_matcher.py:6-31), closed forms of one- and two-token hashes,
   the wrap at 2^64, window hashes equal the Horner hash at every offset, and

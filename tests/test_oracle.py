@@ -291,7 +291,7 @@ def test_kdev_scores_closed_form():
 
 
 class _FakeRope:
-    """Closed-form RoPE with one angle per position (tests/test_ascend.py:57-82)."""
+    """Closed-form RoPE with one angle per position (tests/test_ascend.py:17-42)."""
 
     def __init__(self, neox, angle):
         self.neox, self.angle = neox, angle
@@ -493,3 +493,124 @@ def test_match_tokens_brute_force_properties():
             else:
                 p += 1
         assert got == expect, (trial, tokens, chunks, start)
+
+
+def _attention_brute_force(q, k, v, pos, scale):
+    """Per-(query, head) causal softmax in float64 with Python scalars."""
+    nq, hq, d = q.shape
+    nk, hkv, _ = k.shape
+    g = hq // hkv
+    out = np.zeros((nq, hq, d))
+    for i in range(nq):
+        for h in range(hq):
+            kvh = h // g
+            logits = [scale * math.fsum(float(q[i, h, j]) * float(k[t, kvh, j]) for j in range(d))
+                      for t in range(int(pos[i]) + 1)]
+            top = max(logits)
+            w = [math.exp(x - top) for x in logits]
+            total = math.fsum(w)
+            for j in range(d):
+                out[i, h, j] = math.fsum(w[t] * float(v[t, kvh, j]) for t in range(len(w))) / total
+    return out
+
+
+def test_blend_attention_scaled_softmax_brute_force():
+    """Non-constant logits, scale not in {0, 1}, GQA 3 query heads per KV head,
+    positions that cut the context at different keys (ascend.py:827-846)."""
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((5, 6, 8)).astype(np.float32)
+    k = rng.standard_normal((9, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((9, 2, 8)).astype(np.float32)
+    pos = np.array([0, 8, 3, 6, 1])
+    for scale in (0.37, 1.7):
+        got = O.blend_attention(q, k, v, pos, scale, None)
+        want = _attention_brute_force(q, k, v, pos, scale)
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=1e-6)
+    # the scale matters: the result at 0.37 is not the result at 1.7 or at 1
+    assert np.abs(O.blend_attention(q, k, v, pos, 0.37, None)
+                  - O.blend_attention(q, k, v, pos, 1.0, None)).max() > 1e-2
+
+
+def test_blend_attention_two_key_closed_form():
+    """A query at position 1 sees keys 0 and 1 only; the weight on key 1 is
+    sigmoid(scale * (q.k1 - q.k0)) and the output is v0 + w1 (v1 - v0)."""
+    rng = np.random.default_rng(22)
+    q = rng.standard_normal((1, 2, 16)).astype(np.float32)
+    k = rng.standard_normal((4, 1, 16)).astype(np.float32)
+    k[2:] *= 50.0  # keys past the query position would dominate if not masked
+    v = rng.standard_normal((4, 1, 16)).astype(np.float32)
+    scale = 0.61
+    got = O.blend_attention(q, k, v, np.array([1]), scale, None)
+    for h in range(2):
+        diff = float(np.dot(q[0, h].astype(np.float64), (k[1, 0] - k[0, 0]).astype(np.float64)))
+        w1 = 1.0 / (1.0 + math.exp(-scale * diff))
+        want = v[0, 0].astype(np.float64) + w1 * (v[1, 0].astype(np.float64) - v[0, 0])
+        np.testing.assert_allclose(got[0, h], want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rounding", ["bf16", "f16"])
+def test_blend_attention_rounding_sequence_matches_torch_cpu(rounding):
+    """The rounded path against torch's own CPU kernels run in the order the
+    reference's einsum path uses (ascend.py:834-846): einsum in the input
+    dtype, ``* scale`` in the input dtype, masked_fill with the dtype's
+    minimum, float32 softmax cast back to the input dtype, einsum. Query and
+    key values are multiples of 1/8 so the score sums are exact in float32
+    and only the roundings under test can differ."""
+    torch = pytest.importorskip("torch")
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16}[rounding]
+    rng = np.random.default_rng(23)
+    nq, hq, hkv, nk, d = 6, 4, 2, 11, 16
+    q = (rng.integers(-12, 13, (nq, hq, d)) / 8.0).astype(np.float32)
+    k = (rng.integers(-12, 13, (nk, hkv, d)) / 8.0).astype(np.float32)
+    v = O.round_bf16(rng.standard_normal((nk, hkv, d))) if rounding == "bf16" else \
+        O.round_f16(rng.standard_normal((nk, hkv, d)))
+    pos = np.array([10, 0, 4, 7, 2, 9])
+    scale = 0.3
+    tq, tk, tv = (torch.from_numpy(x).to(dt) for x in (q, k, v))
+    g = hq // hkv
+    tk = tk[:, :, None].expand(-1, -1, g, -1).reshape(nk, hq, d)
+    tv = tv[:, :, None].expand(-1, -1, g, -1).reshape(nk, hq, d)
+    mask = torch.from_numpy(pos)[:, None] < torch.arange(nk)[None, :]
+    w = torch.einsum("qhd,khd->hqk", tq, tk) * scale
+    w = w.masked_fill(mask[None], torch.finfo(w.dtype).min)
+    p = torch.softmax(w.float(), dim=-1).to(dt)
+    want = torch.einsum("hqk,khd->qhd", p, tv).float().numpy()
+    got = O.blend_attention(q, k, v, pos, scale, rounding)
+    np.testing.assert_array_equal(got, want)
+    # a rounding dropped anywhere in the chain is visible at these inputs
+    assert not np.array_equal(O.blend_attention(q, k, v, pos, scale, None), want)
+
+
+@pytest.mark.parametrize("neox", [False, True])
+def test_relocate_key_bf16_matches_torch_cpu_bf16_ops(neox):
+    """relocate_key(bf16=True) against torch's CPU bf16 elementwise kernels run
+    in the order of ascend.py:76-103 (cache cast to the key dtype, index,
+    delta cos/sin, rotation; every product, sum and difference rounded to
+    bf16 by torch). Elementwise ops round per element, so equality is exact."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(24)
+    head, heads, rows, max_pos = 16, 3, 40, 300
+    inv = 1.0 / (10000 ** (np.arange(0, head, 2) / head))
+    ang = np.arange(max_pos)[:, None] * inv[None, :]
+    cache = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+    key = O.round_bf16(rng.standard_normal((rows, heads * head)))
+    old = rng.integers(0, max_pos, rows)
+    new = rng.integers(0, max_pos, rows)
+    tcache = torch.from_numpy(cache).to(torch.bfloat16)
+    oc, os_ = tcache.index_select(0, torch.from_numpy(old)).chunk(2, dim=-1)
+    nc, ns = tcache.index_select(0, torch.from_numpy(new)).chunk(2, dim=-1)
+    dcos = (nc * oc + ns * os_).unsqueeze(1)
+    dsin = (ns * oc - nc * os_).unsqueeze(1)
+    shaped = torch.from_numpy(key).to(torch.bfloat16).reshape(rows, heads, head)
+    if neox:
+        first, second = torch.chunk(shaped, 2, dim=-1)
+        want = torch.cat((first * dcos - second * dsin, second * dcos + first * dsin), dim=-1)
+    else:
+        first, second = shaped[..., ::2], shaped[..., 1::2]
+        want = torch.stack((first * dcos - second * dsin, second * dcos + first * dsin), dim=-1).flatten(-2)
+    want = want.reshape(rows, heads * head).float().numpy()
+    got = O.relocate_key(cache, old, new, key, head, neox, bf16=True)
+    np.testing.assert_array_equal(got, want)
+    # float32 arithmetic rounded once at the end is not the same thing
+    once = O.round_bf16(O.relocate_key(cache, old, new, key, head, neox, bf16=False))
+    assert not np.array_equal(once, want)
