@@ -18,11 +18,15 @@ gfx950 paged-gather kernel and the copies on a HIP side stream:
                             the reference does. Then an event, and the batch
                             goes to a publisher thread (backpressure
                             semaphore)
-  _publish_after_event      publisher thread: event.synchronize(), then put
-                            the per-chunk slots (or views of the batch) into
-                            the store; any failure aborts every chunk of the
-                            batch
+  _publish                  publisher thread: wait for the batch's event,
+                            then put the per-chunk slots (or views of the
+                            batch) into the store; any failure aborts every
+                            chunk of the batch
   wait_for_save             Store-stream sync + join publishers; staging freed
+
+A batch in flight is a ``_StoreBatch``; ``_InflightSaves`` bounds and tracks
+the publications per request, ``_StagingCache`` owns the pinned-batch
+scheme's device stagings until the Store stream drains.
 
 Everything enqueued goes to one default-priority Store stream, so the D2H of
 layer l and the gather of layer l + 1 are ordered on it while the serving
@@ -69,8 +73,18 @@ class RequestMetadata:
     save_end: int
 
 
+try:  # vLLM's metadata base, which bind_connector_metadata expects, when vLLM is installed
+    from vllm.distributed.kv_transfer.kv_connector.v1.base import (  # type: ignore
+        KVConnectorMetadata as _MetadataBase,
+    )
+except ImportError:
+    _MetadataBase = object
+
+
 @dataclass(slots=True)
-class CacheBlendConnectorMetadata:
+class CacheBlendConnectorMetadata(_MetadataBase):
+    """What the scheduler hands the worker each step (reference connector.py:70-72)."""
+
     requests: list[RequestMetadata] = field(default_factory=list)
 
 
@@ -105,6 +119,96 @@ def _chain(inner: Future, outer: Future) -> None:
         outer.set_exception(error)
     else:
         outer.set_result(inner.result())
+
+
+@dataclass(slots=True)
+class _StoreBatch:
+    """One request's chunks of one layer on their way into the store.
+
+    ``pending`` lists ``(segment id, layer, tokens)`` per chunk, in the order
+    of ``host``: one pinned slab slot per chunk, or one pinned
+    ``[2, tokens, *row]`` batch whose consecutive token ranges are the chunks.
+    ``ready`` is the GPU event after which ``host`` holds the bytes.
+    """
+
+    request_id: str
+    pending: list[tuple[Any, int, int]]
+    host: Any
+    ready: Any = None
+    enqueued_ns: int | None = None
+
+    def chunks(self):
+        """``(index, segment id, layer, host tensor)`` per chunk; chunks of a
+        pinned batch are views of it, so the store keeps the batch alive."""
+        offset = 0
+        for index, (segment_id, layer_id, tokens) in enumerate(self.pending):
+            if isinstance(self.host, list):
+                yield index, segment_id, layer_id, self.host[index]
+            else:
+                yield index, segment_id, layer_id, self.host[:, offset:offset + tokens]
+            offset += tokens
+
+    @property
+    def tokens(self) -> int:
+        return sum(tokens for _, _, tokens in self.pending)
+
+
+class _InflightSaves:
+    """Publication futures per request, at most ``limit`` batches at once:
+    ``admit`` blocks the saving thread while the limit is reached and a
+    batch's slot frees when its future completes."""
+
+    def __init__(self, limit: int):
+        self._slots = threading.Semaphore(limit)
+        self._lock = threading.Lock()
+        self._futures: dict[str, list[Future]] = {}
+
+    def admit(self) -> None:
+        self._slots.acquire()
+
+    def cancel_admission(self) -> None:
+        self._slots.release()
+
+    def track(self, request_id: str, future: Future) -> None:
+        with self._lock:
+            self._futures.setdefault(request_id, []).append(future)
+        future.add_done_callback(lambda _f: self._slots.release())
+
+    def take(self) -> dict[str, list[Future]]:
+        """Every tracked future, grouped by request; tracking starts over."""
+        with self._lock:
+            taken, self._futures = self._futures, {}
+        return taken
+
+    def __bool__(self) -> bool:
+        with self._lock:
+            return any(self._futures.values())
+
+
+class _StagingCache:
+    """Device stagings of the per-layer pinned-batch scheme: one per request,
+    refilled in place while a layer has as many pending tokens as the last.
+    A staging of another size is retired, not freed, because the D2H of an
+    earlier layer may still read it; everything goes at the Store-stream
+    boundary (``clear``)."""
+
+    def __init__(self):
+        self.live: dict[str, torch.Tensor] = {}
+        self.retired: list[torch.Tensor] = []
+
+    def gather(self, request_id: str, kv_layer: Any, slots: torch.Tensor, block_size: int) -> torch.Tensor:
+        staging = self.live.get(request_id)
+        if staging is not None and staging.shape[1] == slots.numel():
+            gather_paged_kv(kv_layer, slots, block_size, out=staging)
+            return staging
+        if staging is not None:
+            self.retired.append(staging)
+        staging = self.live[request_id] = gather_paged_kv(kv_layer, slots, block_size).contiguous()
+        return staging
+
+    def clear(self) -> None:
+        self.live.clear()
+        self.retired.clear()
 
 
 class StoreStreamWriter:
@@ -157,15 +261,12 @@ class StoreStreamWriter:
         self._trace = tracer or PipelineTracer("worker")
         self._streams = streams
         self._store_stream = store_stream if store_stream is not None else streams.Stream()
-        self._save_pool = ThreadPoolExecutor(max_workers=store_workers,
-                                             thread_name_prefix="cacheblend-save")
-        self._save_slots = threading.Semaphore(max_inflight_store_batches)
-        self._save_lock = threading.Lock()
-        self._save_futures: set[Future] = set()
-        self._pending_store_counts: dict[str, int] = {}
-        self._save_segments: dict[str, list[tuple[int, SegmentId]]] = {}
-        self._store_staging_by_request: dict[str, torch.Tensor] = {}
-        self._retired_store_staging: list[torch.Tensor] = []
+        self._publishers = ThreadPoolExecutor(max_workers=store_workers,
+                                              thread_name_prefix="cacheblend-save")
+        self._inflight = _InflightSaves(max_inflight_store_batches)
+        self._staging = _StagingCache()
+        # chunk identities per request, hashed once: [(prompt offset, id)]
+        self._chunk_ids: dict[str, list[tuple[int, SegmentId]]] = {}
         # per request: (host slot list, device copy); the fused slot list is
         # normally identical for every layer, so it is uploaded once
         self._device_slots: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
@@ -222,7 +323,7 @@ class StoreStreamWriter:
 
     def _request_save_segments(self, request: RequestMetadata, usable: int) -> list[tuple[int, SegmentId]]:
         """Chunk identities hashed once per request (reference connector.py:363-382)."""
-        segments = self._save_segments.setdefault(request.request_id, [])
+        segments = self._chunk_ids.setdefault(request.request_id, [])
         start = len(segments) * self.chunk_size
         begin_chunks = getattr(self._store, "begin_put_chunks", None)
         if begin_chunks is not None and start < usable:
@@ -246,55 +347,46 @@ class StoreStreamWriter:
         request_id: str,
         store_enqueued_ns: int | None = None,
     ) -> None:
-        """Gather + pinned D2H on the Store stream (reference connector.py:384-447)."""
-        self._save_slots.acquire()
+        """Gather + D2H on the Store stream, then publication off the saving
+        thread (reference connector.py:384-447)."""
+        batch = _StoreBatch(request_id, pending, None, enqueued_ns=store_enqueued_ns)
+        self._inflight.admit()
         try:
             if self._store_stream is None:
                 raise RuntimeError("CacheBlend Store stream was not initialized")
-            current = self._streams.current_stream()
+            serving = self._streams.current_stream()
             with self._streams.stream(self._store_stream):
-                self._store_stream.wait_stream(current)
+                self._store_stream.wait_stream(serving)
                 slots = self._upload_slots(request_id, slots, kv_layer)
                 if self._slab is not None:
-                    host = self._slab.alloc_run(len(pending))
+                    batch.host = self._slab.alloc_run(len(pending))
                     if self._slab_transfer == "host_write":
-                        self._gather_to_chunks(kv_layer, slots, [h.data_ptr() for h in host])
+                        self._gather_to_chunks(kv_layer, slots, [h.data_ptr() for h in batch.host])
                     else:
-                        staging, runs = self._gather_for_dma(kv_layer, slots, host)
+                        staging, runs = self._gather_for_dma(kv_layer, slots, batch.host)
                 else:
-                    staging = self._store_staging_by_request.get(request_id)
-                    if staging is None or staging.shape[1] != slots.numel():
-                        if staging is not None:
-                            # an earlier D2H may still read it: keep it until the
-                            # Store stream drains (wait_for_save)
-                            self._retired_store_staging.append(staging)
-                        staging = gather_paged_kv(kv_layer, slots, self.block_size).contiguous()
-                        self._store_staging_by_request[request_id] = staging
-                    else:
-                        gather_paged_kv(kv_layer, slots, self.block_size, out=staging)
-                    host = torch.empty(staging.shape, dtype=staging.dtype, device="cpu", pin_memory=True)
-                    host.copy_(staging, non_blocking=True)
+                    staging = self._staging.gather(request_id, kv_layer, slots, self.block_size)
+                    batch.host = torch.empty(staging.shape, dtype=staging.dtype, device="cpu",
+                                             pin_memory=True)
+                    batch.host.copy_(staging, non_blocking=True)
                 event = self._streams.Event()
                 event.record(self._store_stream)
             if self._slab is not None and self._slab_transfer == "dma":
+                # the copier issues the D2H once the gather is done and sets
+                # batch.ready to the copy's event
                 future = Future()
-                self._copier_queue().put((event, staging, runs, pending, host, request_id,
-                                          store_enqueued_ns, future))
+                self._copier_queue().put((event, staging, runs, batch, future))
                 del staging
             else:
-                future = self._save_pool.submit(
-                    self._publish_after_event, event, pending, host, request_id, store_enqueued_ns
-                )
+                batch.ready = event
+                future = self._publishers.submit(self._publish, batch)
         except Exception:
-            self._save_slots.release()
-            if self._slab is not None and isinstance(locals().get("host"), list):
-                for chunk in locals()["host"]:
+            self._inflight.cancel_admission()
+            if self._slab is not None and isinstance(batch.host, list):
+                for chunk in batch.host:
                     self._slab.free(chunk)
             raise
-        with self._save_lock:
-            self._save_futures.add(future)
-            self._pending_store_counts[request_id] = self._pending_store_counts.get(request_id, 0) + 1
-        future.add_done_callback(self._save_done)
+        self._inflight.track(request_id, future)
 
     def _upload_slots(self, request_id: str, slots: torch.Tensor, kv_layer: Any) -> torch.Tensor:
         """Device copy of a host slot list, reused while it does not change.
@@ -358,147 +450,118 @@ class StoreStreamWriter:
     def _copier_loop(self) -> None:
         """Copier thread: per layer, in order, wait (host side) for the
         gather, issue the runs' D2H copies on the Copy stream, hand the
-        publication to the save pool. A wait between two copies on one
+        publication to the publisher pool. A wait between two copies on one
         stream left the DMA engine idle ~50-100 us whenever the submitting
         thread was busy between them; here the copies follow each other."""
         while True:
             job = self._copy_jobs.get()
             if job is None:
                 return
-            gathered, staging, (dst, src, nbytes), pending, host, request_id, enqueued_ns, future = job
+            gathered, staging, (dst, src, nbytes), batch, future = job
             try:
                 gathered.synchronize()
                 _native.memcpy_runs(dst, src, nbytes, self._copy_stream.cuda_stream, "chunk runs D2H")
                 staging.record_stream(self._copy_stream)
-                copied = self._streams.Event()
-                copied.record(self._copy_stream)
+                batch.ready = self._streams.Event()
+                batch.ready.record(self._copy_stream)
             except BaseException as error:  # the batch fails as a unit
-                for segment_id, _, _ in pending:
+                for segment_id, _, _ in batch.pending:
                     self._store.abort_put(segment_id)
-                for chunk in host:
+                for chunk in batch.host:
                     self._slab.free(chunk)
                 future.set_exception(error)
                 continue
             finally:
                 del staging
-            inner = self._save_pool.submit(self._publish_after_event, copied, pending, host, request_id,
-                                           enqueued_ns)
+            inner = self._publishers.submit(self._publish, batch)
             inner.add_done_callback(lambda f, out=future: _chain(f, out))
 
-    def _publish_host_batch(self, pending: list[tuple[Any, int, int]], host, accepted=None) -> bool:
-        """Per-chunk host tensors into the store (connector.py:449-466): views
-        of one pinned batch, or (fused path) one slab slot per chunk.
-        ``accepted[i]`` records whether the store kept slot i."""
-        offset = 0
-        committed = False
+    def _put_chunks(self, batch: _StoreBatch, kept: list[bool]) -> bool:
+        """Each chunk into the store (reference connector.py:449-466);
+        ``kept[i]`` says whether the store holds chunk i afterwards. True
+        when some segment became committed."""
         holds = getattr(self._store, "holds", None)
-        for index, (segment_id, layer_id, length) in enumerate(pending):
-            chunk = host[index] if isinstance(host, list) else host[:, offset : offset + length]
-            result = self._store.put_layer_host(segment_id, layer_id, chunk)
-            if result is not None:
-                committed |= result
-            if accepted is not None:
-                accepted[index] = holds is not None and holds(segment_id, layer_id, chunk)
-            offset += length
+        committed = False
+        for index, segment_id, layer_id, chunk in batch.chunks():
+            committed |= bool(self._store.put_layer_host(segment_id, layer_id, chunk))
+            kept[index] = holds is not None and holds(segment_id, layer_id, chunk)
         return committed
 
-    def _publish_after_event(
-        self,
-        event: Any,
-        pending: list[tuple[Any, int, int]],
-        host: torch.Tensor,
-        request_id: str | None = None,
-        store_enqueued_ns: int | None = None,
-    ) -> bool:
-        """Publisher thread body (reference connector.py:468-499). Fused path:
-        slots the store did not keep go back to the slab (the ones it keeps
-        return through its release hook when it drops them)."""
-        slots = isinstance(host, list) and self._slab is not None
-        accepted = [False] * len(pending) if slots else None
+    def _publish(self, batch: _StoreBatch) -> bool:
+        """Publisher thread (reference connector.py:468-499): wait for the
+        batch's bytes, publish every chunk, trace. Any failure drops the
+        batch's segments as a unit. Slab slots the store did not keep go
+        back to the slab at once; kept ones return through the store's
+        release hook when it drops them."""
+        kept = [False] * len(batch.pending)
         try:
-            return self._publish_checked(event, pending, host, request_id, store_enqueued_ns, accepted)
-        finally:
-            if slots:
-                for chunk, kept in zip(host, accepted):
-                    if not kept:
-                        self._slab.free(chunk)
-
-    def _publish_checked(self, event, pending, host, request_id, store_enqueued_ns, accepted) -> bool:
-        try:
-            event.synchronize()
-            if accepted is None:
-                committed = self._publish_host_batch(pending, host)
-            else:
-                committed = self._publish_host_batch(pending, host, accepted)
-            if self._trace.enabled:
-                self._trace.emit(
-                    "save_store_finished",
-                    request_id=request_id,
-                    layer_id=pending[0][1] if pending else None,
-                    chunks=len(pending),
-                    tokens=sum(n for _, _, n in pending),
-                    duration_us=((time.monotonic_ns() - store_enqueued_ns) / 1000
-                                 if store_enqueued_ns is not None else None),
-                    committed_segment=committed,
-                )
-            return committed
+            batch.ready.synchronize()
+            committed = self._put_chunks(batch, kept)
         except Exception:
-            for segment_id, _, _ in pending:
+            for segment_id, _, _ in batch.pending:
                 self._store.abort_put(segment_id)
+            committed = None
+        finally:
+            if self._slab is not None and isinstance(batch.host, list):
+                for chunk, held in zip(batch.host, kept):
+                    if not held:
+                        self._slab.free(chunk)
+        if committed is None:
             return False
-
-    def _save_done(self, future: Future) -> None:
-        self._save_slots.release()
+        if self._trace.enabled:
+            self._trace.emit(
+                "save_store_finished",
+                request_id=batch.request_id,
+                layer_id=batch.pending[0][1] if batch.pending else None,
+                chunks=len(batch.pending),
+                tokens=batch.tokens,
+                duration_us=((time.monotonic_ns() - batch.enqueued_ns) / 1000
+                             if batch.enqueued_ns is not None else None),
+                committed_segment=committed,
+            )
+        return committed
 
     def wait_for_save(self) -> None:
-        """Store-stream sync, then join publishers (reference connector.py:504-534)."""
+        """The save boundary (reference connector.py:504-534): drain the Store
+        stream, then every publication enqueued so far; stagings are freed
+        afterwards whatever happened."""
         started = time.monotonic_ns() if self._trace.enabled else 0
-        futures: tuple[Future, ...] = ()
-        counts: dict[str, int] = {}
+        taken: dict[str, list[Future]] = {}
         try:
             if self._store_stream is not None:
                 self._store_stream.synchronize()
-            with self._save_lock:
-                futures = tuple(self._save_futures)
-                counts = dict(self._pending_store_counts)
-                self._pending_store_counts.clear()
-            for future in futures:
-                future.result()
+            taken = self._inflight.take()
+            for futures in taken.values():
+                for future in futures:
+                    future.result()
         finally:
-            with self._save_lock:
-                self._save_futures.difference_update(futures)
-            self._store_staging_by_request.clear()
-            self._retired_store_staging.clear()
+            self._staging.clear()
             self._device_slots.clear()
         if self._trace.enabled:
             duration = (time.monotonic_ns() - started) / 1000
-            for request_id, stores in counts.items():
-                self._trace.emit("save_store_wait_finished", request_id=request_id, stores=stores,
-                                 duration_us=duration)
+            for request_id, futures in taken.items():
+                self._trace.emit("save_store_wait_finished", request_id=request_id,
+                                 stores=len(futures), duration_us=duration)
 
     def finished(self, request_ids) -> None:
         """get_finished's store cleanup (reference connector.py:551-557)."""
         for request_id in request_ids:
             self._store.release(request_id)
-            for _, segment_id in self._save_segments.pop(request_id, ()):
+            for _, segment_id in self._chunk_ids.pop(request_id, ()):
                 self._store.abort_put(segment_id)
 
     def close(self) -> None:
+        """Wait for every publication (including ones enqueued meanwhile),
+        then stop the copier and the publisher pool."""
         try:
-            while True:
-                with self._save_lock:
-                    futures = tuple(self._save_futures)
-                if not futures:
-                    break
-                for future in futures:
-                    future.result()
-                with self._save_lock:
-                    self._save_futures.difference_update(futures)
+            while self._inflight:
+                for futures in self._inflight.take().values():
+                    for future in futures:
+                        future.result()
         finally:
             if self._copier is not None:
                 self._copy_jobs.put(None)
                 self._copier.join()
                 self._copier = None
-            self._store_staging_by_request.clear()
-            self._retired_store_staging.clear()
-            self._save_pool.shutdown(wait=True, cancel_futures=False)
+            self._staging.clear()
+            self._publishers.shutdown(wait=True, cancel_futures=False)

@@ -1,8 +1,13 @@
-"""Opt-in JSONL pipeline tracing (enabled by ``CACHEBLEND_TRACE_DIR``).
+"""Opt-in JSONL pipeline trace, switched on by ``CACHEBLEND_TRACE_DIR``.
 
-Same event stream format as the reference tracer
-(cacheblend_vllm/trace.py:19-64): one line-buffered JSONL file per process
-and component; host-side timestamps only, never a device synchronisation.
+The record format is the reference tracer's (cacheblend_vllm/trace.py:19-64),
+so its trace analysis reads these files unchanged: one file per process and
+component, ``<dir>/<component>-pid-<pid>.jsonl``, opened for append and
+line-buffered; each line a compact, key-sorted JSON object with
+``timestamp_ns``, ``monotonic_ns``, ``pid``, ``thread_id``, ``component``,
+``event``, an optional ``request_id`` and the event's own fields; the first
+line of a tracer is ``trace_started``. Timestamps are taken on the host when
+the event is emitted; tracing never synchronises a device.
 """
 
 from __future__ import annotations
@@ -11,50 +16,55 @@ import json
 import os
 import threading
 import time
-from pathlib import Path
-from typing import Any
+from typing import Any, TextIO
+
+TRACE_DIR_ENV = "CACHEBLEND_TRACE_DIR"
+_encode = json.JSONEncoder(sort_keys=True, separators=(",", ":")).encode
+
+
+def _open_trace_file(component: str) -> TextIO | None:
+    directory = os.environ.get(TRACE_DIR_ENV)
+    if not directory:
+        return None
+    os.makedirs(directory, exist_ok=True)
+    path = os.path.join(directory, f"{component}-pid-{os.getpid()}.jsonl")
+    return open(path, "a", encoding="utf-8", buffering=1)
 
 
 class PipelineTracer:
+    """Event sink of one pipeline component. When tracing is off, ``emit``
+    returns at its first test and ``enabled`` lets callers skip building
+    event fields at all."""
+
+    __slots__ = ("component", "_sink", "_guard")
+
     def __init__(self, component: str):
         self.component = component
-        self._lock = threading.Lock()
-        self._file = None
-        root = os.getenv("CACHEBLEND_TRACE_DIR")
-        if not root:
-            return
-        directory = Path(root)
-        directory.mkdir(parents=True, exist_ok=True)
-        self._file = (directory / f"{component}-pid-{os.getpid()}.jsonl").open(
-            "a", encoding="utf-8", buffering=1
-        )
-        self.emit("trace_started")
+        self._guard = threading.Lock()
+        self._sink = _open_trace_file(component)
+        if self._sink is not None:
+            self.emit("trace_started")
 
     @property
     def enabled(self) -> bool:
-        return self._file is not None
+        return self._sink is not None
 
     def emit(self, event: str, request_id: str | None = None, **fields: Any) -> None:
-        if self._file is None:
+        if self._sink is None:
             return
-        record: dict[str, Any] = {
-            "timestamp_ns": time.time_ns(),
-            "monotonic_ns": time.monotonic_ns(),
-            "pid": os.getpid(),
-            "thread_id": threading.get_ident(),
-            "component": self.component,
-            "event": event,
-        }
+        head = {"timestamp_ns": time.time_ns(), "monotonic_ns": time.monotonic_ns(),
+                "pid": os.getpid(), "thread_id": threading.get_ident(),
+                "component": self.component, "event": event}
         if request_id is not None:
-            record["request_id"] = request_id
-        record.update(fields)
-        line = json.dumps(record, sort_keys=True, separators=(",", ":"))
-        with self._lock:
-            if self._file is not None:
-                self._file.write(line + "\n")
+            head["request_id"] = request_id
+        text = _encode({**head, **fields}) + "\n"
+        with self._guard:
+            sink = self._sink
+            if sink is not None:
+                sink.write(text)
 
     def close(self) -> None:
-        with self._lock:
-            handle, self._file = self._file, None
-        if handle is not None:
-            handle.close()
+        with self._guard:
+            sink, self._sink = self._sink, None
+        if sink is not None:
+            sink.close()

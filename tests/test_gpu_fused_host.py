@@ -89,7 +89,7 @@ def test_fused_store_writes_chunks_bit_exact(layout, transfer):
     for l in range(L):
         writer.save_layer(l, layers[l], [request])
     writer.wait_for_save()
-    segs = writer._save_segments["a"]
+    segs = writer._chunk_ids["a"]
     assert [s for s, _ in segs] == [0, 256, 512]
     for start, sid in segs:
         assert store.is_committed(sid)
@@ -121,7 +121,7 @@ def test_fused_store_then_load_round_trip(order, zero_copy):
     writer.save_layer(0, layers[0], [RequestMetadata("a", list(range(1024)), slots, None, True, 1024)])
     writer.save_layer(1, layers[1], [RequestMetadata("a", list(range(1024)), slots, None, True, 1024)])
     writer.wait_for_save()
-    segs = writer._save_segments["a"]
+    segs = writer._chunk_ids["a"]
     src = (3, 1) if order == "apart" else (1, 2)  # chunks 1 and 2 sit in consecutive slots
     blend = [BlendSegment(segs[src[0]][1], 260), BlendSegment(segs[src[1]][1], 700)]
     store.pin("b", blend)

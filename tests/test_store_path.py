@@ -94,7 +94,7 @@ def test_wait_for_save_synchronizes_single_store_stream():
     w = _writer(RecordingStore())
     w.wait_for_save()
     assert w._store_stream.synchronize_calls == 1
-    assert w._save_futures == set()
+    assert not w._inflight
     w.close()
 
 
@@ -127,7 +127,7 @@ def test_enqueue_store_reuses_staging_and_offloads_on_one_stream(monkeypatch):
     # host would otherwise upload it next to the fake cache)
     monkeypatch.setattr(w, "_upload_slots", lambda _rid, slots, _kv: slots)
     w._enqueue_store_batch([("segment", 0, 4)], object(), torch.arange(4), request_id="request")
-    first_staging = w._store_staging_by_request["request"]
+    first_staging = w._staging.live["request"]
     w._enqueue_store_batch([("segment", 1, 4)], object(), torch.arange(4), request_id="request")
     w.wait_for_save()
     w.close()
@@ -137,7 +137,7 @@ def test_enqueue_store_reuses_staging_and_offloads_on_one_stream(monkeypatch):
     assert streams.events[0].recorded_on is w._store_stream
     assert streams.events[0].synchronize_calls == 1
     assert outputs[0] is None and outputs[1] is first_staging
-    assert w._store_staging_by_request == {}
+    assert w._staging.live == {} and w._staging.retired == []
     assert torch.equal(store.layers[0][2], gathered[0])
     assert torch.equal(store.layers[1][2], gathered[1])
     assert any(e == "save_store_wait_finished" and r == "request" and f["stores"] == 2
@@ -149,12 +149,14 @@ def test_async_publish_aborts_the_whole_segment_on_failure(monkeypatch):
     store = RecordingStore()
     w = _writer(store)
 
-    def fail(_pending, _host):
+    def fail(_batch, _kept):
         raise RuntimeError("publication failed")
 
-    monkeypatch.setattr(w, "_publish_host_batch", fail)
-    assert not w._publish_after_event(RecordingEvent(), [("segment-a", 3, 2), ("segment-b", 3, 2)],
-                                      torch.arange(8).reshape(2, 4))
+    monkeypatch.setattr(w, "_put_chunks", fail)
+    batch = SP._StoreBatch("r", [("segment-a", 3, 2), ("segment-b", 3, 2)],
+                           torch.arange(8).reshape(2, 4), RecordingEvent())
+    assert not w._publish(batch)
+    assert batch.ready.synchronize_calls == 1
     assert store.aborted == ["segment-a", "segment-b"]
     w.close()
 
@@ -163,7 +165,9 @@ def test_publication_uses_views_of_the_pinned_batch():
     store = RecordingStore()
     w = _writer(store)
     host = torch.arange(2 * 8 * 3).reshape(2, 8, 3)
-    w._publish_host_batch([("a", 0, 4), ("b", 0, 4)], host)
+    kept = [None, None]
+    assert w._put_chunks(SP._StoreBatch("r", [("a", 0, 4), ("b", 0, 4)], host), kept)
+    assert kept == [False, False]  # the recording store cannot say it holds them
     (_, _, first), (_, _, second) = store.layers
     assert first.data_ptr() == host.data_ptr()
     assert torch.equal(second, host[:, 4:8])
@@ -234,8 +238,20 @@ def test_save_layer_fuses_pending_chunks_and_aborts_on_error(monkeypatch):
     w.close()
 
 
-def test_thread_safety_of_save_slots():
-    # the semaphore bounds in-flight batches; releases come from futures
-    w = _writer(RecordingStore())
-    assert isinstance(w._save_slots, threading.Semaphore)
-    w.close()
+def test_inflight_saves_bound_and_release():
+    # the limit bounds batches in flight; a slot frees when its future completes
+    from concurrent.futures import Future
+
+    inflight = SP._InflightSaves(2)
+    futures = [Future(), Future()]
+    for f in futures:
+        inflight.admit()
+        inflight.track("r", f)
+    blocked = threading.Thread(target=inflight.admit)
+    blocked.start()
+    blocked.join(0.05)
+    assert blocked.is_alive()          # third admission waits ...
+    futures[0].set_result(True)
+    blocked.join(2)
+    assert not blocked.is_alive()      # ... until a publication finishes
+    assert inflight and list(inflight.take()) == ["r"] and not inflight
