@@ -3,7 +3,8 @@
 Same field names, defaults and validation errors as the reference
 ``CacheBlendConfig`` (cacheblend_vllm/config.py:10-96), so an existing
 ``kv_connector_extra_config`` JSON loads unchanged; unknown fields are an
-error there and here.
+error there and here. One field is added: ``load_staging_layers``, the depth
+of the loader's device ring of hit stagings.
 """
 
 from __future__ import annotations
@@ -37,6 +38,9 @@ class CacheBlendConfig:
     strict_version_check: bool = True
     ipc_root: str = "/tmp/cacheblend-v1"
     model_scope: str | None = None
+    # MI355X loader: layers of hit staging one request's DMA ring holds on
+    # the device (at least 2; not in the reference, which stages one layer)
+    load_staging_layers: int = 4
 
     @classmethod
     def from_extra_config(cls, values: dict[str, Any] | None) -> "CacheBlendConfig":
@@ -81,6 +85,7 @@ class CacheBlendConfig:
             (self.tail_query_tokens >= 0, "tail_query_tokens cannot be negative"),
             (self.selection_strategy == "kv_deviation" or self.tail_query_tokens > 0,
              "Sparse-Q selection requires tail_query_tokens > 0"),
+            (self.load_staging_layers >= 2, "load_staging_layers must be at least 2"),
         )
         for ok, message in checks:
             if not ok:

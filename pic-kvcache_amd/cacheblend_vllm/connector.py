@@ -3,11 +3,13 @@
 Keeps the reference connector's class name, constructor and worker-side
 methods (cacheblend_vllm/connector.py:75-568) for the KV data path:
 
-  register_kv_caches   layer order, pinned chunk store, Store/Load streams
+  register_kv_caches   layer order, pinned chunk store, Store/Load streams,
+                       the layerwise executor of the engine's registered
+                       model (``registry.get_model`` / ``build_executor``)
   save_kv_layer        Store-stream gather + pinned D2H + async publication
   wait_for_save        the Store-completion / publication boundary
-  start_load_kv        PagedBlendLoader + the registered layerwise executor,
-                       failure policy ``kv_load_failure_policy=recompute``
+  start_load_kv        PagedBlendLoader + the executor, failure policy
+                       ``kv_load_failure_policy=recompute``
   get_finished, get_block_ids_with_load_errors, close
 
 The scheduler half (lookup RPC, matcher, plan gating, metadata building)
@@ -19,10 +21,12 @@ kernels consume) is provided in ``store_path``.
 from __future__ import annotations
 
 import re
+import time
 from typing import Any
 
 import torch
 
+from . import registry
 from .config import CacheBlendConfig
 from .host_store import PinnedChunkSlab, PinnedChunkStore
 from .kv_layout import kv_planes
@@ -41,7 +45,14 @@ try:  # vLLM's connector base when vLLM is installed
         KVConnectorBase_V1 as _Base,
         KVConnectorRole,
     )
+
+    try:  # hybrid-memory-allocator support marker (reference connector.py:13-18, 75)
+        from vllm.distributed.kv_transfer.kv_connector.v1.base import SupportsHMA as _HMA  # type: ignore
+    except ImportError:
+        _HMA = object
 except ImportError:  # vLLM absent: a minimal stand-in with the same role enum
+    _HMA = object
+
     import enum
 
     class KVConnectorRole(enum.Enum):  # type: ignore[no-redef]
@@ -74,8 +85,15 @@ def _layer_sort_key(name: str) -> tuple[int, str]:
     return (int(matches[-1]) if matches else 1 << 30, name)
 
 
-class CacheBlendConnectorV1(_Base):
+class CacheBlendConnectorV1(_Base, *(() if _HMA is object else (_HMA,))):
     """CacheBlend KV connector (worker data path on MI355X)."""
+
+    @classmethod
+    def requires_piecewise_for_cudagraph(cls, extra_config: dict[str, Any]) -> bool:
+        """Reference connector.py:78-83: only storing the decode cache needs
+        Python between graph pieces (its save runs per layer during decode);
+        prompt-only stores run outside decode graph replay."""
+        return bool(extra_config.get("save_decode_cache", False))
 
     def __init__(self, vllm_config, role, kv_cache_config=None):
         super().__init__(vllm_config, role, kv_cache_config)
@@ -101,10 +119,11 @@ class CacheBlendConnectorV1(_Base):
 
     # ---------------------------------------------------------- worker
 
-    def register_kv_caches(self, kv_caches: dict[str, Any], executor=None) -> None:
-        """Reference connector.py:168-213 (``executor``: the layerwise model
-        executor whose ``run(request_id, tokens, plan, loader)`` drives the
-        loader; the model forward itself is outside this package)."""
+    def register_kv_caches(self, kv_caches: dict[str, Any]) -> None:
+        """Reference connector.py:168-213. The layerwise executor comes from
+        the model registered for this engine (``registry.get_model``, as the
+        reference does at :205-206) through ``registry.build_executor``; its
+        ``run(request_id, tokens, plan, loader)`` drives the loader."""
         if self.role is not KVConnectorRole.WORKER:
             return
         ordered = sorted(kv_caches.items(), key=lambda item: _layer_sort_key(item[0]))
@@ -113,6 +132,8 @@ class CacheBlendConnectorV1(_Base):
         if not self._kv_caches:
             raise RuntimeError("CacheBlendConnectorV1 received no KV caches")
         key, _ = kv_planes(self._kv_caches[0])
+        executor = registry.build_executor(registry.get_model(self.engine_id), self.config,
+                                           self.block_size)
         # chunks live in pinned slab slots (one pinned arena per 128 chunks,
         # bounded by the store's byte cap) instead of a fresh pinned batch per
         # layer; slots go back to the slab when the store drops a segment
@@ -170,19 +191,46 @@ class CacheBlendConnectorV1(_Base):
         for request in metadata.requests:
             if request.plan is None:
                 continue
+            self._blend_one(forward_context, request)
+
+    def _blend_one(self, forward_context: Any, request: RequestMetadata) -> None:
+        """Load and blend one planned request. The executor may move the
+        forward context's per-layer cursors (``layer_idx``,
+        ``moe_layer_index``); they are put back afterwards. The request's
+        pins are released with the loader's last host-read event, so chunks
+        the store drops meanwhile are not reused under an in-flight copy."""
+        plan = request.plan
+        trace = self._trace.enabled
+        started = time.monotonic_ns() if trace else 0
+        if trace:
+            self._trace.emit("blend_started", request_id=request.request_id,
+                             apc_prefix_tokens=plan.apc_prefix_tokens,
+                             allocation_tokens=plan.allocation_tokens, hit_tokens=plan.hit_tokens,
+                             gap_tokens=plan.gap_tokens, segments=len(plan.segments))
+        saved = {name: getattr(forward_context, name) for name in ("moe_layer_index", "layer_idx")
+                 if hasattr(forward_context, name)}
+        loader = None
+        failure = None
+        try:
             loader = PagedBlendLoader(
-                self._kv_caches, self._store, request.request_id, request.plan,
+                self._kv_caches, self._store, request.request_id, plan,
                 request.slot_mapping, self.block_size, self.config, tracer=self._trace,
                 load_stream=self._load_stream,
             )
-            try:
-                self._executor.run(request.request_id, request.token_ids, request.plan, loader)
-            except Exception:
-                self._record_load_error(request)
-                if not self._recompute_on_failure:
-                    raise
-            finally:
-                self._store.release(request.request_id)
+            self._executor.run(request.request_id, request.token_ids, plan, loader)
+        except Exception as error:
+            failure = type(error).__name__
+            self._record_load_error(request)
+            if not self._recompute_on_failure:
+                raise
+        finally:
+            for name, value in saved.items():
+                setattr(forward_context, name, value)
+            self._store.release(request.request_id,
+                                loader.host_reads_done() if loader is not None else None)
+            if trace:
+                self._trace.emit("blend_finished", request_id=request.request_id,
+                                 duration_us=(time.monotonic_ns() - started) / 1000, error=failure)
 
     def get_finished(self, finished_req_ids: set[str]):
         if self._writer is not None:
@@ -230,3 +278,6 @@ class CacheBlendConnectorV1(_Base):
 
     def request_finished(self, request, block_ids):
         return self._control_plane("request_finished")
+
+    def request_finished_all_groups(self, request, block_ids):
+        return self._control_plane("request_finished_all_groups")

@@ -45,6 +45,9 @@ class _Entry:
     failed: bool = False
     # layer -> in-place address of the stored chunk (see chunk_address)
     addresses: dict[int, tuple | None] = field(default_factory=dict)
+    # GPU events of loads that read this entry's host memory: the memory is
+    # handed back (on_release) only together with them
+    read_events: list = field(default_factory=list)
 
 
 def chunk_address(t: torch.Tensor) -> tuple | None:
@@ -101,11 +104,11 @@ class PinnedChunkSlab:
     def _reclaim(self) -> None:
         keep = []
         lib = _native.load()
-        for ptr, event in self._pending:
-            if event is None or event.query():
+        for ptr, events in self._pending:
+            if all(e.query() for e in events):
                 _native.check(lib.cbk_slab_free(self._handle, ptr), "slab free")
             else:
-                keep.append((ptr, event))
+                keep.append((ptr, events))
         self._pending = keep
 
     def alloc(self) -> torch.Tensor:
@@ -143,8 +146,13 @@ class PinnedChunkSlab:
             return out
 
     def free(self, tensor: torch.Tensor, event=None) -> None:
+        """Give a slot back. ``event`` (a GPU event, or a sequence of them)
+        marks the last GPU access: the slot is reused only once every one
+        of them has completed."""
+        events = tuple(e for e in (event if isinstance(event, (list, tuple)) else (event,))
+                       if e is not None)
         with self._lock:
-            self._pending.append((tensor.data_ptr(), event))
+            self._pending.append((tensor.data_ptr(), events))
             self._reclaim()
 
     def stats(self) -> dict[str, int]:
@@ -163,12 +171,13 @@ class PinnedChunkSlab:
 
 class PinnedChunkStore:
     def __init__(self, chunk_size: int, max_bytes: int,
-                 on_release: Callable[[torch.Tensor], None] | None = None):
+                 on_release: Callable[[torch.Tensor, tuple], None] | None = None):
         if max_bytes <= 0:
             raise ValueError("max_bytes must be positive")
         self.chunk_size = int(chunk_size)
         self.max_bytes = int(max_bytes)
         # called with every layer tensor the store drops (e.g. slab slots)
+        # and the GPU events of loads that may still read it (see release)
         self._on_release = on_release
         # least recently used first (reference storage.py:42, 273-275)
         self._entries: OrderedDict[SegmentId, _Entry] = OrderedDict()
@@ -314,7 +323,7 @@ class PinnedChunkStore:
                 return None
             entry.reserved.discard(layer_id)
             if previous is not None and self._on_release is not None:
-                self._on_release(previous)
+                self._on_release(previous, tuple(entry.read_events))
             entry.layers[layer_id] = cpu_tensor
             entry.addresses.pop(layer_id, None)
             entry.size_bytes += growth
@@ -380,7 +389,11 @@ class PinnedChunkStore:
                 self._pin_sets[request_id] = frozenset(self._pins[request_id])
             return tuple(valid)
 
-    def release(self, request_id: str) -> None:
+    def release(self, request_id: str, event=None) -> None:
+        """Drop ``request_id``'s pins. ``event``: a GPU event recorded after
+        the request's last read of the pinned chunks (a load still in
+        flight); chunks dropped later keep it, so their host memory is not
+        reused before the read completes."""
         with self._lock:
             self._pin_sets.pop(request_id, None)
             self._pin_entries.pop(request_id, None)
@@ -388,6 +401,9 @@ class PinnedChunkStore:
                 entry = self._entries.get(sid)
                 if entry is not None:
                     entry.pins = max(0, entry.pins - 1)
+                    if event is not None:
+                        entry.read_events = [e for e in entry.read_events if not e.query()]
+                        entry.read_events.append(event)
             self._evict(0)
 
     def get_layer(self, request_id: str, segment: BlendSegment, layer_id: int) -> torch.Tensor:
@@ -460,10 +476,12 @@ class PinnedChunkStore:
 
     def _release_layers(self, entry: _Entry) -> None:
         if self._on_release is not None:
+            events = tuple(entry.read_events)
             for tensor in entry.layers.values():
-                self._on_release(tensor)
+                self._on_release(tensor, events)
         entry.layers.clear()
         entry.addresses.clear()
+        entry.read_events.clear()
 
     def _evict(self, required_bytes: int, exclude: SegmentId | None = None) -> None:
         """Drop least recently used committed, unpinned segments until

@@ -123,7 +123,7 @@ class PagedBlendLoader:
         zero_copy: bool | str = "auto",
         max_workgroups: int = 256,
         dma_min_run_bytes: int = 1 << 20,
-        dma_staging_bytes: int = 1 << 30,
+        dma_staging_layers: int | None = None,
     ):
         """How hit rows cross the host link, per layer:
         DMA -- the chunks, coalesced into runs where adjacent in host
@@ -137,9 +137,12 @@ class PagedBlendLoader:
         DMA, "auto" reads in place only when the DMA commands would average
         fewer than ``dma_min_run_bytes`` each, where per-command DMA cost
         (about 9 us, the time of 0.5 MB) dominates.
-        ``dma_staging_bytes`` bounds the device ring the DMA fills (at least
-        two layers' hits): with room for every layer the copies of a request
-        never wait for an assembly."""
+        ``dma_staging_layers`` (default ``config.load_staging_layers``, 4):
+        layers of hits the device ring the DMA fills holds (at least 2, at
+        most the layer count). The host refills a slot only after the
+        assembly that read it, so the copies run at most that many layers
+        ahead of the assemblies; the ring costs that many layers' hit bytes
+        of device memory per request (C3-shaped: 57 MB a layer)."""
         if zero_copy not in (True, False, "auto"):
             raise ValueError("zero_copy must be True, False or 'auto'")
         self.kv_caches = kv_caches
@@ -179,14 +182,18 @@ class PagedBlendLoader:
         self._events: dict[int, torch.cuda.Event] = {}
         self._reuse_events: dict[int, torch.cuda.Event] = {}
         self._staging: list[torch.Tensor] = []
-        # ring of hit stagings, one slot per layer up to dma_staging_bytes:
-        # the copy stream carries no cross-stream waits (a wait between two
-        # DMA copies on one stream left the engine idle ~50-100 us per
-        # layer); the host fences a slot's reuse (_hit_free) only when the
-        # ring wraps
+        # ring of hit stagings, dma_staging_layers slots: the copy stream
+        # carries no cross-stream waits (a wait between two DMA copies on
+        # one stream left the engine idle ~50-100 us per layer); the host
+        # fences a slot's reuse (_hit_free) when the ring wraps
         self._hit_ring: torch.Tensor | None = None
         self._hit_free: dict[int, torch.cuda.Event] = {}
-        self._dma_staging_bytes = int(dma_staging_bytes)
+        layers = config.load_staging_layers if dma_staging_layers is None else int(dma_staging_layers)
+        if layers < 2:
+            raise ValueError("dma_staging_layers must be at least 2")
+        self._ring_layers = layers
+        # the last GPU event after which this loader reads no host memory
+        self._host_reads: torch.cuda.Event | None = None
         self._copy_stream: torch.cuda.Stream | None = None
         self._descs: dict[int, _native.KVDesc] = {}
         self._zero_copy = zero_copy
@@ -261,8 +268,7 @@ class PagedBlendLoader:
         stream that fills it (the copy stream when there is one) and kept
         alive for the Load stream that reads it."""
         if self._hit_ring is None:
-            per_layer = 2 * self.plan.hit_tokens * self._row_bytes
-            slots = max(2, min(len(self.kv_caches), self._dma_staging_bytes // max(1, per_layer)))
+            slots = max(2, min(len(self.kv_caches), self._ring_layers))
             shape = (slots, 2, self.plan.hit_tokens, *self.row_shape)
             if self._copy_stream is not None:
                 with torch.cuda.stream(self._copy_stream):
@@ -423,12 +429,18 @@ class PagedBlendLoader:
 
         if self._load_stream is None:
             load()
+            if self.plan.segments:
+                self._host_reads = torch.cuda.Event()
+                self._host_reads.record(torch.cuda.current_stream(self.device))
         else:
             with torch.cuda.stream(self._load_stream):
                 load()
                 event = torch.cuda.Event()
                 event.record(self._load_stream)
                 self._events[layer_id] = event
+            if self.plan.segments:
+                # the Load stream ran this layer's assembly after its copies
+                self._host_reads = event
         if trace:
             self.tracer.emit(
                 "layer_prefetch_enqueued",
@@ -436,6 +448,14 @@ class PagedBlendLoader:
                 layer_id=layer_id,
                 duration_us=(time.monotonic_ns() - started) / 1000,
             )
+
+    def host_reads_done(self) -> torch.cuda.Event | None:
+        """GPU event after which no load enqueued so far reads the store's
+        host memory (hit copies and in-place reads both complete before the
+        Load stream passes it); None when nothing was read. The connector
+        hands it to ``store.release`` so chunks evicted afterwards are not
+        reused while a copy may still read them."""
+        return self._host_reads
 
     def get(self, layer_id: int) -> torch.Tensor:
         """The layer's buffer, ordered after its load (ascend.py:372-383)."""

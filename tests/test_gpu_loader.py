@@ -215,9 +215,8 @@ def test_loader_dma_ring_wraps_bit_exact(ring_slots):
     layers, store, plan, slots, hosts = _blend_setup(L, 200, bs, heads, dim, 37, segs, 700,
                                                      torch.bfloat16, chunk, seed=11)
     rope = Rope(dim, 2048, True)
-    per_layer = 2 * plan.hit_tokens * heads * dim * 2
     loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk),
-                              zero_copy=False, dma_staging_bytes=ring_slots * per_layer)
+                              zero_copy=False, dma_staging_layers=ring_slots)
     cache = rope.cos_sin_cache.cpu().numpy()
 
     def reloc(old, new, k_bits):

@@ -12,7 +12,7 @@ import torch
 from types import SimpleNamespace
 
 import oracle as O
-from cacheblend_vllm import synthetic
+from cacheblend_vllm import registry, synthetic
 from cacheblend_vllm.config import CacheBlendConfig
 from cacheblend_vllm.connector import CacheBlendConnectorV1, KVConnectorRole
 from cacheblend_vllm.host_store import PinnedChunkStore
@@ -49,7 +49,7 @@ def test_save_then_blend_load_round_trip():
     for l in range(L):
         writer.save_layer(l, layers[l], [request])
     writer.wait_for_save()
-    segs = writer._save_segments["a"]
+    segs = writer._chunk_ids["a"]
     assert [s for s, _ in segs] == [0, 256, 512, 768]
     for start, sid in segs:
         assert store.is_committed(sid)
@@ -112,14 +112,16 @@ def test_connector_worker_save_and_load_with_failure_policy():
             raise RuntimeError("model failure")
 
     executor = Executor()
-    conn.register_kv_caches(layers, executor=executor)
+    registry.clear_for_test()
+    registry.register_model("e", executor)
+    conn.register_kv_caches(layers)
     slots = synthetic.block_slots(torch.arange(8), 16, 128)
     req = RequestMetadata("r", list(range(128)), slots, None, True, 128)
     conn.bind_connector_metadata(CacheBlendConnectorMetadata([req]))
     for name in layers:
         conn.save_kv_layer(name, layers[name], None)
     conn.wait_for_save()
-    segs = conn._writer._save_segments["r"]
+    segs = conn._writer._chunk_ids["r"]
     assert all(conn._store.is_committed(sid) for _, sid in segs)
     # a failing load reports exactly the blocks of the external span
     plan = BlendPlan(16, 128, 64, (BlendSegment(segs[1][1], 64),))
@@ -132,3 +134,4 @@ def test_connector_worker_save_and_load_with_failure_policy():
     with pytest.raises(NotImplementedError, match="control plane"):
         conn.build_connector_meta(None)
     conn.close()
+    registry.clear_for_test()

@@ -35,7 +35,7 @@ def test_commit_after_all_layers_and_known_hash():
 
 def test_lru_eviction_skips_pinned_and_uncommitted_then_fails_closed():
     released = []
-    store = PinnedChunkStore(CH, 3 * CHUNK_BYTES, on_release=released.append)
+    store = PinnedChunkStore(CH, 3 * CHUNK_BYTES, on_release=lambda t, events: released.append(t))
     a, _ = _put(store, 0)
     b, _ = _put(store, 100)
     c, _ = _put(store, 200)
@@ -57,7 +57,7 @@ def test_lru_eviction_skips_pinned_and_uncommitted_then_fails_closed():
 
 def test_cancel_abort_and_failed_segments_drop_as_a_unit():
     released = []
-    store = PinnedChunkStore(CH, 1 << 20, on_release=released.append)
+    store = PinnedChunkStore(CH, 1 << 20, on_release=lambda t, events: released.append(t))
     sid = store.begin_put("m", 0, list(range(CH)), 2)
     assert store.reserve_layer(sid, 0) and store.reserve_layer(sid, 1)
     assert not store.reserve_layer(sid, 1)         # already in flight
@@ -164,3 +164,36 @@ def test_begin_put_chunks_equals_per_chunk_begin_put():
     assert a.reserve_layers(ids, 1) == [False, False, False]
     with pytest.raises(ValueError, match="outside"):
         a.reserve_layers(ids, 2)
+
+
+class _Event:
+    """A GPU event stand-in whose completion the test controls."""
+
+    def __init__(self, done=False):
+        self.done = done
+
+    def query(self):
+        return self.done
+
+
+def test_release_event_travels_with_evicted_chunks():
+    """A load's last host-read event, given at release, is handed to the
+    release hook with every chunk the store drops afterwards; completed
+    events are pruned when new ones arrive."""
+    released = []
+    store = PinnedChunkStore(CH, 2 * CHUNK_BYTES, on_release=lambda t, ev: released.append((t, ev)))
+    a, _ = _put(store, 0)
+    b, _ = _put(store, 100)
+    store.pin("r", [BlendSegment(a, 0), BlendSegment(b, 0)])
+    old, live = _Event(done=True), _Event()
+    store.release("r", old)
+    store.pin("s", [BlendSegment(a, 0)])
+    store.release("s", live)                       # a: the completed event is pruned
+    assert store._entries[a].read_events == [live]
+    assert store._entries[b].read_events == [old]
+    _put(store, 200)                               # evicts b (pinning "s" touched a)
+    _put(store, 300)                               # evicts a
+    assert [ev for _, ev in released] == [(old,), (live,)]
+    assert store.current_bytes == 2 * CHUNK_BYTES
+    store.clear()                                  # entries never read: no events
+    assert [ev for _, ev in released[2:]] == [(), ()]
