@@ -370,13 +370,17 @@ def sparse_q(torch, S, synthetic, dev):
         selected, stats = sel.sparse_q_select(query, key, absolute, gap, scale, 1)
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) / 3 * 1e3
-    achieved = 2 * flops_pass / (ms / 1e3) / 1e12
+    # algorithmic work: one Q.K^T over the unmasked logits (2 D Hq sum(pos+1));
+    # the kernel pair computes the logits twice (row statistics, then column
+    # sums), reported separately as executed work
+    achieved = flops_pass / (ms / 1e3) / 1e12
     return {
         "queries": nq, "keys": nk, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
         "score_ms": round(ms, 3),
-        "flops_per_pass": flops_pass,
-        "two_pass_TFLOPs": round(achieved, 1),
+        "algorithmic_flops": flops_pass,
+        "TFLOPs": round(achieved, 1),
         "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4),
+        "executed_two_pass_TFLOPs": round(2 * achieved, 1),
         "exp_per_s": round(2 * hq * float((pos + 1).sum()) / (ms / 1e3), 1),
         "select_total_ms_with_masks_and_sync": round(total_ms, 3),
         "selected": int(selected.numel()),
@@ -464,7 +468,7 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
         writer.wait_for_save()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        committed = sum(store.is_committed(sid) for _, sid in writer._save_segments[request.request_id])
+        committed = sum(store.is_committed(sid) for _, sid in writer._chunk_ids[request.request_id])
         writer.close()
         store.clear()
         return elapsed, committed
@@ -512,7 +516,7 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     for l in range(L):
         writer.save_layer(l, layers[l], [request])
     writer.wait_for_save()
-    segments = [BlendSegment(sid, start) for start, sid in writer._save_segments["reload"]]
+    segments = [BlendSegment(sid, start) for start, sid in writer._chunk_ids["reload"]]
     store.pin("reload", segments)
     chunks = [[store.get_layer("reload", seg, l) for seg in segments] for l in range(L)]
 
@@ -557,6 +561,23 @@ def _sleep_cycles_per_us(torch) -> float:
     return 20_000_000 / (e0.elapsed_time(e1) * 1e3)
 
 
+def _c3_segments(allocation_end: int = 32767, apc: int = 2048) -> list[tuple[int, int, int]]:
+    """The Qwen3-30B-A3B blend-load plan: 12 reused segments of 256-token
+    multiples after the APC prefix, separated by 1-511-token gaps, the rest of
+    the span a trailing gap. Returns (source_start, target_start, length)."""
+    rng = np.random.default_rng(0)
+    gaps = rng.integers(1, 512, 12)
+    chunks_total = (allocation_end - apc - int(gaps.sum())) // 256
+    lens = 1 + rng.multinomial(chunks_total - 12, np.full(12, 1 / 12))
+    segs, pos, src = [], apc, 0
+    for g, m in zip(gaps, lens):
+        pos += int(g)
+        segs.append((src, pos, 256 * int(m)))
+        src += 256 * int(m) + 512
+        pos += 256 * int(m)
+    return segs
+
+
 def blend_load(torch, synthetic, dev, args):
     """Qwen3-30B-A3B blend load: 48 layers, 4 KV heads x 128 bf16, 16-token
     blocks; 32768-token prompt, 2048-token APC prefix, 12 reused segments of
@@ -577,16 +598,7 @@ def blend_load(torch, synthetic, dev, args):
     from cacheblend_vllm.types import BlendPlan, BlendSegment
 
     L, BS, H, D, A, APC = 48, 16, 4, 128, 32767, 2048
-    rng = np.random.default_rng(0)
-    gaps = rng.integers(1, 512, 12)
-    chunks_total = (A - APC - int(gaps.sum())) // 256
-    lens = 1 + rng.multinomial(chunks_total - 12, np.full(12, 1 / 12))
-    segs, pos, src = [], APC, 0
-    for g, m in zip(gaps, lens):
-        pos += int(g)
-        segs.append((src, pos, 256 * int(m)))
-        src += 256 * int(m) + 512
-        pos += 256 * int(m)
+    segs = _c3_segments(A, APC)
     hit = sum(n for _, _, n in segs)
     nb = (A + BS - 1) // BS + 8
     layers = [synthetic.paged_pool(nb, BS, H, D, torch.bfloat16, dev, seed=100 + l) for l in range(L)]
@@ -905,13 +917,62 @@ def _kdev_async(torch, S, fresh, cached, gap):
 _kdev_async.scores = None
 
 
+def _host_cpu() -> dict:
+    """Host CPU identity from /proc/cpuinfo and the threads this process may use."""
+    fields = {}
+    logical = 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key == "processor":
+                    logical += 1
+                elif key in ("model name", "vendor_id", "cpu family", "model", "stepping") and key not in fields:
+                    fields[key] = value.strip()
+    except OSError:
+        pass
+    name = fields.get("model name", "unknown")
+    model = (f"{name} (vendor {fields.get('vendor_id', '?')}, family {fields.get('cpu family', '?')}, "
+             f"model {fields.get('model', '?')}, stepping {fields.get('stepping', '?')})")
+    affinity = len(os.sched_getaffinity(0))
+    return {"cpu_model": model, "host_cpu_count": os.cpu_count(), "cpuinfo_processors": logical,
+            "affinity_cpus": affinity}
+
+
+def _median_time(fn, min_runs: int, max_runs: int, budget_s: float) -> tuple[float, int]:
+    for _ in range(2):  # warm-up
+        fn()
+    times = []
+    stop = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < stop and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(torch, synthetic):
-    """The reference's torch path on the host cores, on a bounded sample:
-    4 of the 36 layers (full 8192-token prompt) gathered and scattered back."""
+    """The reference's torch path (the build's restatement in
+    oracle/torch_cpu_path.py, pinned against the oracle) on the host cores,
+    on bounded samples of each workload:
+      C2 (headline): 4 of 36 layers of the 8192-token prompt gathered and
+          scattered back with advanced indexing / index_put_;
+      C1: the fp32 plumbing case end to end;
+      C3: 2 of 48 layers of the blend load (APC gather, gap zeroing, per
+          segment plane copies, bf16 K relocation, index scatter, commit);
+      C4: K-deviation scores + top-k selection over 65,536 tokens;
+      C5: 16 of the 512 eight-query chunks of the Sparse-Q loop (the
+          reference's loop is dense over the whole key context, so a chunk
+          costs the same wherever it sits), scaled to all 512."""
     sys.path.insert(0, ROOT)
     from oracle import torch_cpu_path as ref
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    host = _host_cpu()
+    # the box allots each GPU job a share of the host (OMP_NUM_THREADS);
+    # without one, every CPU this process may run on
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(host["affinity_cpus"], share) if share > 0 else host["affinity_cpus"]
     torch.set_num_threads(threads)
     NB, BS, H, D, T, LS = 4096, 16, 8, 128, 8192, 4
     # filled (not torch.zeros, whose untouched pages all map the shared zero
@@ -922,51 +983,97 @@ def cpu_baseline(torch, synthetic):
     src = synthetic.block_slots(perm[:512], BS, T)
     dst = synthetic.block_slots(perm[512:1024], BS, T)
 
-    def run():
+    def c2():
         for layer in layers:
             chunk = ref.gather(layer, src, BS).contiguous()
             ref.scatter(chunk, layer, dst, BS)
 
-    for _ in range(2):
-        run()
-    times = []
-    budget = time.perf_counter() + 15.0
-    while len(times) < 10 or (time.perf_counter() < budget and len(times) < 40):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > budget + 15.0:
-            break
-    med = statistics.median(times)
-    nbytes = 4 * LS * 2 * T * H * D * 2
-    value = nbytes / med / 1e9
-    # K-deviation selection at 65,536 tokens on the host
+    med, runs = _median_time(c2, 10, 40, 15.0)
+    value = 4 * LS * 2 * T * H * D * 2 / med / 1e9
+    del layers
+    log(f"cpu baseline C2: {value:.2f} GB/s on {threads} threads")
+
+    # C1: fp32 separate K/V [64, 16, 2, 64], 512 tokens -> two 256-token chunks
+    # -> scatter to a fresh permutation; K-deviation top 15% over the 512 tokens
+    g1 = torch.Generator().manual_seed(0)
+    k1, v1 = torch.randn(64, 16, 2, 64, generator=g1), torch.randn(64, 16, 2, 64, generator=g1)
+    kv1 = torch.stack((k1, v1))
+    s1 = synthetic.block_slots(torch.randperm(64, generator=g1)[:32], 16, 512)
+    d1 = synthetic.block_slots(torch.randperm(64, generator=g1)[:32], 16, 512)
+    noisy = torch.randperm(512, generator=g1)[:51]
+    gap1 = torch.zeros(512, dtype=torch.bool)
+
+    def c1():
+        chunks = [ref.gather(kv1, s1[i:i + 256], 16).contiguous() for i in (0, 256)]
+        for i, c in zip((0, 256), chunks):
+            ref.scatter(c, kv1, d1[i:i + 256], 16)
+        cached = torch.cat([c[0] for c in chunks]).reshape(512, 128)
+        fresh = cached.clone()
+        fresh[noisy] += 0.05
+        ref.select(ref.kdev_scores(fresh, cached), gap1, 0.15)
+
+    c1_med, _ = _median_time(c1, 10, 200, 2.0)
+
+    # C3: 2 sampled layers of the 48-layer blend load
+    A, APC, H3 = 32767, 2048, 4
+    segs = _c3_segments(A, APC)
+    hit = sum(n for _, _, n in segs)
+    nb3 = (A + BS - 1) // BS + 8
+    pages3 = [torch.full((2, nb3, BS, H3, D), 0.5 * (i + 1), dtype=torch.bfloat16) for i in range(2)]
+    slots3 = synthetic.block_slots(torch.randperm(nb3, generator=g)[: (A + BS - 1) // BS], BS, A)
+    hosts3 = [[(s0, t0, torch.full((2, n, H3, D), 0.25 * (i + 1), dtype=torch.bfloat16)) for s0, t0, n in segs]
+              for i in range(2)]
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ang = torch.arange(65536, dtype=torch.float32)[:, None] * inv
+    rope_cache = torch.cat([ang.cos(), ang.sin()], -1)
+    bufs = [torch.empty((2, A, H3, D), dtype=torch.bfloat16) for _ in range(2)]
+
+    def c3():
+        for i in range(2):
+            ref.blend_load_layer(pages3[i], slots3, BS, APC, A, hosts3[i], rope_cache, D, True, bufs[i])
+
+    c3_med, c3_runs = _median_time(c3, 3, 10, 10.0)
+    c3_layer_s = c3_med / 2
+    del pages3, hosts3, bufs
+    log(f"cpu baseline C3: {c3_layer_s * 1e3:.1f} ms per layer")
+
+    # C4: K-deviation selection at 65,536 tokens
     fresh, cached, gap = synthetic.kdev_inputs(65536, 4, 128, torch.bfloat16, "cpu", seed=0)
-    ktimes = []
-    for i in range(8):
-        t0 = time.perf_counter()
-        scores = ref.kdev_scores(fresh, cached)
-        ref.select(scores, gap, 0.15, ref.dilate(gap, 16))
-        if i >= 2:
-            ktimes.append(time.perf_counter() - t0)
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    c4_med, _ = _median_time(lambda: ref.select(ref.kdev_scores(fresh, cached), gap, 0.15,
+                                                ref.dilate(gap, 16)), 6, 20, 5.0)
+    del fresh, cached, gap
+
+    # C5: 16 of 512 eight-query chunks over the 98,304-key context
+    nk, hq, hkv = 98304, 32, 4
+    g5 = torch.Generator().manual_seed(0)
+    key5 = (torch.randn((nk, hkv, D), generator=g5) / D ** 0.5).to(torch.bfloat16)
+    qpos = torch.from_numpy(np.flatnonzero(synthetic.sparse_q_layout(nk, 4096, seed=0)))
+    picks = torch.linspace(0, 511, 16).long()
+    sample_pos = torch.cat([qpos[8 * c: 8 * c + 8] for c in picks.tolist()])
+    q5 = (torch.randn((sample_pos.numel(), hq, D), generator=g5) / D ** 0.5).to(torch.bfloat16)
+    c5_med, _ = _median_time(lambda: ref.sparse_q_full_scores(q5, key5, sample_pos, D ** -0.5, 8), 2, 5, 10.0)
+    c5_chunk_s = c5_med / 16
+    log(f"cpu baseline C5: {c5_chunk_s * 1e3:.1f} ms per 8-query chunk")
+
     return {
         "value": round(value, 3),
         "unit": "GB/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "kind": "port",
         "sample": f"4 of 36 layers, 8192-token prompt, gather+scatter with the reference's torch ops "
-                  f"(advanced indexing / index_put_), median of {len(times)} runs",
-        "kdev_select_us_per_64k_tokens": round(statistics.median(ktimes) * 1e6, 1),
-        "cpu_model": cpu,
+                  f"(advanced indexing / index_put_), median of {runs} runs",
+        "threads_note": "threads = the host share this process is given (OMP_NUM_THREADS on the GPU box, "
+                        "else its CPU affinity)",
+        **host,
+        "c1_plumbing_us": round(c1_med * 1e6, 1),
+        "c3_blend_load": {"ms_per_layer": round(c3_layer_s * 1e3, 2),
+                          "hit_GBps": round(hit * 2 * H3 * D * 2 / c3_layer_s / 1e9, 3),
+                          "est_48_layers_ms": round(48 * c3_layer_s * 1e3, 1),
+                          "sample": f"2 of 48 layers, median of {c3_runs} runs"},
+        "kdev_select_us_per_64k_tokens": round(c4_med * 1e6, 1),
+        "c5_sparse_q": {"ms_per_chunk": round(c5_chunk_s * 1e3, 2),
+                        "est_full_ms": round(512 * c5_chunk_s * 1e3, 1),
+                        "sample": "16 of 512 chunks of 8 queries (evenly spaced), scaled x32"},
     }
 
 
