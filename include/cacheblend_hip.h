@@ -248,6 +248,27 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                     int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                     cbk_stream_t stream);
 
+/* Largest n cbk_kdev_select_noalloc accepts. */
+#define CBK_NOALLOC_SELECT_MAX_TOKENS 1048576
+
+/*
+ * cbk_kdev_select without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. The workspace is
+ * a static device array sized for CBK_NOALLOC_SELECT_MAX_TOKENS tokens
+ * (5.04 MiB per GPU, held until the process ends); larger n is rejected
+ * with CBK_ERR_INVALID. The caller passes every input and output. Calls
+ * that overlap on one GPU (concurrent streams) race on the shared array;
+ * calls in sequence do not (each clears the counters it needs).
+ */
+int cbk_kdev_select_noalloc(const void* fresh_dev, int64_t fresh_row_stride_elems,
+                            const void* cached_dev, int64_t cached_row_stride_elems,
+                            int64_t cached_num_rows, const int64_t* cached_rows_dev,
+                            int64_t cached_row0, int64_t n, int64_t width, int32_t dtype,
+                            const uint8_t* gap_dev, const uint8_t* forced_dev, int64_t radius,
+                            double ratio, float* scores_dev, int64_t* out_idx_dev,
+                            int64_t* out_count_dev, cbk_stream_t stream);
+
 /*
  * Blend-buffer assembly for one layer: out_{k,v}[p] for p in [0, num_tokens)
  * from src_map_dev[p] (int32):

@@ -83,6 +83,13 @@ _SIGNATURES = {
             c_vp, c_vp, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp,
         ],
     ),
+    "cbk_kdev_select_noalloc": (
+        ctypes.c_int,
+        [
+            c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32,
+            c_vp, c_vp, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, c_vp,
+        ],
+    ),
     "cbk_dilate": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
     "cbk_blend_assemble": (
         ctypes.c_int,

@@ -20,6 +20,8 @@
 // the zero launch is skipped there)
 // Every tile is 2048 consecutive tokens (8 per thread), so tile order is
 // index order and ties resolve to the lower index deterministically.
+#include <mutex>
+
 #include "cbk_common.hpp"
 
 namespace cbk {
@@ -177,8 +179,8 @@ struct SelLayout {
   uint64_t bytes;     // total
 };
 
-__host__ SelLayout sel_layout(int64_t n) {
-  SelLayout L;
+constexpr SelLayout sel_layout(int64_t n) {
+  SelLayout L{};
   L.nblocks = uint32_t((n + kSelTile - 1) / kSelTile);
   const uint64_t nb4 = (uint64_t(L.nblocks) + 3) & ~uint64_t(3);
   L.blk_ties = kHeader;
@@ -613,6 +615,58 @@ __global__ __launch_bounds__(256) void dilate_kernel(const uint8_t* gap, uint32_
 }
 
 }  // namespace
+
+// ------------------------------------------------ allocation-free selection
+// cbk_kdev_select_noalloc takes its workspace from `scratch`, a file-scope
+// device array sized for CBK_NOALLOC_SELECT_MAX_TOKENS tokens (5.04 MiB,
+// held on every GPU the library runs on until the process ends). In host
+// code `scratch` names a host-side stand-in, not device memory: its device
+// address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is ever passed to kernels. Every
+// call on one GPU shares the array; the counters that must start at zero
+// are cleared by the call's own score launch, and calls that overlap on one
+// GPU (two streams at once) race on it.
+constexpr size_t kNoallocScratchBytes = size_t(sel_layout(CBK_NOALLOC_SELECT_MAX_TOKENS).bytes);
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on the device `stream` belongs to (the
+// current device for the NULL stream).
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int current = -1;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess)
+    return set_error(CBK_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(err));
+  int device = current;
+  if (stream != nullptr) {
+    err = hipStreamGetDevice(stream, &device);
+    if (err != hipSuccess)
+      return set_error(CBK_ERR_LAUNCH, "hipStreamGetDevice: %s", hipGetErrorString(err));
+  }
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(CBK_ERR_UNSUPPORTED, "device %d beyond the %d the scratch table holds", device,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[device] == nullptr) {
+    if (device != current && (err = hipSetDevice(device)) != hipSuccess)
+      return set_error(CBK_ERR_LAUNCH, "hipSetDevice(%d): %s", device, hipGetErrorString(err));
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (device != current) hipSetDevice(current);
+    if (err != hipSuccess || ptr == nullptr)
+      return set_error(CBK_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                       hipGetErrorString(err));
+    g_scratch_dev[device] = ptr;
+  }
+  *out = g_scratch_dev[device];
+  return CBK_OK;
+}
+
 }  // namespace cbk
 
 extern "C" {
@@ -663,6 +717,26 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
     return rc;
   return cbk::launch_select(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
                             out_count_dev, workspace_dev, workspace_bytes, s, zero);
+}
+
+int cbk_kdev_select_noalloc(const void* fresh_dev, int64_t fresh_row_stride_elems,
+                            const void* cached_dev, int64_t cached_row_stride_elems,
+                            int64_t cached_num_rows, const int64_t* cached_rows_dev,
+                            int64_t cached_row0, int64_t n, int64_t width, int32_t dtype,
+                            const uint8_t* gap_dev, const uint8_t* forced_dev, int64_t radius,
+                            double ratio, float* scores_dev, int64_t* out_idx_dev,
+                            int64_t* out_count_dev, cbk_stream_t stream) {
+  cbk::clear_error();
+  if (n > CBK_NOALLOC_SELECT_MAX_TOKENS)
+    return cbk::set_error(CBK_ERR_INVALID,
+                          "kdev_select_noalloc: %lld tokens exceed its static scratch maximum of %d",
+                          (long long)n, CBK_NOALLOC_SELECT_MAX_TOKENS);
+  void* scratch = nullptr;
+  if (int rc = cbk::noalloc_scratch(static_cast<hipStream_t>(stream), &scratch)) return rc;
+  return cbk_kdev_select(fresh_dev, fresh_row_stride_elems, cached_dev, cached_row_stride_elems,
+                         cached_num_rows, cached_rows_dev, cached_row0, n, width, dtype, gap_dev,
+                         forced_dev, radius, ratio, scores_dev, out_idx_dev, out_count_dev, scratch,
+                         cbk::kNoallocScratchBytes, stream);
 }
 
 int cbk_dilate(const uint8_t* gap_dev, int64_t n, int64_t radius, uint8_t* forced_dev,

@@ -1,0 +1,65 @@
+"""GPU: the allocation-free K-deviation selection entry point.
+
+cbk_kdev_select_noalloc (static device scratch, no workspace argument) is
+checked against cbk_kdev_select (caller workspace) through the C ABI: the
+same scores bit for bit, the same index set and count, on two calls in a
+row with the second smaller; sizes beyond its maximum are rejected before
+anything runs.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from cacheblend_vllm import _native, synthetic
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+MAX_TOKENS = 1048576  # CBK_NOALLOC_SELECT_MAX_TOKENS
+
+
+def _call(lib, fresh, cached, gap, ratio, radius, workspace=None):
+    n, width = fresh.shape
+    scores = torch.full((n,), float("nan"), device=DEV)
+    out = torch.full((max(n, 1),), -7, dtype=torch.long, device=DEV)
+    count = torch.full((1,), -7, dtype=torch.long, device=DEV)
+    args = [fresh.data_ptr(), fresh.stride(0), cached.data_ptr(), cached.stride(0), cached.shape[0],
+            None, 0, n, width, _native.DTYPE_CODES[fresh.dtype], gap.data_ptr(), None, radius, ratio,
+            scores.data_ptr(), out.data_ptr(), count.data_ptr()]
+    stream = _native.stream_handle(DEV)
+    if workspace is None:
+        rc = lib.cbk_kdev_select_noalloc(*args, stream)
+    else:
+        rc = lib.cbk_kdev_select(*args, workspace.data_ptr(), workspace.numel(), stream)
+    _native.check(rc, "kdev select")
+    torch.cuda.synchronize()
+    k = int(count.item())
+    return scores, out[:k].clone(), k
+
+
+def test_noalloc_select_matches_workspace_entry_point():
+    lib = _native.load()
+    for n, seed, ratio, radius in ((65536, 0, 0.15, 16), (5000, 1, 0.3, 0)):  # second call smaller
+        print(f"noalloc kdev select n={n} seed={seed}", flush=True)
+        fresh, cached, gap = synthetic.kdev_inputs(n, 4, 128, torch.bfloat16, DEV, seed=seed)
+        gap_u8 = gap.view(torch.uint8)
+        workspace = torch.empty(lib.cbk_select_workspace_bytes(n), dtype=torch.uint8, device=DEV)
+        want_scores, want_idx, want_k = _call(lib, fresh, cached, gap_u8, ratio, radius, workspace)
+        got_scores, got_idx, got_k = _call(lib, fresh, cached, gap_u8, ratio, radius)
+        assert torch.equal(got_scores.view(torch.int32), want_scores.view(torch.int32))
+        assert got_k == want_k > 0
+        assert torch.equal(got_idx, want_idx)
+        assert bool((got_idx[1:] > got_idx[:-1]).all())
+        assert bool(gap[got_idx].sum() == gap.sum())   # every gap token is selected
+
+
+def test_noalloc_select_rejects_sizes_beyond_its_scratch():
+    lib = _native.load()
+    tiny = torch.zeros(8, dtype=torch.uint8, device=DEV)
+    rc = lib.cbk_kdev_select_noalloc(tiny.data_ptr(), 1, tiny.data_ptr(), 1, 1, None, 0, MAX_TOKENS + 1, 1,
+                                     _native.DTYPE_CODES[torch.float32], tiny.data_ptr(), None, 0, 0.15,
+                                     tiny.data_ptr(), tiny.data_ptr(), tiny.data_ptr(),
+                                     _native.stream_handle(DEV))
+    assert rc == -1  # CBK_ERR_INVALID
+    assert b"static scratch maximum of 1048576" in lib.cbk_last_error()
