@@ -256,7 +256,7 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). No counterpart in the reference. The workspace is
  * a static device array sized for CBK_NOALLOC_SELECT_MAX_TOKENS tokens
- * (5.04 MiB per GPU, held until the process ends); larger n is rejected
+ * (5.11 MiB per GPU, held until the process ends); larger n is rejected
  * with CBK_ERR_INVALID. The caller passes every input and output. Calls
  * that overlap on one GPU (concurrent streams) race on the shared array;
  * calls in sequence do not (each clears the counters it needs).

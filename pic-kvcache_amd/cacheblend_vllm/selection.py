@@ -129,7 +129,16 @@ def select(
     ``int((N - #gap) * ratio)`` clamped to ``[1, available]``.
     """
     out, count = select_async(scores, gap_mask, ratio, forced_mask, radius)
-    return out[: int(count.item())]
+    return out[: _selected_count(count)]
+
+
+def _selected_count(count: torch.Tensor) -> int:
+    """The device count a selection wrote; negative means its one-launch
+    kernel's blocks could not all be resident (it gave up, nothing valid)."""
+    value = int(count.item())
+    if value < 0:
+        raise RuntimeError("selection failed: its grid barrier timed out (blocks not co-resident)")
+    return value
 
 
 def kdev_select(
@@ -171,7 +180,7 @@ def kdev_select(
         count.data_ptr(), ws.data_ptr(), ws.numel(), _native.stream_handle(fresh.device),
     )
     _native.check(rc, "kdev_select")
-    return out[: int(count.item())], scores
+    return out[: _selected_count(count)], scores
 
 
 def dilate(gap_mask: torch.Tensor, radius: int) -> torch.Tensor:

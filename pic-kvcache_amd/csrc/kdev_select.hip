@@ -167,13 +167,20 @@ constexpr uint32_t kHeader = 8512; // words cleared by the zero kernel
 // ctrl slots
 enum : uint32_t {
   C_GAP = 0, C_BASE, C_T_PREP, C_T_P2, C_T_P3, C_T_TIES, C_T_COUNT,
-  C_TOPK, C_PREFIX1, C_KREM1, C_PREFIX2, C_KREM2, C_THRESH, C_NEED, C_TOTAL
+  C_TOPK, C_PREFIX1, C_KREM1, C_PREFIX2, C_KREM2, C_THRESH, C_NEED, C_TOTAL,
+  // one-launch select: grid barrier arrivals / generation, candidates, error
+  C_BAR = 16, C_GEN, C_CANDS, C_ERR
 };
+// candidates the one-launch select finishes in LDS (keys sharing the k-th
+// key's 12- or 24-bit prefix)
+constexpr uint32_t kCandCap = 8192;
 
 struct SelLayout {
   uint32_t nblocks;
   uint64_t blk_ties;  // word offset: per-tile tie count -> exclusive tie offset
   uint64_t blk_sel;   // word offset: per-tile selected count -> exclusive output offset
+  uint64_t tiles;     // word offset: 4 per-tile arrays of the one-launch select
+  uint64_t cands;     // word offset: kCandCap candidate keys, then their indices
   uint64_t keys;      // word offset: n order keys
   uint64_t base;      // BYTE offset: n base flags
   uint64_t bytes;     // total
@@ -185,7 +192,9 @@ constexpr SelLayout sel_layout(int64_t n) {
   const uint64_t nb4 = (uint64_t(L.nblocks) + 3) & ~uint64_t(3);
   L.blk_ties = kHeader;
   L.blk_sel = L.blk_ties + nb4;
-  L.keys = L.blk_sel + nb4;
+  L.tiles = L.blk_sel + nb4;
+  L.cands = L.tiles + 4 * nb4;
+  L.keys = L.cands + 2 * uint64_t(kCandCap);
   L.base = (L.keys + uint64_t(n)) * 4;
   L.bytes = (L.base + uint64_t(n) + 255) & ~uint64_t(255);
   return L;
@@ -206,6 +215,15 @@ struct SelArgs {
   uint8_t* base;
   int64_t* out_idx;
   int64_t* out_count;
+  // one-launch select: per-tile base / sure / tie / selected counts and the
+  // candidate list (keys, then indices with the base flag in bit 31)
+  uint32_t* tile_base;
+  uint32_t* tile_sure;
+  uint32_t* tile_ties;
+  uint32_t* tile_cnt;
+  uint32_t* cand_key;
+  uint32_t* cand_idx;
+  uint32_t vec_ok;  // scores 16-byte and masks 8-byte aligned
 };
 
 __device__ __forceinline__ uint32_t order_key(float s) {
@@ -235,7 +253,7 @@ __device__ __forceinline__ bool last_block(uint32_t* ticket, uint32_t nblocks, u
 // largest key: cum(above) < k <= cum(above) + hist[bin].
 template <int NBINS>
 __device__ void find_bin_desc(const uint32_t* hist, uint32_t k, uint32_t* lds_scan,
-                              uint32_t* out_bin, uint32_t* out_krem) {
+                              uint32_t* out_bin, uint32_t* out_krem, uint32_t* out_count = nullptr) {
   constexpr int PER = NBINS / kSelThreads;
   uint32_t c[PER];
   uint32_t s = 0;
@@ -253,6 +271,7 @@ __device__ void find_bin_desc(const uint32_t* hist, uint32_t k, uint32_t* lds_sc
       if (run < k && k <= run + c[p]) {
         *out_bin = NBINS - 1 - threadIdx.x * PER - p;
         *out_krem = k - run;
+        if (out_count) *out_count = c[p];
       }
       run += c[p];
     }
@@ -525,6 +544,677 @@ __global__ __launch_bounds__(kSelThreads) void sel_write_kernel(const SelArgs a)
   }
 }
 
+// ---------------------------------------------------------------------
+// One-launch selection (cooperative launch, every block co-resident).
+//
+// Block b owns tile b (kSelThreads * ITEMS tokens, ITEMS consecutive tokens
+// per thread, kept in registers across the grid barriers):
+//   P1  base flags (gap | forced | dilated gap), order keys, the tile's
+//       12-bit first-digit histogram merged into H1; gap / base counts.
+//   --  barrier
+//   P2  every block finds the k-th key's first digit in H1 (the same answer
+//       everywhere). If at most kCandCap keys share it, each block appends
+//       its keys with that digit (key, index, base flag) to the candidate
+//       list and publishes its count of tokens taken for sure (base, or a
+//       higher digit); otherwise a second 12-bit digit narrows the prefix
+//       (one more barrier), and if that still leaves more than kCandCap
+//       keys the last 8 bits fix the k-th key exactly (ties path below).
+//   --  barrier
+//   P3  every block loads the candidates into LDS and finds the k-th
+//       largest (key desc, index asc) among them: the threshold key T and
+//       the largest index `cut` taken among keys equal to T. A token is
+//       selected iff base, key > T, or key == T and index <= cut. Its
+//       output offset is the sure counts of the earlier tiles plus the
+//       selected non-base candidates below its first index.
+// Ties path (more than kCandCap keys share the k-th key's 24-bit prefix,
+// e.g. masses of equal scores): T and `need` come from the 8-bit digit,
+// tiles publish their ties and sure counts, take ties in index order, and
+// publish their selected counts before writing (three more barriers).
+// ---------------------------------------------------------------------
+
+constexpr uint32_t kBarrierSpins = 1u << 22;
+
+// Grid-wide barrier over `nblocks` co-resident blocks. C_BAR counts every
+// block's arrivals over the launch (zeroed before it): barrier number
+// `round` (1, 2, ...) is passed once it reaches round * nblocks. Arrival is
+// a posted atomic, so a block waits one round trip for the last arrival.
+// Returns false when the select failed: a barrier that waited longer than
+// kBarrierSpins polls (blocks not co-resident), flagged in C_ERR so every
+// block stops.
+__device__ bool grid_barrier(uint32_t* ctrl, uint32_t nblocks, uint32_t round, uint32_t* lds_flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();  // this block's global writes before its arrival
+    __hip_atomic_fetch_add(ctrl + C_BAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t target = round * nblocks;
+    uint32_t ok = 1, spins = 0;
+    while (__hip_atomic_load(ctrl + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (++spins > kBarrierSpins ||
+          __hip_atomic_load(ctrl + C_ERR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        atomicOr(ctrl + C_ERR, 1u);
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __threadfence();  // the other blocks' writes after the barrier
+    *lds_flag = ok;
+  }
+  __syncthreads();
+  return *lds_flag != 0;
+}
+
+__device__ __forceinline__ uint32_t ld_rlx(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum over blocks' published values v[0 .. count) (block-wide).
+__device__ uint32_t block_sum_published(const uint32_t* v, uint32_t count, uint32_t* scan) {
+  uint32_t local = 0;
+  for (uint32_t t = threadIdx.x; t < count; t += kSelThreads) local += ld_rlx(&v[t]);
+  uint32_t total;
+  block_exclusive_scan<kSelThreads>(local, scan, &total);
+  return total;
+}
+
+// LDS histogram `h` of NBINS bins: the bin holding the k-th largest
+// (descending) or k-th smallest (ascending) element, and k's rank inside it.
+template <int NBINS, bool DESC>
+__device__ void lds_find_bin(const uint32_t* h, uint32_t k, uint32_t* scan, uint32_t* out_bin,
+                             uint32_t* out_krem) {
+  constexpr int PER = (NBINS + kSelThreads - 1) / kSelThreads;
+  uint32_t c[PER];
+  uint32_t s = 0;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int j = threadIdx.x * PER + p;
+    const int bin = DESC ? NBINS - 1 - j : j;
+    c[p] = j < NBINS ? h[bin] : 0u;
+    s += c[p];
+  }
+  uint32_t total;
+  const uint32_t before = block_exclusive_scan<kSelThreads>(s, scan, &total);
+  if (before < k && k <= before + s) {
+    uint32_t run = before;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      if (run < k && k <= run + c[p]) {
+        const int j = threadIdx.x * PER + p;
+        *out_bin = DESC ? NBINS - 1 - j : j;
+        *out_krem = k - run;
+      }
+      run += c[p];
+    }
+  }
+  __syncthreads();
+}
+
+// Among the LDS candidates ck[0 .. cnt) whose top (32 - bits) key bits equal
+// `prefix`, the key of the k-th largest: radix passes of up to 10 bits.
+// Returns T; *need = k's rank among the candidates equal to T, *ties = their
+// count.
+__device__ uint32_t cand_kth_key(const uint32_t* ck, uint32_t cnt, uint32_t prefix, int bits, uint32_t k,
+                                 uint32_t* h, uint32_t* scan, uint32_t* sv, uint32_t* need,
+                                 uint32_t* ties) {
+  uint32_t pfx = prefix;
+  uint32_t want = k;
+  uint32_t last = cnt;
+  while (bits > 0) {
+    const int b = bits > 10 ? 10 : bits;
+    bits -= b;
+    for (uint32_t j = threadIdx.x; j < (1u << b); j += kSelThreads) h[j] = 0u;
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+      const uint32_t key = ck[j];
+      if ((key >> (bits + b)) == pfx) atomicAdd(&h[(key >> bits) & ((1u << b) - 1u)], 1u);
+    }
+    __syncthreads();
+    if (b == 10) lds_find_bin<1024, true>(h, want, scan, &sv[0], &sv[1]);
+    else if (b == 9) lds_find_bin<512, true>(h, want, scan, &sv[0], &sv[1]);
+    else lds_find_bin<256, true>(h, want, scan, &sv[0], &sv[1]);  // b <= 8 here
+    const uint32_t bin = sv[0];
+    want = sv[1];
+    last = h[bin];
+    pfx = (pfx << b) | bin;
+    __syncthreads();
+  }
+  *need = want;
+  *ties = last;
+  return pfx;
+}
+
+// The `need`-th smallest index among LDS candidates whose key equals T
+// (indices < 2^31 in ci's low bits): radix passes of 11, 10 and 10 bits.
+__device__ uint32_t cand_kth_tie_index(const uint32_t* ck, const uint32_t* ci, uint32_t cnt, uint32_t T,
+                                       uint32_t need, uint32_t* h, uint32_t* scan, uint32_t* sv) {
+  uint32_t pfx = 0;
+  uint32_t want = need;
+  int done = 0;  // index bits fixed so far, from bit 30 down
+  const int widths[3] = {11, 10, 10};
+  for (int pass = 0; pass < 3; ++pass) {
+    const int b = widths[pass];
+    const int low = 31 - done - b;
+    for (uint32_t j = threadIdx.x; j < (1u << b); j += kSelThreads) h[j] = 0u;
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+      const uint32_t idx = ci[j] & 0x7FFFFFFFu;
+      if (ck[j] == T && (idx >> (low + b)) == pfx) atomicAdd(&h[(idx >> low) & ((1u << b) - 1u)], 1u);
+    }
+    __syncthreads();
+    if (b == 11) lds_find_bin<2048, false>(h, want, scan, &sv[0], &sv[1]);
+    else lds_find_bin<1024, false>(h, want, scan, &sv[0], &sv[1]);
+    pfx = (pfx << b) | sv[0];
+    want = sv[1];
+    done += b;
+    __syncthreads();
+  }
+  return pfx;
+}
+
+// The bin of a global 4096-bin histogram (read after a grid barrier, so
+// plain loads see every block's counts) holding the k-th largest element,
+// scanning from the top bin down; thread t reads bins [4080 - 16t, 4096 -
+// 16t) as four 16-byte loads. Outputs the bin, k's rank inside it and the
+// bin's count; one block barrier.
+__device__ void find_bin_desc_4096(const uint32_t* hist, uint32_t k, uint32_t* lds, uint32_t* out_bin,
+                                   uint32_t* out_krem, uint32_t* out_count) {
+  constexpr int PER = 4096 / kSelThreads;  // 16
+  const uint32_t lo = 4096 - PER * (threadIdx.x + 1);
+  uint32_t c[PER];
+#pragma unroll
+  for (int q = 0; q < PER / 4; ++q) {
+    const uint4 v = *reinterpret_cast<const uint4*>(hist + lo + 4 * q);
+    c[4 * q] = v.x; c[4 * q + 1] = v.y; c[4 * q + 2] = v.z; c[4 * q + 3] = v.w;
+  }
+  uint32_t s = 0;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) s += c[p];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t inc = wave_inclusive_scan(s);
+  if (lane == 63) lds[wave] = inc;
+  __syncthreads();
+  uint32_t above = inc - s;  // bins above this thread's, within its wave
+  for (uint32_t w = 0; w < wave; ++w) above += lds[w];
+  if (above < k && k <= above + s) {
+    uint32_t run = above;
+#pragma unroll
+    for (int p = PER - 1; p >= 0; --p) {  // descending bins: highest first
+      if (run < k && k <= run + c[p]) {
+        *out_bin = lo + p;
+        *out_krem = k - run;
+        *out_count = c[p];
+      }
+      run += c[p];
+    }
+  }
+}
+
+// Block-wide sums of K values per thread (two barriers, no atomics). `lds`
+// holds K * kSelThreads / 64 words.
+template <int K>
+__device__ __forceinline__ void block_sums(uint32_t (&v)[K], uint32_t* lds) {
+  constexpr int NW = kSelThreads / 64;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const uint32_t w = wave_sum_u32(v[k]);
+    if ((threadIdx.x & 63) == 0) lds[k * NW + wave] = w;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += lds[k * NW + w];
+    v[k] = t;
+  }
+  __syncthreads();
+}
+
+// Dilation radius the register path handles: a token's window lies inside
+// the 56 gap flags [i0 - 24, i0 + 32) its thread loads.
+constexpr int kRegDilation = 24;
+
+template <int ITEMS>
+__global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs a) {
+  constexpr uint32_t TILE = kSelThreads * ITEMS;
+  extern __shared__ uint32_t smem[];
+  __shared__ uint32_t scan[16];
+  __shared__ uint32_t red[16];
+  __shared__ uint32_t sv[4];
+  __shared__ uint32_t flag;
+  uint32_t* ctrl = a.ws + kCtrl;
+  uint32_t bar_round = 0;
+  const uint32_t ntiles = gridDim.x;
+  const uint32_t tile = blockIdx.x;
+  const uint32_t tile0 = tile * TILE;
+  const uint32_t i0 = tile0 + threadIdx.x * ITEMS;
+  const int r = a.radius;
+
+  // ---------------------------------------------------------------- P1
+  uint32_t* hist = smem;          // 4096
+  uint32_t* window = smem + 4096;  // TILE + 2r
+  // this thread's tokens: scores, gap and forced flags, all loads issued
+  // before any is used (vector loads on a full tile)
+  float sc[ITEMS];
+  uint8_t gp[ITEMS], fc[ITEMS];
+  if (a.vec_ok && i0 + ITEMS <= a.n) {
+#pragma unroll
+    for (int q = 0; q < ITEMS / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(a.scores + i0 + 4 * q);
+      sc[4 * q] = v.x; sc[4 * q + 1] = v.y; sc[4 * q + 2] = v.z; sc[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < ITEMS / 8; ++q) {
+      const uint64_t g8 = *reinterpret_cast<const uint64_t*>(a.gap + i0 + 8 * q);
+      const uint64_t f8 = a.forced ? *reinterpret_cast<const uint64_t*>(a.forced + i0 + 8 * q) : 0ull;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gp[8 * q + e] = uint8_t(g8 >> (8 * e));
+        fc[8 * q + e] = uint8_t(f8 >> (8 * e));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e) {
+      const uint32_t i = i0 + e;
+      const bool in = i < a.n;
+      sc[e] = in ? a.scores[i] : 0.f;
+      gp[e] = in ? a.gap[i] : 0;
+      fc[e] = in && a.forced ? a.forced[i] : 0;
+    }
+  }
+  // dilation: with ITEMS == 8 and r <= kRegDilation each thread loads the
+  // 56 gap flags [i0 - 24, i0 + 32) as seven 8-byte words into a bit mask;
+  // otherwise the tile's window [tile0 - r, tile0 + TILE + r) becomes a
+  // prefix count of gaps in LDS
+  const bool reg_dil = ITEMS == 8 && r > 0 && r <= kRegDilation;
+  uint64_t gmask = 0;
+  if (reg_dil) {
+#pragma unroll
+    for (int q = 0; q < 7; ++q) {
+      const int64_t g0 = int64_t(i0) - 24 + 8 * q;
+      uint64_t w8 = 0;
+      if (a.vec_ok && g0 >= 0 && g0 + 8 <= int64_t(a.n)) {
+        w8 = *reinterpret_cast<const uint64_t*>(a.gap + g0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t g = g0 + e;
+          w8 |= (g >= 0 && g < int64_t(a.n)) ? uint64_t(a.gap[g]) << (8 * e) : 0ull;
+        }
+      }
+      uint64_t bits = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bits |= ((w8 >> (8 * e)) & 0xFFull) ? (1ull << e) : 0ull;
+      gmask |= bits << (8 * q);
+    }
+  }
+#pragma unroll
+  for (uint32_t q = 0; q < 4096 / (4 * kSelThreads); ++q)
+    reinterpret_cast<uint4*>(hist)[threadIdx.x + q * kSelThreads] = make_uint4(0u, 0u, 0u, 0u);
+  if (r > 0 && !reg_dil) {
+    const uint32_t W = TILE + 2 * r;
+    for (uint32_t w = threadIdx.x; w < W; w += kSelThreads) {
+      const int64_t g = int64_t(tile0) - r + w;
+      window[w] = (g >= 0 && g < int64_t(a.n) && a.gap[g]) ? 1u : 0u;
+    }
+    __syncthreads();
+    const uint32_t per = (W + kSelThreads - 1) / kSelThreads;
+    const uint32_t beg = threadIdx.x * per;
+    const uint32_t end = min(W, beg + per);
+    uint32_t local = 0;
+    for (uint32_t w = beg; w < end; ++w) {
+      local += window[w];
+      window[w] = local;
+    }
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan<kSelThreads>(local, scan, &total);
+    for (uint32_t w = beg; w < end; ++w) window[w] += excl;
+  }
+  __syncthreads();
+  // keys; base tokens (key of -inf) are counted, not histogrammed: their
+  // count joins H1's -inf bin in the merge, which spares the LDS histogram
+  // its most crowded bin
+  uint32_t key[ITEMS];
+  uint32_t base_bits = 0, valid_bits = 0, gap_cnt = 0, base_cnt = 0;
+  const uint64_t dil_mask = reg_dil ? ((1ull << (2 * r + 1)) - 1ull) : 0ull;
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e) {
+    const uint32_t i = i0 + e;
+    key[e] = 0u;
+    if (i < a.n) {
+      const bool g = gp[e] != 0;
+      bool b = g || fc[e] != 0;
+      if (r > 0 && !b) {
+        if (reg_dil) {
+          b = (gmask >> (24 + e - r)) & dil_mask;
+        } else {
+          const uint32_t k = i - tile0 + r;  // window index of token i
+          const uint32_t hi = window[k + r];
+          const uint32_t lo = (k >= uint32_t(r) + 1) ? window[k - r - 1] : 0u;
+          b = hi > lo;
+        }
+      }
+      key[e] = b ? kKeyNegInf : order_key(sc[e]);
+      valid_bits |= 1u << e;
+      base_bits |= (b ? 1u : 0u) << e;
+      gap_cnt += g ? 1u : 0u;
+      base_cnt += b ? 1u : 0u;
+      if (!b) atomicAdd(&hist[key[e] >> 20], 1u);
+    }
+  }
+  uint32_t counts[2] = {gap_cnt, base_cnt};
+  block_sums(counts, red);
+  if (threadIdx.x == 0) {
+    if (counts[0]) atomicAdd(&ctrl[C_GAP], counts[0]);
+    if (counts[1]) atomicAdd(&ctrl[C_BASE], counts[1]);
+    a.tile_base[tile] = counts[1];
+  }
+  for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads) {
+    const uint32_t c = hist[i] + (i == (kKeyNegInf >> 20) ? counts[1] : 0u);
+    if (c) atomicAdd(&a.ws[kH1 + i], c);
+  }
+  if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+    if (threadIdx.x == 0) *a.out_count = -1;
+    return;
+  }
+
+  // ---------------------------------------------------------------- P2
+  // budget: int(cached * ratio) as Python computes it, then [1, available]
+  const int64_t gaps = ld_rlx(&ctrl[C_GAP]);
+  const int64_t bases = ld_rlx(&ctrl[C_BASE]);
+  int64_t topk = 0;
+  {
+    const int64_t cached = int64_t(a.n) - gaps;
+    const int64_t available = int64_t(a.n) - bases;
+    if (cached && available) {
+      topk = int64_t(double(cached) * a.ratio);
+      topk = topk < 1 ? 1 : topk;
+      topk = topk > available ? available : topk;
+    }
+  }
+  uint32_t write_bits = base_bits;  // selected tokens of this thread
+  uint32_t out_off = 0;
+  if (topk == 0) {
+    // only base tokens: the earlier tiles' base counts give the offset
+    uint32_t before[1] = {0};
+    for (uint32_t t = threadIdx.x; t < tile; t += kSelThreads) before[0] += a.tile_base[t];
+    block_sums(before, red);
+    out_off = before[0];
+    if (tile == 0 && threadIdx.x == 0) *a.out_count = bases;
+  } else {
+    find_bin_desc_4096(a.ws + kH1, uint32_t(topk), scan, &sv[0], &sv[1], &sv[3]);
+    __syncthreads();
+    uint32_t prefix = sv[0];
+    uint32_t krem = sv[1];
+    uint32_t cnt = sv[3];
+    int shift = 20;
+    bool exact = false;  // the ties path: T fixed by all 32 bits
+    if (cnt > kCandCap) {
+      // second digit: key[19:8] among keys with key[31:20] == prefix
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads) hist[i] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e)
+        if (((valid_bits >> e) & 1u) && (key[e] >> 20) == prefix) atomicAdd(&hist[(key[e] >> 8) & 0xFFFu], 1u);
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads)
+        if (hist[i]) atomicAdd(&a.ws[kH2 + i], hist[i]);
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+        if (threadIdx.x == 0) *a.out_count = -1;
+        return;
+      }
+      __syncthreads();
+      find_bin_desc_4096(a.ws + kH2, krem, scan, &sv[0], &sv[1], &sv[3]);
+      __syncthreads();
+      prefix = (prefix << 12) | sv[0];
+      krem = sv[1];
+      cnt = sv[3];
+      shift = 8;
+      if (cnt > kCandCap) {
+        // last digit: key[7:0] among keys with key[31:8] == prefix
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < 256; i += kSelThreads) hist[i] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < ITEMS; ++e)
+          if (((valid_bits >> e) & 1u) && (key[e] >> 8) == prefix) atomicAdd(&hist[key[e] & 0xFFu], 1u);
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < 256; i += kSelThreads)
+          if (hist[i]) atomicAdd(&a.ws[kH3 + i], hist[i]);
+        if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+          if (threadIdx.x == 0) *a.out_count = -1;
+          return;
+        }
+        find_bin_desc<256>(a.ws + kH3, krem, scan, &sv[0], &sv[1]);
+        __syncthreads();
+        prefix = (prefix << 8) | sv[0];
+        krem = sv[1];
+        shift = 0;
+        exact = true;
+      }
+    }
+    if (!exact) {
+      // -------------------------------------------- candidate path
+      uint32_t sure = 0, mine = 0;
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        if (!((valid_bits >> e) & 1u)) continue;
+        const uint32_t d = key[e] >> shift;
+        sure += (((base_bits >> e) & 1u) || d > prefix) ? 1u : 0u;
+        mine += d == prefix ? 1u : 0u;
+      }
+      // candidate slots: wave scans, a wave offset from an LDS counter, the
+      // block's range from one global counter
+      const uint32_t lane = threadIdx.x & 63;
+      const uint32_t inc = wave_inclusive_scan(mine);
+      const uint32_t wave_total = __shfl(inc, 63, 64);
+      const uint32_t sure_w = wave_sum_u32(sure);
+      if (threadIdx.x == 0) { red[8] = 0; red[9] = 0; }
+      __syncthreads();
+      uint32_t wave_off = 0;
+      if (lane == 63) {
+        wave_off = atomicAdd(&red[8], wave_total);
+        atomicAdd(&red[9], sure_w);
+      }
+      wave_off = __shfl(wave_off, 63, 64);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        a.tile_sure[tile] = red[9];
+        sv[2] = red[8] ? atomicAdd(&ctrl[C_CANDS], red[8]) : 0u;
+      }
+      __syncthreads();
+      uint32_t pos = sv[2] + wave_off + inc - mine;
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        if (((valid_bits >> e) & 1u) && (key[e] >> shift) == prefix) {
+          a.cand_key[pos] = key[e];
+          a.cand_idx[pos] = (i0 + e) | (((base_bits >> e) & 1u) << 31);
+          ++pos;
+        }
+      }
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+        if (threadIdx.x == 0) *a.out_count = -1;
+        return;
+      }
+      // ---------------------------------------------------------- P3
+      uint32_t* ck = smem;
+      uint32_t* ci = smem + kCandCap;
+      uint32_t* h = smem + 2 * kCandCap;  // 2048
+      // candidates written by every block before the barrier: 16-byte
+      // loads, all issued before any is stored (capacity-padded, so a
+      // partial last vector stays inside the candidate arrays)
+      constexpr uint32_t kVecPerThread = kCandCap / (4 * kSelThreads);
+      uint4 vk[kVecPerThread], vi[kVecPerThread];
+#pragma unroll
+      for (uint32_t q = 0; q < kVecPerThread; ++q) {
+        const uint32_t j = 4 * (threadIdx.x + q * kSelThreads);
+        if (j < cnt) {
+          vk[q] = *reinterpret_cast<const uint4*>(a.cand_key + j);
+          vi[q] = *reinterpret_cast<const uint4*>(a.cand_idx + j);
+        }
+      }
+      // the tiles' sure counts, loaded with the candidates
+      uint32_t sure_before = 0, sure_all = 0;
+      for (uint32_t t = threadIdx.x; t < ntiles; t += kSelThreads) {
+        const uint32_t v = a.tile_sure[t];
+        sure_all += v;
+        sure_before += t < tile ? v : 0u;
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kVecPerThread; ++q) {
+        const uint32_t j = 4 * (threadIdx.x + q * kSelThreads);
+        if (j < cnt) {
+          *reinterpret_cast<uint4*>(ck + j) = vk[q];
+          *reinterpret_cast<uint4*>(ci + j) = vi[q];
+        }
+      }
+      __syncthreads();
+      // the k-th largest (key desc, index asc) among the candidates: with a
+      // 20-bit remainder, one 11-bit LDS pass first; when at most 64
+      // candidates then share the prefix, one wave ranks them directly,
+      // else radix passes on the remaining key bits, then on the indices
+      // of the keys equal to T
+      uint32_t pfx = prefix, want = krem, rest = uint32_t(shift), m = cnt;
+      if (rest == 20) {
+        for (uint32_t j = threadIdx.x; j < 2048; j += kSelThreads) h[j] = 0u;
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) atomicAdd(&h[(ck[j] >> 9) & 2047u], 1u);
+        __syncthreads();
+        lds_find_bin<2048, true>(h, want, scan, &sv[0], &sv[1]);
+        m = h[sv[0]];
+        pfx = (pfx << 11) | sv[0];
+        want = sv[1];
+        rest = 9;
+        __syncthreads();
+      }
+      uint32_t T, cut;
+      if (m <= 64) {
+        uint32_t* list = h;  // the m candidates sharing the prefix
+        if (threadIdx.x == 0) sv[2] = 0;
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+          if ((ck[j] >> rest) == pfx) {
+            const uint32_t slot = atomicAdd(&sv[2], 1u);
+            list[2 * slot] = ck[j];
+            list[2 * slot + 1] = ci[j] & 0x7FFFFFFFu;
+          }
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+          const uint32_t lane = threadIdx.x;
+          const bool have = lane < m;
+          const uint32_t kk = have ? list[2 * lane] : 0u;
+          const uint32_t ii = have ? list[2 * lane + 1] : 0xFFFFFFFFu;
+          uint32_t rank = 0;
+          for (uint32_t l = 0; l < m; ++l) {
+            const uint32_t kl = __shfl(kk, int(l), 64);
+            const uint32_t il = __shfl(ii, int(l), 64);
+            rank += (kl > kk || (kl == kk && il < ii)) ? 1u : 0u;
+          }
+          if (have && rank == want - 1) {
+            sv[0] = kk;
+            sv[1] = ii;
+          }
+        }
+        __syncthreads();
+        T = sv[0];
+        cut = sv[1];
+      } else {
+        uint32_t need, ties;
+        T = cand_kth_key(ck, cnt, pfx, int(rest), want, h, scan, sv, &need, &ties);
+        cut = need >= ties ? 0x7FFFFFFFu : cand_kth_tie_index(ck, ci, cnt, T, need, h, scan, sv);
+      }
+      uint32_t before = 0, taken = 0;
+      for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+        const uint32_t idx = ci[j] & 0x7FFFFFFFu;
+        const bool sel = ck[j] > T || (ck[j] == T && idx <= cut);
+        if (sel && !(ci[j] >> 31)) {
+          ++taken;
+          before += idx < tile0 ? 1u : 0u;
+        }
+      }
+      uint32_t sums[4] = {taken, before, sure_before, sure_all};
+      block_sums(sums, red);
+      out_off = sums[2] + sums[1];
+      if (tile == 0 && threadIdx.x == 0) *a.out_count = int64_t(sums[3]) + sums[0];
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        const uint32_t i = i0 + e;
+        if ((valid_bits >> e) & 1u) {
+          if (key[e] > T || (key[e] == T && i <= cut)) write_bits |= 1u << e;
+        }
+      }
+    } else {
+      // ------------------------------------------------ ties path
+      const uint32_t T = prefix;
+      const uint32_t need = krem;
+      uint32_t ties = 0, sure = 0;
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        if (!((valid_bits >> e) & 1u)) continue;
+        ties += key[e] == T ? 1u : 0u;
+        sure += (((base_bits >> e) & 1u) || key[e] > T) ? 1u : 0u;
+      }
+      uint32_t tile_ties, tile_sure;
+      uint32_t rank = block_exclusive_scan<kSelThreads>(ties, scan, &tile_ties);
+      block_exclusive_scan<kSelThreads>(sure, scan, &tile_sure);
+      if (threadIdx.x == 0) a.tile_ties[tile] = tile_ties;
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+        if (threadIdx.x == 0) *a.out_count = -1;
+        return;
+      }
+      uint32_t tb = 0;
+      for (uint32_t t = threadIdx.x; t < tile; t += kSelThreads) tb += ld_rlx(&a.tile_ties[t]);
+      uint32_t tie_off;
+      block_exclusive_scan<kSelThreads>(tb, scan, &tie_off);
+      const int64_t left = int64_t(need) - int64_t(tie_off);
+      const uint32_t allow = left <= 0 ? 0u : (left < int64_t(tile_ties) ? uint32_t(left) : tile_ties);
+      uint32_t count = 0;
+#pragma unroll
+      for (int e = 0; e < ITEMS; ++e) {
+        if (!((valid_bits >> e) & 1u)) continue;
+        bool sel = ((base_bits >> e) & 1u) || key[e] > T;
+        if (key[e] == T) {
+          sel = sel || rank < allow;
+          ++rank;
+        }
+        if (sel) {
+          write_bits |= 1u << e;
+          ++count;
+        }
+      }
+      uint32_t tile_count;
+      block_exclusive_scan<kSelThreads>(count, scan, &tile_count);
+      if (threadIdx.x == 0) a.tile_cnt[tile] = tile_count;
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+        if (threadIdx.x == 0) *a.out_count = -1;
+        return;
+      }
+      uint32_t cb = 0, ca = 0;
+      for (uint32_t t = threadIdx.x; t < ntiles; t += kSelThreads) {
+        const uint32_t v = ld_rlx(&a.tile_cnt[t]);
+        ca += v;
+        cb += t < tile ? v : 0u;
+      }
+      uint32_t sb, sa;
+      block_exclusive_scan<kSelThreads>(cb, scan, &sb);
+      block_exclusive_scan<kSelThreads>(ca, scan, &sa);
+      out_off = sb;
+      if (tile == 0 && threadIdx.x == 0) *a.out_count = sa;
+    }
+  }
+  // ------------------------------------------------------------- write
+  uint32_t total;
+  uint32_t pos = out_off + block_exclusive_scan<kSelThreads>(__popc(write_bits), scan, &total);
+#pragma unroll
+  for (int e = 0; e < ITEMS; ++e) {
+    if (((write_bits >> e) & 1u) && pos < a.n) a.out_idx[pos++] = int64_t(i0 + e);
+  }
+}
+
 __global__ void write_zero_count_kernel(int64_t* out_count) { *out_count = 0; }
 
 int check_select(const float* scores, const uint8_t* gap, int64_t n, int64_t radius, double ratio,
@@ -542,6 +1232,57 @@ int check_select(const float* scores, const uint8_t* gap, int64_t n, int64_t rad
                      (unsigned long long)L.bytes);
   CBK_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "workspace must be 16-byte aligned");
   return CBK_OK;
+}
+
+constexpr int kNotLaunched = 1;
+
+// Blocks of sel_onepass_kernel<ITEMS> with `lds` dynamic LDS bytes that the
+// device can hold at once, per device (cached: the occupancy query is a
+// runtime call).
+template <int ITEMS>
+int onepass_capacity(size_t lds, int* capacity) {
+  static std::mutex mu;
+  static int cached_dev[16] = {};
+  static size_t cached_lds[16] = {};
+  static int cached_cap[16] = {};
+  static int used = 0;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_error(CBK_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(err));
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cached_dev[i] == dev && cached_lds[i] == lds) {
+      *capacity = cached_cap[i];
+      return CBK_OK;
+    }
+  int per_cu = 0, cus = 0, coop = 0;
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sel_onepass_kernel<ITEMS>, kSelThreads, lds);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+  if (err != hipSuccess) return set_error(CBK_ERR_LAUNCH, "occupancy query: %s", hipGetErrorString(err));
+  *capacity = coop ? per_cu * cus : 0;
+  if (used < 16) {
+    cached_dev[used] = dev;
+    cached_lds[used] = lds;
+    cached_cap[used] = *capacity;
+    ++used;
+  }
+  return CBK_OK;
+}
+
+// kNotLaunched when the tiles do not fit on the device at once.
+template <int ITEMS>
+int launch_onepass(const SelArgs& a, int64_t n, int64_t radius, hipStream_t stream) {
+  constexpr int64_t tile = int64_t(kSelThreads) * ITEMS;
+  const int64_t grid = (n + tile - 1) / tile;
+  const int64_t p1 = 4096 + tile + 2 * radius + 1;
+  const int64_t p3 = 2 * int64_t(kCandCap) + 2048;
+  const size_t lds = size_t(p1 > p3 ? p1 : p3) * sizeof(uint32_t);
+  int capacity = 0;
+  if (int rc = onepass_capacity<ITEMS>(lds, &capacity)) return rc;
+  if (grid > capacity) return kNotLaunched;
+  hipLaunchKernelGGL(sel_onepass_kernel<ITEMS>, dim3(uint32_t(grid)), dim3(kSelThreads), lds, stream, a);
+  return launch_status("select (one launch)");
 }
 
 // header_zeroed: an earlier launch on the stream cleared the kHeader counter
@@ -570,9 +1311,21 @@ int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced
   a.base = static_cast<uint8_t*>(ws) + L.base;
   a.out_idx = out_idx;
   a.out_count = out_count;
+  a.tile_base = a.ws + L.tiles;
+  a.tile_sure = a.tile_base + (L.cands - L.tiles) / 4;
+  a.tile_ties = a.tile_sure + (L.cands - L.tiles) / 4;
+  a.tile_cnt = a.tile_ties + (L.cands - L.tiles) / 4;
+  a.cand_key = a.ws + L.cands;
+  a.cand_idx = a.cand_key + kCandCap;
+  a.vec_ok = (reinterpret_cast<uintptr_t>(scores) % 16 == 0 && reinterpret_cast<uintptr_t>(gap) % 8 == 0 &&
+              reinterpret_cast<uintptr_t>(forced) % 8 == 0) ? 1u : 0u;
+  if (!header_zeroed) hipLaunchKernelGGL(sel_zero_kernel, dim3(1), dim3(kSelThreads), 0, stream, a.ws);
+  // one cooperative launch when every tile's block can be resident at once
+  int rc = launch_onepass<8>(a, n, radius, stream);
+  if (rc == kNotLaunched) rc = launch_onepass<32>(a, n, radius, stream);
+  if (rc != kNotLaunched) return rc;
   const dim3 grid(L.nblocks), block(kSelThreads);
   const size_t prep_lds = (4096 + 16 + kSelTile + 2 * size_t(radius) + 1) * sizeof(uint32_t);
-  if (!header_zeroed) hipLaunchKernelGGL(sel_zero_kernel, dim3(1), block, 0, stream, a.ws);
   hipLaunchKernelGGL(sel_prepare_kernel, grid, block, prep_lds, stream, a);
   hipLaunchKernelGGL(sel_pass_kernel<2>, grid, block, 0, stream, a);
   hipLaunchKernelGGL(sel_pass_kernel<3>, grid, block, 0, stream, a);
@@ -618,7 +1371,7 @@ __global__ __launch_bounds__(256) void dilate_kernel(const uint8_t* gap, uint32_
 
 // ------------------------------------------------ allocation-free selection
 // cbk_kdev_select_noalloc takes its workspace from `scratch`, a file-scope
-// device array sized for CBK_NOALLOC_SELECT_MAX_TOKENS tokens (5.04 MiB,
+// device array sized for CBK_NOALLOC_SELECT_MAX_TOKENS tokens (5.11 MiB,
 // held on every GPU the library runs on until the process ends). In host
 // code `scratch` names a host-side stand-in, not device memory: its device
 // address is looked up once per device (hipGetSymbolAddress, with that
@@ -657,7 +1410,7 @@ static int noalloc_scratch(hipStream_t stream, void** out) {
       return set_error(CBK_ERR_LAUNCH, "hipSetDevice(%d): %s", device, hipGetErrorString(err));
     void* ptr = nullptr;
     err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (device != current) hipSetDevice(current);
+    if (device != current) (void)hipSetDevice(current);
     if (err != hipSuccess || ptr == nullptr)
       return set_error(CBK_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", device,
                        hipGetErrorString(err));

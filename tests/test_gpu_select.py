@@ -225,3 +225,32 @@ def test_cpu_plumbing_kdev_leg_exact_zero_ties():
     # closed form: every noisy token, then the 25 lowest-index zero-score tokens
     rest = np.setdiff1d(np.arange(512), noisy.numpy())[:76 - 51]
     np.testing.assert_array_equal(got.cpu().numpy(), np.union1d(noisy.numpy(), rest))
+
+
+@pytest.mark.parametrize("n, case", [
+    (65536, "one_bin"),        # every key shares the first 12-bit digit: second digit narrows
+    (65536, "two_values"),     # two distinct keys: the last digit fixes the k-th key, index ties
+    (1_500_000, "normal"),     # 8192-token tiles
+    (5_000_000, "normal"),     # more tiles than fit at once: the multi-launch pipeline
+])
+def test_select_narrowing_paths_and_sizes(n, case):
+    """Selection paths the k-th key's neighbourhood decides: few keys in its
+    12-bit bin (candidates finished in LDS), a crowded bin narrowed by the
+    next 12 bits, a crowded 24-bit prefix (ties resolved by index), and
+    spans larger than one cooperative launch holds."""
+    rng = np.random.default_rng(n + len(case))
+    if case == "one_bin":
+        scores = (1.0 + rng.random(n) / 8.5).astype(np.float32)   # all in [1, 1.125)
+    elif case == "two_values":
+        scores = np.where(rng.random(n) < 0.5, 2.0, 3.0).astype(np.float32)
+    else:
+        scores = rng.standard_normal(n).astype(np.float32)
+    gap = rng.random(n) < 0.1
+    forced = rng.random(n) < 0.02
+    for ratio, radius in ((0.15, 16), (0.6, 0)):
+        print(f"n={n} case={case} ratio={ratio} radius={radius}", flush=True)
+        fc = forced | (O.dilate(gap, radius) if radius else False)
+        want = O.select(scores, gap, ratio, fc)
+        got = S.select(torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV), ratio,
+                       torch.from_numpy(forced).to(DEV), radius=radius)
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
