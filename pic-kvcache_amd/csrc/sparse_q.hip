@@ -123,8 +123,12 @@ __device__ __forceinline__ void round_pair(float& x, float& y) {
 
 // ------------------------------------------------------------ rowstats
 
-// One 64-key block against MAXT row tiles: MFMA, round, (mask), online stats.
-template <typename V, int KSTEPS, int MAXT, int RMODE, bool MASK>
+// One 64-key block against MAXT row tiles: MFMA, round, (mask), then the
+// row statistics: online (max, sum) updates, or -- FIXED -- sums against the
+// row's reference m, the maximum of its first key block (a logit of the row,
+// hence at most its maximum: no term exceeds 2^(max - m); a row whose sum
+// does not stay finite is recomputed online).
+template <typename V, int KSTEPS, int MAXT, int RMODE, bool MASK, bool FIXED = false>
 __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* blk, int32_t k0,
                                                const V (&afrag)[MAXT][KSTEPS], int ntiles_w,
                                                const int32_t (&rpos)[4], float (&m)[MAXT][4],
@@ -164,6 +168,13 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
         r[c] = raw[c];
         r[c + 1] = raw[c + 1];
         round_pair<RMODE>(r[c], r[c + 1]);  // -inf stays -inf
+      }
+      if constexpr (FIXED) {
+        float sum = __builtin_amdgcn_exp2f(fmaf(r[0], a.c2, -m[t][i]));
+#pragma unroll
+        for (int c = 1; c < kColTiles; ++c) sum += __builtin_amdgcn_exp2f(fmaf(r[c], a.c2, -m[t][i]));
+        l[t][i] += sum;
+        continue;
       }
       // online max / sum in the log2 domain; the max is taken on the
       // unrounded dots (canonical floats, no extra max(x, x); rounding is
@@ -229,8 +240,6 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
   const int ntiles_w = (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
     const char* row = (t < ntiles_w && qi < a.nq)
                           ? query_row(a, qi, g * a.groups + wave + 4 * t, 2) : nullptr;
 #pragma unroll
@@ -276,21 +285,53 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
       }
     }
   };
-  if (nkb > 0) {
-    request(0, 0);
-    request(1, 1);
-    for (int32_t kb = 0; kb < nkb; ++kb) {
-      CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
-      asm volatile("s_barrier" ::: "memory");
-      request(kb + 2, (kb + 2) % kBuffers);  // into the buffer computed one block ago
-      const int32_t k0 = kb * kKeyBlock1;
-      const uint16_t* blk = kbuf[kb % kBuffers];
-      if (k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk))
-        rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-      else
-        rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+  // Row statistics against a fixed reference (the first key block's
+  // maximum) when that block is visible to every row of the tile, so every
+  // lane's reference is a finite logit of its row; online (max, sum) updates
+  // otherwise, and again from the start when a fixed-reference sum did not
+  // stay finite (a logit over 127 above its row's reference, in log2 units).
+  __shared__ uint32_t s_redo;
+  bool fixed = minpos >= kKeyBlock1 - 1;
+  for (;;) {
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
+    if (nkb > 0) {
+      request(0, 0);
+      request(1, 1);
+      for (int32_t kb = 0; kb < nkb; ++kb) {
+        CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
+        asm volatile("s_barrier" ::: "memory");
+        request(kb + 2, (kb + 2) % kBuffers);  // into the buffer computed one block ago
+        const int32_t k0 = kb * kKeyBlock1;
+        const uint16_t* blk = kbuf[kb % kBuffers];
+        const bool masked = k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk);
+        if (fixed && kb > 0) {
+          if (masked)
+            rowstats_block<V, KSTEPS, MAXT, RMODE, true, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+          else
+            rowstats_block<V, KSTEPS, MAXT, RMODE, false, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+        } else if (masked) {
+          rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+        } else {
+          rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
+        }
+      }
+      CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends (or restarts)
     }
-    CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends
+    if (!fixed) break;
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < MAXT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bad |= !(l[t][i] < 3.0e38f);
+    if (threadIdx.x == 0) s_redo = 0;
+    __syncthreads();
+    if (bad) s_redo = 1;
+    __syncthreads();
+    if (!s_redo) break;
+    fixed = false;
   }
   // merge the 16 lanes that hold the same rows, then publish m2 + log2(l)
 #pragma unroll

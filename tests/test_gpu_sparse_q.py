@@ -200,3 +200,30 @@ def test_sparse_q_small_contexts(n_active, prefix, d):
                                   absolute.numpy()[rows.numpy()], d ** -0.5, True)
     np.testing.assert_allclose(full.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
     assert abs(float(full.sum()) - rows.numel() * hq) < 1e-3 * rows.numel() * hq
+
+
+def test_sparse_q_rows_far_above_their_first_block():
+    """Row statistics are summed against the first key block's maximum; rows
+    with a logit more than 127 (log2 units) above it overflow that sum and
+    are recomputed with online maxima. Here one key, far from the first
+    block, carries logits ~350 log2 units above every other for a third of
+    the queries; every score must still match the oracle."""
+    g = torch.Generator().manual_seed(7)
+    n_active, prefix, hq, hkv, d = 300, 200, 8, 2, 64
+    nk = prefix + n_active
+    q = torch.randn(n_active, hq, d, generator=g) / d ** 0.5
+    k = torch.randn(nk, hkv, d, generator=g) / d ** 0.5
+    q[::3] = 1.0
+    k[260] = 30.0
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    gap = torch.from_numpy(synthetic.gap_layout(n_active, 7, hit_chunk=64, max_hit_chunks=3, max_gap=63))
+    absolute = torch.arange(prefix, nk)
+    rows = torch.nonzero(gap).flatten()
+    scale = d ** -0.5
+    _, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, scale, want_full=True)
+    want = O.sparse_q_full_scores(q.float().numpy()[rows.numpy()], k.float().numpy(),
+                                  absolute.numpy()[rows.numpy()], scale, True)
+    full = full.cpu().numpy()
+    assert np.all(np.isfinite(full))
+    np.testing.assert_allclose(full, want, rtol=RTOL, atol=1e-6)
+    assert full[260] > 0.3 * rows.numel() * hq   # the big key takes most of those rows' mass
