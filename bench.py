@@ -212,7 +212,7 @@ def main() -> int:
     if not args.skip_extras:
         reload_slots = synthetic.block_slots(perm[1024:1536], BS, T).to(dev)
         result.update(extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev,
-                             reload_slots))
+                             reload_slots, (gather_ms, scatter_ms)))
 
     if not args.skip_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, synthetic)
@@ -220,21 +220,59 @@ def main() -> int:
     return 0
 
 
-def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev, reload_slots):
+def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev, reload_slots,
+           all_layer_ms):
     out = {}
     L = len(layers)
     BS = cache.block_size
     layer_bytes = staging[0].numel() * staging.element_size()
 
-    # per-layer launches (save_kv_layer granularity), device time per layer
+    # per-layer launches (the connector's granularity: save_kv_layer
+    # gathers one layer, a reload or commit scatters one), device time per
+    # layer, beside a plain device copy of the same bytes per launch (layer l
+    # into layer l + L/2 of the staging, so every copy reads what was written
+    # half a rotation, 1.2 GB, earlier: nothing comes from the 256 MB
+    # last-level cache). Against the all-layer launch of the same kernel,
+    # t(1 layer) = fixed + x and t(36 layers) = fixed + 36 x split each launch
+    # into its fixed cost (ramp, drain, the gap to the next launch) and the
+    # streaming rate between them
     def per_layer():
         for l in range(L):
             cache.gather(src_slots, out=staging[l:l + 1], layers=(l, l + 1))
 
-    ms = event_time_ms(torch, per_layer, max(3, args.steps // 4))
-    out["per_layer_gather"] = {"GBps": round(2 * L * layer_bytes / (ms / 1e3) / 1e9, 1),
-                               "us_per_layer": round(ms * 1e3 / L, 2)}
-    log(f"per-layer gather: {out['per_layer_gather']}")
+    reps = max(3, args.steps // 4)
+    ms = event_time_ms(torch, per_layer, reps)
+    per_layer_scatter_slots = reload_slots
+
+    def per_layer_scatter():
+        for l in range(L):
+            cache.scatter(staging[l:l + 1], per_layer_scatter_slots, layers=(l, l + 1))
+
+    ms_s = event_time_ms(torch, per_layer_scatter, reps)
+
+    def plain_copies():
+        for l in range(L):
+            staging[(l + L // 2) % L].copy_(staging[l])
+
+    ms_c = event_time_ms(torch, plain_copies, reps)
+    ceiling = 2 * L * layer_bytes / (ms_c / 1e3) / 1e9
+
+    def per_layer_entry(ms_total, ms_all_layers):
+        us1 = ms_total * 1e3 / L
+        stream_us = (ms_all_layers * 1e3 - us1) / (L - 1)
+        gb = 2 * layer_bytes / (us1 / 1e6) / 1e9
+        return {"GBps": round(gb, 1), "us_per_layer": round(us1, 2),
+                "frac_of_hbm_peak": round(gb / HBM_PEAK_GBPS, 4),
+                "frac_of_same_size_copy": round(gb / ceiling, 4),
+                "launch_fixed_us": round(us1 - stream_us, 2),
+                "streaming_GBps": round(2 * layer_bytes / (stream_us / 1e6) / 1e9, 1)}
+
+    out["per_layer_gather"] = per_layer_entry(ms, all_layer_ms[0])
+    out["per_layer_scatter"] = per_layer_entry(ms_s, all_layer_ms[1])
+    out["per_layer_plain_copy"] = {"GBps": round(ceiling, 1), "us_per_copy": round(ms_c * 1e3 / L, 2),
+                                   "bytes_per_copy": 2 * layer_bytes}
+    log(f"per-layer gather: {out['per_layer_gather']}, scatter {out['per_layer_scatter']}, "
+        f"plain copy {out['per_layer_plain_copy']}")
 
     # host link: pinned D2H / H2D of the whole staging (1.2 GB)
     host = torch.empty(staging.shape, dtype=staging.dtype, pin_memory=True)
@@ -770,9 +808,23 @@ def blend_load(torch, synthetic, dev, args):
 
     ms = event_time_ms(torch, commit_all, 5)
     commit_bytes = 2 * 2 * n * H * D * es  # read + written, K and V
+    # a plain device copy of the same bytes per launch, layer l's pool into
+    # layer l + 24's (after every check above), so each copy reads a pool
+    # last written 1.5 GB earlier
+    elems = commit_bytes // 2 // es
+    flat = [layer.view(-1) for layer in layers]
+
+    def plain_copies():
+        for l in range(L):
+            flat[(l + L // 2) % L][:elems].copy_(flat[l][:elems])
+
+    ms_c = event_time_ms(torch, plain_copies, 5)
+    gb = L * commit_bytes / (ms / 1e3) / 1e9
+    ceiling = L * commit_bytes / (ms_c / 1e3) / 1e9
     out["commit_scatter"] = {"tokens_per_layer": n, "us_per_layer": round(ms * 1e3 / L, 2),
-                             "GBps": round(L * commit_bytes / (ms / 1e3) / 1e9, 1),
-                             "frac_of_hbm_peak": round(L * commit_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                             "GBps": round(gb, 1), "frac_of_hbm_peak": round(gb / HBM_PEAK_GBPS, 4),
+                             "plain_copy_same_bytes_GBps": round(ceiling, 1),
+                             "frac_of_same_size_copy": round(gb / ceiling, 4)}
     return out
 
 
@@ -791,6 +843,14 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     for _ in range(args.steps):
         _kdev_async(torch, S, fresh, cached, gap)
     del copy_dst, fresh, cached
+    # one-layer launches, as the connector issues them: save_kv_layer's
+    # gather of one layer, a reload's scatter of one layer (36 of each per step)
+    for _ in range(args.steps):
+        for l in range(staging.shape[0]):
+            cache.gather(src_slots, out=staging[l:l + 1], layers=(l, l + 1))
+        for l in range(staging.shape[0]):
+            cache.scatter(staging[l:l + 1], dst_slots, layers=(l, l + 1))
+    _profile_commit(torch, synthetic, args, dev)
     nk, hq, hkv, d = 98304, 32, 4, 128
     g = torch.Generator(device=dev).manual_seed(0)
     query = (torch.randn((nk, hq, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
@@ -808,9 +868,29 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     del aq, ak, av
     _profile_host_link(torch, synthetic, cache, src_slots, args, dev)
     torch.cuda.synchronize()
-    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select, "
-        "store gather into host chunks, blend assembly from host chunks), sparse_q")
+    log(f"profile run done: {args.steps} x (gather, scatter, plain copy, kdev select, one-layer "
+        "gathers and scatters, C3 commits, store gather into host chunks, blend assembly from "
+        "host chunks), sparse_q, attention")
     return 0
+
+
+def _profile_commit(torch, synthetic, args, dev):
+    """The blend loader's commit at the Qwen3-30B-A3B blend span: the
+    [2, 32767, 4, 128] bf16 layer buffer's rows past the 2048-token APC prefix
+    (30,719 tokens) scattered into one layer's pages, 8 layers' pools in turn
+    (537 MB, past the last-level cache), 8 launches per step."""
+    from cacheblend_vllm import kv_layout as KL
+
+    A, APC, BS, H, D = 32767, 2048, 16, 4, 128
+    nb = (A + BS - 1) // BS + 8
+    pools = [synthetic.paged_pool(nb, BS, H, D, torch.bfloat16, dev, seed=200 + l) for l in range(8)]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
+    slots = synthetic.block_slots(perm[: (A + BS - 1) // BS], BS, A).to(dev)
+    buf = torch.randn(2, A, H, D, device=dev).to(torch.bfloat16)
+    for _ in range(args.steps):
+        for pool in pools:
+            KL.scatter_paged_kv(buf[:, APC:], pool, slots[APC:], BS)
+    torch.cuda.synchronize()
 
 
 def _profile_host_link(torch, synthetic, cache, src_slots, args, dev):

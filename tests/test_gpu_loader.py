@@ -252,21 +252,35 @@ def test_loader_without_relocation_is_a_bit_copy():
     np.testing.assert_array_equal(_bits(buf), want)
 
 
-def test_loader_blend_load_workload_sample():
-    """Qwen3-30B-A3B-shaped blend span (4 KV heads x 128 bf16, 16-token
-    blocks): 2048-token APC prefix, 12 hit segments of 256-multiples, gaps of
-    1-511 tokens, over 2 layers, checked against the oracle."""
-    rng = np.random.default_rng(0)
-    segs, pos, src = [], 2048, 0
-    for _ in range(12):
-        pos += int(rng.integers(1, 512))
-        n = 256 * int(rng.integers(1, 6))
-        segs.append((src, pos, n))
-        src += n + 256
-        pos += n
-    alloc_end = pos + int(rng.integers(1, 512))
-    nb = (alloc_end + 15) // 16 + 64
-    layers, store, plan, slots, hosts = _blend_setup(2, nb, 16, 4, 128, 2048, segs, alloc_end,
+def _full_blend_span(allocation_end=32767, apc=2048, seed=0):
+    """The Qwen3-30B-A3B blend span: 12 reused segments of 256-token
+    multiples after a 2048-token APC prefix, separated by 1-511-token gaps,
+    the rest of the span a trailing gap. (source_start, target_start, length)."""
+    rng = np.random.default_rng(seed)
+    gaps = rng.integers(1, 512, 12)
+    chunks_total = (allocation_end - apc - int(gaps.sum())) // 256
+    lens = 1 + rng.multinomial(chunks_total - 12, np.full(12, 1 / 12))
+    segs, pos, src = [], apc, 0
+    for g, m in zip(gaps, lens):
+        pos += int(g)
+        segs.append((src, pos, 256 * int(m)))
+        src += 256 * int(m) + 512
+        pos += 256 * int(m)
+    return segs
+
+
+def test_loader_blend_load_full_span_both_paths():
+    """The whole Qwen3-30B-A3B blend span (allocation_end 32767, 2048-token
+    APC prefix, 12 hit segments, 4 KV heads x 128 bf16, 16-token blocks) over
+    2 layers, on both transfer paths: DMA into the hit ring ("auto" picks it,
+    each segment's plane is one host run of >= 256 KiB) and the assembly
+    reading the pinned chunks in place. Every assembled buffer and the pages
+    after each commit equal the oracle's, bit for bit."""
+    A, APC, bs = 32767, 2048, 16
+    segs = _full_blend_span(A, APC)
+    assert segs[-1][1] + segs[-1][2] < A and sum(n for *_, n in segs) > 25000
+    nb = (A + bs - 1) // bs + 64
+    layers, store, plan, slots, hosts = _blend_setup(2, nb, bs, 4, 128, APC, segs, A,
                                                      torch.bfloat16, 256, seed=5)
     rope = Rope(128, 65536, True, base=1e6)
     cache = rope.cos_sin_cache.cpu().numpy()
@@ -275,16 +289,23 @@ def test_loader_blend_load_workload_sample():
         k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
         return O.f32_to_bf16(O.relocate_key(cache, old, new, k, 128, True, bf16=True)).reshape(k_bits.shape)
 
-    loader = PagedBlendLoader(layers, store, "req", plan, slots, 16, _cfg())
-    loader.prefetch(0, rope)
-    assert 0 in loader._zc_layers  # pinned chunks: hit rows read over PCIe
+    want = [O.loader_assemble(_bits(layers[l]), slots.numpy(), bs, APC, A,
+                              [(s, t, _bits(hosts[i, l])) for i, (s, t, _) in enumerate(segs)],
+                              relocate=reloc) for l in range(2)]
+    # the commit writes [apc:] only, so a second load assembles the same buffers
+    pages = [_bits(layers[l]).copy() for l in range(2)]
     for l in range(2):
-        buf = loader.get(l)
-        loader.prefetch(l + 1, rope)
-        want = O.loader_assemble(
-            _bits(layers[l]), slots.numpy(), 16, 2048, alloc_end,
-            [(s, t, _bits(hosts[i, l])) for i, (s, t, _) in enumerate(segs)], relocate=reloc,
-        )
-        np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
-        loader.commit(l, buf)
-    torch.cuda.synchronize()
+        O.loader_commit(want[l], pages[l], slots.numpy(), bs, APC, A)
+    for zero_copy in ("auto", True):
+        loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(), zero_copy=zero_copy)
+        loader.prefetch(0, rope)
+        for l in range(2):
+            buf = loader.get(l)
+            loader.prefetch(l + 1, rope)
+            np.testing.assert_array_equal(_bits(buf), want[l], err_msg=f"{zero_copy} layer {l}")
+            loader.commit(l, buf)
+        torch.cuda.synchronize()
+        for l in range(2):
+            np.testing.assert_array_equal(_bits(layers[l]), pages[l], err_msg=f"{zero_copy} commit {l}")
+        # "auto" takes DMA for these runs; True reads the chunks in place
+        assert (len(loader._zc_layers) > 0) == (zero_copy is True)
