@@ -98,12 +98,18 @@ template <> struct Ops<true> {  // f16
   }
 };
 
-// Rounds a pair to the dtype and back (the dtype's matmul / multiply output).
+// Rounds a pair to the dtype and back (the dtype's matmul / multiply output;
+// bf16: one instruction per value).
 template <bool F16>
 __device__ __forceinline__ void round2(float& x, float& y) {
-  const uint32_t u = Ops<F16>::pack(x, y);
-  x = Ops<F16>::lo(u);
-  y = Ops<F16>::hi(u);
+  if constexpr (F16) {
+    const uint32_t u = Ops<F16>::pack(x, y);
+    x = Ops<F16>::lo(u);
+    y = Ops<F16>::hi(u);
+  } else {
+    x = bf16_round(x);
+    y = bf16_round(y);
+  }
 }
 
 // bf16 / f16 1.0 in both halves of a word: the B operand of the "ones"

@@ -175,4 +175,14 @@ __device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);
 }
 
+// x rounded to bf16 (nearest even; -inf, +inf and NaN stay what they are),
+// as a float, in one instruction: v_cvt_pk_bf16_f32 with 0 for the low half
+// leaves the rounded value in the high half and zeros below it, which is the
+// float's bit pattern.
+__device__ __forceinline__ float bf16_round(float x) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __uint_as_float(__builtin_bit_cast(uint32_t, __builtin_convertvector((f2){0.f, x}, b2)));
+}
+
 }  // namespace cbk

@@ -104,17 +104,13 @@ __device__ __forceinline__ f32x4 mfma16<h16x8>(const h16x8& a, const h16x8& b, c
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Rounds the logits of one MFMA row group to the input dtype, two at a time
-// for bf16 (v_cvt_pk_bf16_f32), as a bf16/f16 matmul output would be.
+// Rounds two logits to the input dtype, as a bf16/f16 matmul output would
+// be (bf16: one instruction per logit).
 template <int RMODE>
 __device__ __forceinline__ void round_pair(float& x, float& y) {
   if constexpr (RMODE == 1) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 r = __builtin_convertvector((f2){x, y}, b2);
-    const uint32_t u = __builtin_bit_cast(uint32_t, r);
-    x = __uint_as_float(u << 16);
-    y = __uint_as_float(u & 0xffff0000u);
+    x = bf16_round(x);
+    y = bf16_round(y);
   } else if constexpr (RMODE == 2) {
     x = __half2float(__float2half(x));
     y = __half2float(__float2half(y));
@@ -195,8 +191,11 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
 
 // K blocks of 64 keys stream through three LDS buffers by DMA, as the query
 // units do in colsum (see there for the wait and barrier scheme).
-template <typename V, int KSTEPS, int MAXT, int RMODE>
-__global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
+// FULL: the group is exactly 4 * MAXT heads, so every wave has MAXT row tiles
+// (a compile-time count: no branch between the tiles of a block).
+template <typename V, int KSTEPS, int MAXT, int RMODE, bool FULL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_rowstats_kernel(
+    const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per key row
   constexpr uint32_t kInsts = P / 4;              // requests per wave per block (1 KiB each)
@@ -237,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void sq_rowstats_kernel(const SqArgs a) {
 
   V afrag[MAXT][KSTEPS];
   float m[MAXT][4], l[MAXT][4];
-  const int ntiles_w = (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
+  const int ntiles_w = FULL ? MAXT : (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     const char* row = (t < ntiles_w && qi < a.nq)
@@ -388,8 +387,10 @@ __device__ __forceinline__ void colsum_mfma(const uint16_t* qlds, uint32_t hl, c
 
 // Software-pipelined over the unit's 4 head slots: the MFMAs of head hl + 1
 // are issued before the VALU work of head hl, which they do not depend on.
-// Slots past the group (nh < 4) compute on rows that are never used.
-template <typename V, int KSTEPS, int RMODE, bool MASK>
+// Slots past the group (nh < 4) compute on rows that are never used. FULL
+// (every chunk holds 4 heads, the group is a multiple of 4): no branch
+// inside the unit, which the compiler then schedules as one block.
+template <typename V, int KSTEPS, int RMODE, bool MASK, bool FULL>
 __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
                                             uint32_t nh, int32_t kw0, const int32_t (&rpos)[4],
                                             const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
@@ -399,7 +400,7 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
 #pragma unroll
   for (uint32_t hl = 0; hl < kHeadChunk; ++hl) {
     if (hl + 1 < kHeadChunk) colsum_mfma<V, KSTEPS>(qlds, hl + 1, bfrag, acc[(hl + 1) & 1], col, rgrp);
-    if (hl < nh) {
+    if (FULL || hl < nh) {
       float mrow[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
@@ -424,7 +425,7 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
 }
 
 // three waves per SIMD: the LDS holds three workgroups' buffers
-template <typename V, int KSTEPS, int RMODE>
+template <typename V, int KSTEPS, int RMODE, bool FULL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_colsum_kernel(
     const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
@@ -527,9 +528,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         for (int i = 0; i < 4; ++i) rpos[i] = tbuf[b][4 * rgrp + i];
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
         if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt) * kQTile + kQTile > a.nq)
-          colsum_unit<V, KSTEPS, RMODE, true>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, true, FULL>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
         else
-          colsum_unit<V, KSTEPS, RMODE, false>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, false, FULL>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
       }
     }
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends
@@ -643,13 +644,22 @@ template <typename V, int RMODE, int KS>
 void launch_mfma_ks(const SqArgs& a, hipStream_t stream) {
   const dim3 g1((a.nq + kQTile - 1) / kQTile, a.hkv);
   const dim3 g2((a.nk + kKeyBlock2 - 1) / kKeyBlock2, a.hkv);
-  if (a.groups <= 4)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE>), g1, dim3(kThreads), 0, stream, a);
-  else if (a.groups <= 8)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE>), g1, dim3(kThreads), 0, stream, a);
+  if (a.groups == 4)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups < 4)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 8)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups < 8)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 16)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE>), g1, dim3(kThreads), 0, stream, a);
-  hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE>), g2, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
+  if (a.groups % kHeadChunk == 0)
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true>), g2, dim3(kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, false>), g2, dim3(kThreads), 0, stream, a);
 }
 
 template <typename V, int RMODE>
