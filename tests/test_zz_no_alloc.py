@@ -63,3 +63,40 @@ def test_noalloc_select_rejects_sizes_beyond_its_scratch():
                                      _native.stream_handle(DEV))
     assert rc == -1  # CBK_ERR_INVALID
     assert b"static scratch maximum of 1048576" in lib.cbk_last_error()
+
+
+def test_noalloc_select_replays_in_a_hip_graph():
+    """The caller the entry point is for: HIP graph capture. One capture
+    (after an eager warm-up), then replays with the program's own eager work
+    in between -- another allocation-free select on other data, which leaves
+    its own contents in the shared scratch -- and every replay must equal
+    the eager result bit for bit."""
+    lib = _native.load()
+    n, ratio, radius = 65536, 0.15, 16
+    fresh, cached, gap = synthetic.kdev_inputs(n, 4, 128, torch.bfloat16, DEV, seed=3)
+    other = synthetic.kdev_inputs(20000, 4, 128, torch.bfloat16, DEV, seed=4)
+    gap_u8 = gap.view(torch.uint8)
+    want_scores, want_idx, want_k = _call(lib, fresh, cached, gap_u8, ratio, radius)
+    scores = torch.full((n,), float("nan"), device=DEV)
+    out = torch.full((n,), -7, dtype=torch.long, device=DEV)
+    count = torch.full((1,), -7, dtype=torch.long, device=DEV)
+    args = [fresh.data_ptr(), fresh.stride(0), cached.data_ptr(), cached.stride(0), cached.shape[0],
+            None, 0, n, fresh.shape[1], _native.DTYPE_CODES[fresh.dtype], gap_u8.data_ptr(), None,
+            radius, ratio, scores.data_ptr(), out.data_ptr(), count.data_ptr()]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.cbk_kdev_select_noalloc(*args, _native.stream_handle(DEV))
+    _native.check(rc, "kdev select (captured)")
+    for rep in range(4):
+        print(f"graph replay {rep}", flush=True)
+        scores.fill_(float("nan"))
+        out.fill_(-7)
+        count.fill_(-7)
+        _, _, k_other = _call(lib, other[0], other[1], other[2].view(torch.uint8), 0.3, 0)
+        assert k_other > 0
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(count.item()) == want_k
+        assert torch.equal(scores.view(torch.int32), want_scores.view(torch.int32))
+        assert torch.equal(out[:want_k], want_idx)
