@@ -26,6 +26,9 @@
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
+#include <mutex>
+
 #include "cbk_common.hpp"
 
 namespace cbk {
@@ -56,6 +59,8 @@ struct SqArgs {
   float c2;               // scale * log2(e)
   int32_t round_mode;     // 0 none, 1 bf16, 2 f16
   float2* stats;          // [hq][nq_pad] (m2 + log2(l), unused)
+  float2* chunk_stats;    // [row_chunks][hq][nq_pad] (m2, l) of each key range, row_chunks > 1
+  uint32_t row_chunks;    // key ranges per (query tile, kv head) in rowstats
   int32_t* tiles;         // [ntiles][32]: the 16 query positions (-1 past nq), min, max, unused
   float* partial;         // [hkv][nk]
   uint16_t* qdense;       // [ntiles][hkv][groups][16][D]: query rows in colsum's unit order
@@ -206,8 +211,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   __shared__ int32_t s_minmax[2];
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
-  const uint32_t qt = ntiles - 1 - blockIdx.x;  // latest positions (most keys) first
-  const uint32_t g = blockIdx.y;
+  // workgroup -> (tile, key range, kv head), the kv head fastest and the
+  // latest tiles (most keys) first, so that workgroups are dispatched in
+  // decreasing order of work across all heads
+  const uint32_t g = blockIdx.x % a.hkv;
+  const uint32_t chunk = (blockIdx.x / a.hkv) % a.row_chunks;
+  const uint32_t qt = ntiles - 1 - blockIdx.x / (a.hkv * a.row_chunks);
   const uint32_t q0 = qt * kQTile;
   if (threadIdx.x < kQTile) s_pos[threadIdx.x] = query_pos(a, q0 + threadIdx.x);
   __syncthreads();
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     }
     s_minmax[0] = lo;
     s_minmax[1] = hi;
-    if (g == 0) {
+    if (g == 0 && chunk == 0) {
       a.tiles[kTileWords * qt + kQTile] = lo;
       a.tiles[kTileWords * qt + kQTile + 1] = hi;
     }
@@ -245,17 +254,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     for (int s = 0; s < KSTEPS; ++s)
       afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (32 * s + 8 * rgrp) * 2) : V(0);
     // the dense copy colsum streams (zeros past nq)
-    if (t < ntiles_w) {
+    if (t < ntiles_w && chunk == 0) {
       uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wave + 4 * t) * (kQTile * D) + col * D;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) *reinterpret_cast<V*>(dst + 32 * s + 8 * rgrp) = afrag[t][s];
     }
   }
-  if (g == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
+  if (g == 0 && chunk == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
   // nothing of the compiler's own in flight once the requests start
   CBK_WAIT_VM_LGKM0(0);
 
-  const int32_t nkb = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
+  // this workgroup's key blocks: [kb_lo, kb_hi), an equal share of the tile's
+  const int32_t nkb_tile = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
+  const int32_t kb_lo = int32_t(int64_t(nkb_tile) * chunk / a.row_chunks);
+  const int32_t kb_hi = int32_t(int64_t(nkb_tile) * (chunk + 1) / a.row_chunks);
   // per-lane byte offsets of a block's requests (key row, swizzled piece)
   uint32_t koff[kInsts];
   uint32_t krow[kInsts];
@@ -265,10 +277,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const uint32_t piece = (lane % P) ^ lds_swizzle<D>(krow[j]);
     koff[j] = (krow[j] * a.k_stride + g * a.d + piece * 8) * 2;
   }
-  // block kb (clamped: a request past the end repeats the last block) into buffer b;
-  // rows past nk of the last block read its last key (masked)
+  // block kb (clamped: a request past the range repeats its last block) into
+  // buffer b; rows past nk of the last block read its last key (masked)
   auto request = [&](int32_t kb, int b) {
-    kb = min(kb, nkb - 1);
+    kb = min(kb, kb_hi - 1);
     const int32_t k0 = kb * kKeyBlock1;
     const char* base = a.k + int64_t(k0) * a.k_stride * 2;
     const uint32_t lk = lds_address(kbuf[b]);
@@ -284,29 +296,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       }
     }
   };
-  // Row statistics against a fixed reference (the first key block's
+  // Row statistics against a fixed reference (the range's first block's
   // maximum) when that block is visible to every row of the tile, so every
   // lane's reference is a finite logit of its row; online (max, sum) updates
   // otherwise, and again from the start when a fixed-reference sum did not
   // stay finite (a logit over 127 above its row's reference, in log2 units).
   __shared__ uint32_t s_redo;
-  bool fixed = minpos >= kKeyBlock1 - 1;
+  bool fixed = (kb_lo + 1) * kKeyBlock1 - 1 <= minpos;
   for (;;) {
 #pragma unroll
     for (int t = 0; t < MAXT; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
-    if (nkb > 0) {
-      request(0, 0);
-      request(1, 1);
-      for (int32_t kb = 0; kb < nkb; ++kb) {
+    if (kb_hi > kb_lo) {
+      request(kb_lo, 0);
+      request(kb_lo + 1, 1);
+      for (int32_t kb = kb_lo; kb < kb_hi; ++kb) {
+        const int it = kb - kb_lo;
         CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
         asm volatile("s_barrier" ::: "memory");
-        request(kb + 2, (kb + 2) % kBuffers);  // into the buffer computed one block ago
+        request(kb + 2, (it + 2) % kBuffers);  // into the buffer computed one block ago
         const int32_t k0 = kb * kKeyBlock1;
-        const uint16_t* blk = kbuf[kb % kBuffers];
+        const uint16_t* blk = kbuf[it % kBuffers];
         const bool masked = k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk);
-        if (fixed && kb > 0) {
+        if (fixed && kb > kb_lo) {
           if (masked)
             rowstats_block<V, KSTEPS, MAXT, RMODE, true, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
           else
@@ -332,7 +345,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     if (!s_redo) break;
     fixed = false;
   }
-  // merge the 16 lanes that hold the same rows, then publish m2 + log2(l)
+  // merge the 16 lanes that hold the same rows, then publish m2 + log2(l),
+  // or this key range's (m2, l) for sq_merge_kernel
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     if (t >= ntiles_w) break;
@@ -347,9 +361,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         stats_merge(mm, ll, mo, lo);
       }
       const uint32_t q = q0 + 4 * rgrp + i;  // rows past nq too: colsum reads whole tiles
-      if (col == 0) a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
+      if (col == 0) {
+        if (a.row_chunks == 1)
+          a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
+        else
+          a.chunk_stats[(int64_t(chunk) * a.hq + h) * a.nq_pad + q] = make_float2(mm, ll);
+      }
     }
   }
+}
+
+// Merges the key ranges' (m2, l) of every (head, query) row in range order
+// (the same result run to run) and publishes m2 + log2(l).
+__global__ __launch_bounds__(kThreads) void sq_merge_kernel(const SqArgs a) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t rows = a.hq * a.nq_pad;
+  if (i >= rows) return;
+  float m = kNegInf, l = 0.f;
+  for (uint32_t c = 0; c < a.row_chunks; ++c) {
+    const float2 p = a.chunk_stats[int64_t(c) * rows + i];
+    stats_merge(m, l, p.x, p.y);
+  }
+  a.stats[i] = row_stats(m, l);
 }
 
 // -------------------------------------------------------------- colsum
@@ -437,9 +470,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   __shared__ __attribute__((aligned(16))) float2 sbuf[kQBuffers][128];  // 64 used, lanes 32-63 repeat
   __shared__ __attribute__((aligned(16))) int32_t tbuf[kQBuffers][64];  // tile record, repeated
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t g = blockIdx.y;
-  const int32_t kw0 = int32_t(blockIdx.x) * kKeyBlock2 + int32_t(wave) * 16 * kColTiles;
-  const int32_t kb0 = int32_t(blockIdx.x) * kKeyBlock2;
+  // workgroup -> (key block, kv head), the kv head fastest: the earliest key
+  // blocks (seen by the most queries) of every head are dispatched first
+  const uint32_t g = blockIdx.x % a.hkv;
+  const int32_t kb0 = int32_t(blockIdx.x / a.hkv) * kKeyBlock2;
+  const int32_t kw0 = kb0 + int32_t(wave) * 16 * kColTiles;
   const uint32_t col = lane & 15, rgrp = lane >> 4;
 
   V bfrag[kColTiles][KSTEPS];
@@ -594,6 +629,7 @@ __global__ __launch_bounds__(kThreads) void sq_colsum_f32_kernel(const SqArgs a)
 
 // ---------------------------------------------------------------- gather
 
+// out / full = the sum over kv heads of the partial column sums, in head order.
 __global__ __launch_bounds__(kThreads) void sq_gather_kernel(const float* partial, uint32_t nk, uint32_t hkv,
                                                              const int64_t* index, uint32_t n,
                                                              float* out, float* full) {
@@ -622,9 +658,12 @@ __global__ void sq_zero_kernel(float* p, uint64_t n) {
 // Largest head_dim of the MFMA path: the dense query copy is sized for it.
 constexpr int64_t kMaxHeadDim = 128;
 
+// Key ranges a (query tile, kv head) of rowstats may be split into.
+constexpr uint32_t kMaxRowChunks = 4;
+
 struct SqLayout {
   uint32_t nq_pad, ntiles;
-  uint64_t stats, tiles, partial, qdense, bytes;  // byte offsets
+  uint64_t stats, tiles, partial, qdense, chunk_stats, bytes;  // byte offsets
 };
 
 __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
@@ -636,14 +675,48 @@ __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   L.partial = (L.tiles + uint64_t(L.ntiles) * kTileWords * 4 + 255) & ~uint64_t(255);
   L.qdense = (L.partial + uint64_t(hkv) * nk * 4 + 255) & ~uint64_t(255);
   // padded by one unit: a partial head chunk's requests read past its group
-  L.bytes = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
+  L.chunk_stats = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
+  L.bytes = (L.chunk_stats + uint64_t(kMaxRowChunks) * hq * L.nq_pad * 8 + 255) & ~uint64_t(255);
   return L;
 }
 
+// Compute units of the current device (cached per device).
+int device_cus(int* cus) {
+  static std::mutex mu;
+  static int cached[64] = {};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_error(CBK_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(err));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) {
+    *cus = cached[dev];
+    return CBK_OK;
+  }
+  err = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return set_error(CBK_ERR_LAUNCH, "CU count: %s", hipGetErrorString(err));
+  if (dev >= 0 && dev < 64) cached[dev] = *cus;
+  return CBK_OK;
+}
+
+// Key ranges per (query tile, kv head) in rowstats: tiles differ in work by
+// their positions (causal), and one workgroup per tile left the latest tiles
+// running alone at the end; with ranges, about three workgroups per resident
+// slot are dispatched in decreasing order of work.
+constexpr uint32_t kRowChunkTarget = 3;  // rowstats workgroups per resident slot (about)
+
+uint32_t row_chunks(uint32_t units, int cus) {
+  const uint32_t slots = 3u * uint32_t(cus);  // rowstats: three workgroups per CU
+  const uint32_t k = units ? (kRowChunkTarget * slots + units - 1) / units : 1u;
+  return std::max(1u, std::min(kMaxRowChunks, k));
+}
+
+// Sets the launch's key ranges in `a`.
 template <typename V, int RMODE, int KS>
-void launch_mfma_ks(const SqArgs& a, hipStream_t stream) {
-  const dim3 g1((a.nq + kQTile - 1) / kQTile, a.hkv);
-  const dim3 g2((a.nk + kKeyBlock2 - 1) / kKeyBlock2, a.hkv);
+void launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
+  const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
+  a.row_chunks = row_chunks(ntiles * a.hkv, cus);
+  const dim3 g1(ntiles * a.hkv * a.row_chunks);
+  const dim3 g2(((a.nk + kKeyBlock2 - 1) / kKeyBlock2) * a.hkv);
   if (a.groups == 4)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 4)
@@ -656,6 +729,9 @@ void launch_mfma_ks(const SqArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
+  if (a.row_chunks > 1)
+    hipLaunchKernelGGL(sq_merge_kernel, dim3((a.hq * a.nq_pad + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                       stream, a);
   if (a.groups % kHeadChunk == 0)
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true>), g2, dim3(kThreads), 0, stream, a);
   else
@@ -663,10 +739,12 @@ void launch_mfma_ks(const SqArgs& a, hipStream_t stream) {
 }
 
 template <typename V, int RMODE>
-int launch_mfma(const SqArgs& a, int ksteps, hipStream_t stream) {
+int launch_mfma(SqArgs& a, int ksteps, hipStream_t stream) {
+  int cus = 0;
+  if (int rc = device_cus(&cus)) return rc;
   switch (ksteps) {
-    case 2: launch_mfma_ks<V, RMODE, 2>(a, stream); break;
-    case 4: launch_mfma_ks<V, RMODE, 4>(a, stream); break;
+    case 2: launch_mfma_ks<V, RMODE, 2>(a, cus, stream); break;
+    case 4: launch_mfma_ks<V, RMODE, 4>(a, cus, stream); break;
     default: return set_error(CBK_ERR_UNSUPPORTED, "head_dim %u", a.d);
   }
   return launch_status("sparse_q mfma");
@@ -729,6 +807,8 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
   a.tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
   a.partial = reinterpret_cast<float*>(ws + L.partial);
   a.qdense = reinterpret_cast<uint16_t*>(ws + L.qdense);
+  a.chunk_stats = reinterpret_cast<float2*>(ws + L.chunk_stats);
+  a.row_chunks = 1;
   a.nq_pad = L.nq_pad;
   if (nq == 0) {
     const uint64_t n = uint64_t(hkv) * nk;
