@@ -236,7 +236,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     }
   }
   __syncthreads();
-  const int32_t minpos = s_minmax[0], maxpos = min(s_minmax[1], int32_t(a.nk) - 1);
+  // workgroup-uniform, and scalar: the key-block loop and its branches stay
+  // uniform (an LDS value is per-lane to the compiler, which then keeps the
+  // loop counter and every loop-carried value in vector registers)
+  const int32_t minpos = __builtin_amdgcn_readfirstlane(s_minmax[0]);
+  const int32_t maxpos = __builtin_amdgcn_readfirstlane(min(s_minmax[1], int32_t(a.nk) - 1));
   const uint32_t col = lane & 15, rgrp = lane >> 4;
   int32_t rpos[4];
 #pragma unroll
@@ -266,8 +270,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 
   // this workgroup's key blocks: [kb_lo, kb_hi), an equal share of the tile's
   const int32_t nkb_tile = maxpos < 0 ? 0 : maxpos / kKeyBlock1 + 1;
-  const int32_t kb_lo = int32_t(int64_t(nkb_tile) * chunk / a.row_chunks);
-  const int32_t kb_hi = int32_t(int64_t(nkb_tile) * (chunk + 1) / a.row_chunks);
+  const int32_t kb_lo = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(nkb_tile) * chunk / a.row_chunks));
+  const int32_t kb_hi = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(nkb_tile) * (chunk + 1) / a.row_chunks));
   // per-lane byte offsets of a block's requests (key row, swizzled piece)
   uint32_t koff[kInsts];
   uint32_t krow[kInsts];
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     __syncthreads();
     if (bad) s_redo = 1;
     __syncthreads();
-    if (!s_redo) break;
+    if (!__builtin_amdgcn_readfirstlane(s_redo)) break;  // uniform: the loops stay scalar
     fixed = false;
   }
   // merge the 16 lanes that hold the same rows, then publish m2 + log2(l),
@@ -556,7 +560,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       const int b = it % kQBuffers;
       const int32_t qt = ntiles - 1 - it / int32_t(nchunks);
       const uint32_t hc = uint32_t(it) % nchunks;
-      const int32_t tmin = tbuf[b][kQTile], tmax = tbuf[b][kQTile + 1];
+      const int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[b][kQTile]);  // uniform: scalar
+      const int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[b][kQTile + 1]);
       if (tmax >= kw0) {
         int32_t rpos[4];
 #pragma unroll
