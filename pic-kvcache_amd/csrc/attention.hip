@@ -248,10 +248,13 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   using O = Ops<F16>;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t row = lane & 15, grp = lane >> 4;
-  const uint32_t kvh = blockIdx.y;
+  // workgroup -> (row tile, kv head), the kv head fastest and the latest
+  // tiles (most keys) first: work is dispatched in decreasing order across
+  // all heads
+  const uint32_t kvh = blockIdx.x % a.hkv;
   const uint32_t nrows = a.nq * a.group;
   const uint32_t ntiles = (nrows + kRows - 1) / kRows;
-  const uint32_t tile = ntiles - 1 - blockIdx.x;  // latest positions (most keys) first
+  const uint32_t tile = ntiles - 1 - blockIdx.x / a.hkv;
   const uint32_t r_wave = tile * kRows + wave * 16 * RT;
 
   // this lane's rows (one per row tile): (query, head) and their Q fragments
@@ -498,7 +501,7 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
   a.scale = scale;
   const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
   constexpr int RT = kRowTiles;
-  const dim3 grid(uint32_t((nrows + 64 * RT - 1) / (64 * RT)), uint32_t(hkv));
+  const dim3 grid(uint32_t((nrows + 64 * RT - 1) / (64 * RT)) * uint32_t(hkv));
   const bool f16 = dtype == CBK_DTYPE_F16;
   if (head_dim == 128) {
     if (f16) hipLaunchKernelGGL((attn_kernel<true, 128, RT>), grid, dim3(kThreads), 0, s, a);
