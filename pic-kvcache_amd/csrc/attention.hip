@@ -501,7 +501,10 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
   a.scale = scale;
   const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
   constexpr int RT = kRowTiles;
-  const dim3 grid(uint32_t((nrows + 64 * RT - 1) / (64 * RT)) * uint32_t(hkv));
+  const uint64_t groups = (nrows + 64 * RT - 1) / (64 * RT) * uint64_t(hkv);
+  CBK_REQUIRE(groups * kThreads < (uint64_t(1) << 32), "blend attention: %llu workgroups exceed one launch",
+              (unsigned long long)groups);
+  const dim3 grid(static_cast<uint32_t>(groups));
   const bool f16 = dtype == CBK_DTYPE_F16;
   if (head_dim == 128) {
     if (f16) hipLaunchKernelGGL((attn_kernel<true, 128, RT>), grid, dim3(kThreads), 0, s, a);

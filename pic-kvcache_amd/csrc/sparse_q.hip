@@ -6,10 +6,13 @@
 // keys of the context with keys k > pos_q masked (ascend.py:696-698).
 //
 // Two passes over Q.K^T on MFMA (v_mfma_f32_16x16x32_{bf16,f16}):
-//   rowstats  one workgroup per (16-query tile, kv head): the G query heads
-//             of the group x 16 queries against 64-key blocks staged in LDS,
-//             online max / sum per row in the log2 domain, merged across
-//             the 16 lanes that share a row -> m + log2(l) per (head, query)
+//   rowstats  one workgroup per (16-query tile, key range, kv head): the G
+//             query heads of the group x 16 queries against the range's
+//             64-key blocks staged in LDS, sums of exp against the range's
+//             first-block maximum (online max / sum where that does not
+//             apply) in the log2 domain, merged across the 16 lanes that
+//             share a row -> (m, l) per (range, head, query)
+//   merge     the ranges' (m, l) of each row, in range order -> m + log2(l)
 //   colsum    one workgroup per (256-key block, kv head): each wave keeps its
 //             64 keys' K fragments in registers and streams the query tiles
 //             (all G heads staged in LDS), accumulating exp2(x - m - log2 l) per
@@ -717,11 +720,17 @@ uint32_t row_chunks(uint32_t units, int cus) {
 
 // Sets the launch's key ranges in `a`.
 template <typename V, int RMODE, int KS>
-void launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
-  const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
-  a.row_chunks = row_chunks(ntiles * a.hkv, cus);
-  const dim3 g1(ntiles * a.hkv * a.row_chunks);
-  const dim3 g2(((a.nk + kKeyBlock2 - 1) / kKeyBlock2) * a.hkv);
+int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
+  const uint64_t ntiles = (a.nq + kQTile - 1) / kQTile;
+  const uint64_t kblocks = (a.nk + kKeyBlock2 - 1) / kKeyBlock2;
+  a.row_chunks = row_chunks(uint32_t(ntiles * a.hkv), cus);
+  // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
+  CBK_REQUIRE(ntiles * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
+                  kblocks * a.hkv * kThreads < (uint64_t(1) << 32),
+              "sparse_q: %llu query tiles x %llu key blocks x %u kv heads exceed one launch",
+              (unsigned long long)ntiles, (unsigned long long)kblocks, a.hkv);
+  const dim3 g1(uint32_t(ntiles * a.hkv * a.row_chunks));
+  const dim3 g2(uint32_t(kblocks * a.hkv));
   if (a.groups == 4)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 4)
@@ -741,17 +750,20 @@ void launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true>), g2, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, false>), g2, dim3(kThreads), 0, stream, a);
+  return CBK_OK;
 }
 
 template <typename V, int RMODE>
 int launch_mfma(SqArgs& a, int ksteps, hipStream_t stream) {
   int cus = 0;
   if (int rc = device_cus(&cus)) return rc;
+  int rc = CBK_OK;
   switch (ksteps) {
-    case 2: launch_mfma_ks<V, RMODE, 2>(a, cus, stream); break;
-    case 4: launch_mfma_ks<V, RMODE, 4>(a, cus, stream); break;
+    case 2: rc = launch_mfma_ks<V, RMODE, 2>(a, cus, stream); break;
+    case 4: rc = launch_mfma_ks<V, RMODE, 4>(a, cus, stream); break;
     default: return set_error(CBK_ERR_UNSUPPORTED, "head_dim %u", a.d);
   }
+  if (rc) return rc;
   return launch_status("sparse_q mfma");
 }
 
