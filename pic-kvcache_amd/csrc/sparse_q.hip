@@ -726,7 +726,8 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   a.row_chunks = row_chunks(uint32_t(ntiles * a.hkv), cus);
   // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
   CBK_REQUIRE(ntiles * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
-                  kblocks * a.hkv * kThreads < (uint64_t(1) << 32),
+                  kblocks * a.hkv * kThreads < (uint64_t(1) << 32) &&
+                  uint64_t(a.hq) * a.nq_pad < (uint64_t(1) << 32),
               "sparse_q: %llu query tiles x %llu key blocks x %u kv heads exceed one launch",
               (unsigned long long)ntiles, (unsigned long long)kblocks, a.hkv);
   const dim3 g1(uint32_t(ntiles * a.hkv * a.row_chunks));
