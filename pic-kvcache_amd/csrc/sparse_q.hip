@@ -5,7 +5,8 @@
 // matmul output, cacheblend_vllm/ascend.py:694) and the softmax runs over all
 // keys of the context with keys k > pos_q masked (ascend.py:696-698).
 //
-// Two passes over Q.K^T on MFMA (v_mfma_f32_16x16x32_{bf16,f16}):
+// Two passes over Q.K^T on MFMA (v_mfma_f32_16x16x32_{bf16,f16}; the row
+// pass of 16-head groups on v_mfma_f32_32x32x16_{bf16,f16}):
 //   rowstats  one workgroup per (16-query tile, key range, kv head): the G
 //             query heads of the group x 16 queries against the range's
 //             64-key blocks staged in LDS, sums of exp against the range's
@@ -22,8 +23,10 @@
 //   gather    out[i] = sum over kv heads (fixed order) of partial[.][idx[i]]
 // MFMA operand layout (checked on gfx950): A[i][k] in lane i + 16*(k/8),
 // element k%8; B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4),
-// register i%4. Q.K^T has both operands row-major in D, so A and B fragments
-// are the same 16-byte loads of 8 consecutive dims.
+// register i%4; 32x32x16: A[i][k] in lane i + 32*(k/8), B[k][j] in lane
+// j + 32*(k/8), element k%8; D[i][j] in lane j + 32*((i/4)%2), register
+// 4*(i/8) + i%4. Q.K^T has both operands row-major in D, so A and B
+// fragments are the same 16-byte loads of 8 consecutive dims.
 //
 // A float32 path (no MFMA, exact float32 dots) serves float32 inputs.
 #include <hip/hip_bf16.h>
@@ -31,6 +34,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "cbk_common.hpp"
 
@@ -40,6 +44,7 @@ namespace {
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
@@ -110,6 +115,17 @@ __device__ __forceinline__ f32x4 mfma16<s16x8>(const s16x8& a, const s16x8& b, c
 template <>
 __device__ __forceinline__ f32x4 mfma16<h16x8>(const h16x8& a, const h16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <typename V>
+__device__ __forceinline__ f32x16 mfma32(const V& a, const V& b, const f32x16& c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<s16x8>(const s16x8& a, const s16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<h16x8>(const h16x8& a, const h16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // Rounds two logits to the input dtype, as a bf16/f16 matmul output would
@@ -197,6 +213,75 @@ __device__ __forceinline__ void rowstats_block(const SqArgs& a, const uint16_t* 
   }
 }
 
+// The same block on 32x32x16 MFMAs with the product transposed: S^T = K.Q^T,
+// A = 32 keys of the block, B = a pair tile's 32 query rows (16 queries of
+// two heads of the wave). Each lane then holds one row (its query column,
+// lane % 32) and 16 keys of each 32-key half of the block: keys
+// 8 * (r / 4) + 4 * (lane / 32) + r % 4 in register r. A row's statistics
+// are one (max, sum) per lane, merged with the other half-wave at the end,
+// so four head slots fit the register budget of three waves per SIMD.
+// Pair tiles whose first slot is past the group (nslots) are skipped.
+template <typename V, int D, int NT, int RMODE, bool MASK, bool FIXED>
+__device__ __forceinline__ void rowstats_block_wide(const SqArgs& a, const uint16_t* blk, int32_t k0,
+                                                    const V (&qfrag)[NT][D / 16], int nslots, int32_t rpos,
+                                                    float (&m)[NT][1], float (&l)[NT][1], uint32_t lane) {
+  constexpr int S = D / 16;
+  const uint32_t kr = lane & 31, hi = lane >> 5;
+  f32x16 acc[NT][2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const uint32_t row = kt * 32 + kr;
+    V kfrag[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      kfrag[s] = *reinterpret_cast<const V*>(&blk[row * D + ((2 * s + hi) ^ lds_swizzle<D>(row)) * 8]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (2 * t >= nslots) break;
+      acc[t][kt] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < S; ++s) acc[t][kt] = mfma32<V>(kfrag[s], qfrag[t][s], acc[t][kt]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (2 * t >= nslots) break;
+    float x[32];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        x[kt * 16 + r] = acc[t][kt][r];
+        if constexpr (MASK) {
+          const int32_t key = k0 + kt * 32 + 8 * (r / 4) + 4 * int32_t(hi) + (r % 4);
+          if (key > rpos || key >= int32_t(a.nk)) x[kt * 16 + r] = kNegInf;
+        }
+      }
+    float ms;
+    if constexpr (FIXED) {
+      ms = m[t][0];
+    } else {
+      // online max on the unrounded dots, as in the 16x16 block
+      float bm = fmaxf(x[0], x[1]);
+#pragma unroll
+      for (int i = 2; i < 32; ++i) bm = fmaxf(bm, x[i]);
+      const float mn = fmaxf(m[t][0], bm * a.c2);
+      ms = (MASK && mn == kNegInf) ? 0.f : mn;
+      l[t][0] *= __builtin_amdgcn_exp2f(m[t][0] - ms);
+      m[t][0] = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) round_pair<RMODE>(x[i], x[i + 1]);  // -inf stays -inf
+    float s0 = 0.f, s1 = 0.f;  // two chains of adds
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+      s0 += __builtin_amdgcn_exp2f(fmaf(x[i], a.c2, -ms));
+      s1 += __builtin_amdgcn_exp2f(fmaf(x[i + 1], a.c2, -ms));
+    }
+    l[t][0] += s0 + s1;
+  }
+}
+
 // K blocks of 64 keys stream through three LDS buffers by DMA, as the query
 // units do in colsum (see there for the wait and barrier scheme).
 // FULL: the group is exactly 4 * MAXT heads, so every wave has MAXT row tiles
@@ -212,14 +297,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[kBuffers][kKeyBlock1 * D];
   __shared__ int32_t s_pos[kQTile];
   __shared__ int32_t s_minmax[2];
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index in a scalar register: what derives from it stays scalar
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
   // workgroup -> (tile, key range, kv head), the kv head fastest and the
   // latest tiles (most keys) first, so that workgroups are dispatched in
   // decreasing order of work across all heads
-  const uint32_t g = blockIdx.x % a.hkv;
-  const uint32_t chunk = (blockIdx.x / a.hkv) % a.row_chunks;
-  const uint32_t qt = ntiles - 1 - blockIdx.x / (a.hkv * a.row_chunks);
+  // (a division by a runtime value runs on the VALU: readfirstlane brings
+  // the results back to scalar registers)
+  const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x % a.hkv);
+  const uint32_t chunk = __builtin_amdgcn_readfirstlane((blockIdx.x / a.hkv) % a.row_chunks);
+  const uint32_t qt = __builtin_amdgcn_readfirstlane(ntiles - 1 - blockIdx.x / (a.hkv * a.row_chunks));
   const uint32_t q0 = qt * kQTile;
   if (threadIdx.x < kQTile) s_pos[threadIdx.x] = query_pos(a, q0 + threadIdx.x);
   __syncthreads();
@@ -244,27 +332,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // loop counter and every loop-carried value in vector registers)
   const int32_t minpos = __builtin_amdgcn_readfirstlane(s_minmax[0]);
   const int32_t maxpos = __builtin_amdgcn_readfirstlane(min(s_minmax[1], int32_t(a.nk) - 1));
+  // Row tiles of a wave: its head slots are heads wave + 4 * slot of the
+  // group. 16x16x32 (MAXT <= 2): one tile per slot, 4 rows per lane.
+  // 32x32x16 (MAXT = 4): pair tiles of slots 2t and 2t + 1, one row per lane
+  // (157 against 168 registers and half the spills of the 16x16 form there:
+  // 16 heads per KV head 7% faster; at 8 heads the 16x16 form measured 1-3%
+  // faster, the 32x32 form's busier co-execution lowering the clock that
+  // the power limit allows).
+  constexpr bool WIDE = MAXT == 4;
+  constexpr int NT = WIDE ? MAXT / 2 : MAXT;    // row tiles
+  constexpr int NR = WIDE ? 1 : 4;              // rows per lane and tile
+  constexpr int NS = WIDE ? D / 16 : KSTEPS;    // MFMA steps over the head dim
+  constexpr uint32_t kStepDims = WIDE ? 16 : 32;
   const uint32_t col = lane & 15, rgrp = lane >> 4;
-  int32_t rpos[4];
+  const uint32_t d0 = WIDE ? 8 * (lane >> 5) : 8 * rgrp;  // this lane's dims within a step
+  int32_t rpos[NR];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rpos[i] = s_pos[4 * rgrp + i];
+  for (int i = 0; i < NR; ++i) rpos[i] = s_pos[WIDE ? col : 4 * rgrp + i];
   const uint32_t qi = q0 + col;
 
-  V afrag[MAXT][KSTEPS];
-  float m[MAXT][4], l[MAXT][4];
-  const int ntiles_w = FULL ? MAXT : (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
+  V afrag[NT][NS];
+  float m[NT][NR], l[NT][NR];
+  const int nslots = FULL ? MAXT : (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    const char* row = (t < ntiles_w && qi < a.nq)
-                          ? query_row(a, qi, g * a.groups + wave + 4 * t, 2) : nullptr;
+  for (int t = 0; t < NT; ++t) {
+    const int slot = WIDE ? 2 * t + int(rgrp & 1) : t;
+    const char* row = (slot < nslots && qi < a.nq)
+                          ? query_row(a, qi, g * a.groups + wave + 4 * slot, 2) : nullptr;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (32 * s + 8 * rgrp) * 2) : V(0);
+    for (int s = 0; s < NS; ++s)
+      afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (kStepDims * s + d0) * 2) : V(0);
     // the dense copy colsum streams (zeros past nq)
-    if (t < ntiles_w && chunk == 0) {
-      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wave + 4 * t) * (kQTile * D) + col * D;
+    if (slot < nslots && chunk == 0) {
+      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wave + 4 * slot) * (kQTile * D) + col * D;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) *reinterpret_cast<V*>(dst + 32 * s + 8 * rgrp) = afrag[t][s];
+      for (int s = 0; s < NS; ++s) *reinterpret_cast<V*>(dst + kStepDims * s + d0) = afrag[t][s];
     }
   }
   if (g == 0 && chunk == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
@@ -309,42 +411,53 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // otherwise, and again from the start when a fixed-reference sum did not
   // stay finite (a logit over 127 above its row's reference, in log2 units).
   __shared__ uint32_t s_redo;
-  bool fixed = (kb_lo + 1) * kKeyBlock1 - 1 <= minpos;
+  // blocks [kb_lo, kb_m) are visible to every row of the tile and lie below
+  // nk; the blocks from kb_m on are masked
+  const int32_t kb_vis = int32_t(min((int64_t(minpos) + 1) / kKeyBlock1, int64_t(a.nk) / kKeyBlock1));
+  const int32_t kb_m = min(max(kb_vis, kb_lo), kb_hi);
+  bool fixed = kb_lo < kb_m;
+  // one block: wait for it, request the block two ahead into the buffer
+  // computed one block ago, then the block's statistics (each variant in a
+  // loop of its own: no register copies between variants in the hot loop)
+  auto step = [&](auto mask, auto fix, int32_t kb) {
+    const int it = kb - kb_lo;
+    CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
+    asm volatile("s_barrier" ::: "memory");
+    request(kb + 2, (it + 2) % kBuffers);
+    if constexpr (WIDE)
+      rowstats_block_wide<V, D, NT, RMODE, decltype(mask)::value, decltype(fix)::value>(
+          a, kbuf[it % kBuffers], kb * kKeyBlock1, afrag, nslots, rpos[0], m, l, lane);
+    else
+      rowstats_block<V, KSTEPS, MAXT, RMODE, decltype(mask)::value, decltype(fix)::value>(
+          a, kbuf[it % kBuffers], kb * kKeyBlock1, afrag, nslots, rpos, m, l, col, rgrp);
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
   for (;;) {
 #pragma unroll
-    for (int t = 0; t < MAXT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
+      for (int i = 0; i < NR; ++i) { m[t][i] = kNegInf; l[t][i] = 0.f; }
     if (kb_hi > kb_lo) {
       request(kb_lo, 0);
       request(kb_lo + 1, 1);
-      for (int32_t kb = kb_lo; kb < kb_hi; ++kb) {
-        const int it = kb - kb_lo;
-        CBK_WAIT_VM_LGKM0(kInsts);  // block kb has landed; the newest block may be pending
-        asm volatile("s_barrier" ::: "memory");
-        request(kb + 2, (it + 2) % kBuffers);  // into the buffer computed one block ago
-        const int32_t k0 = kb * kKeyBlock1;
-        const uint16_t* blk = kbuf[it % kBuffers];
-        const bool masked = k0 + kKeyBlock1 - 1 > minpos || k0 + kKeyBlock1 > int32_t(a.nk);
-        if (fixed && kb > kb_lo) {
-          if (masked)
-            rowstats_block<V, KSTEPS, MAXT, RMODE, true, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-          else
-            rowstats_block<V, KSTEPS, MAXT, RMODE, false, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-        } else if (masked) {
-          rowstats_block<V, KSTEPS, MAXT, RMODE, true>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-        } else {
-          rowstats_block<V, KSTEPS, MAXT, RMODE, false>(a, blk, k0, afrag, ntiles_w, rpos, m, l, col, rgrp);
-        }
+      int32_t kb = kb_lo;
+      if (fixed) {
+        step(no(), no(), kb++);  // the reference block, online
+        for (; kb < kb_m; ++kb) step(no(), yes(), kb);
+        for (; kb < kb_hi; ++kb) step(yes(), yes(), kb);
+      } else {
+        for (; kb < kb_m; ++kb) step(no(), no(), kb);
+        for (; kb < kb_hi; ++kb) step(yes(), no(), kb);
       }
       CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends (or restarts)
     }
     if (!fixed) break;
     bool bad = false;
 #pragma unroll
-    for (int t = 0; t < MAXT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bad |= !(l[t][i] < 3.0e38f);
+      for (int i = 0; i < NR; ++i) bad |= !(l[t][i] < 3.0e38f);
     if (threadIdx.x == 0) s_redo = 0;
     __syncthreads();
     if (bad) s_redo = 1;
@@ -352,23 +465,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     if (!__builtin_amdgcn_readfirstlane(s_redo)) break;  // uniform: the loops stay scalar
     fixed = false;
   }
-  // merge the 16 lanes that hold the same rows, then publish m2 + log2(l),
-  // or this key range's (m2, l) for sq_merge_kernel
+  // merge the lanes that hold the same rows (16 lanes, or the two half-waves
+  // of the wide tiles), then publish m2 + log2(l), or this key range's
+  // (m2, l) for sq_merge_kernel
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    if (t >= ntiles_w) break;
-    const uint32_t h = g * a.groups + wave + 4 * t;
+  for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NR; ++i) {
       float mm = m[t][i], ll = l[t][i];
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) {
+      for (int off = WIDE ? 32 : 1; off < (WIDE ? 64 : 16); off <<= 1) {
         const float mo = __shfl_xor(mm, off, 64);
         const float lo = __shfl_xor(ll, off, 64);
         stats_merge(mm, ll, mo, lo);
       }
-      const uint32_t q = q0 + 4 * rgrp + i;  // rows past nq too: colsum reads whole tiles
-      if (col == 0) {
+      const int slot = WIDE ? 2 * t + int(rgrp & 1) : t;
+      const uint32_t h = g * a.groups + wave + 4 * slot;
+      const uint32_t q = q0 + (WIDE ? col : 4 * rgrp + i);  // rows past nq too: colsum reads whole tiles
+      if ((WIDE ? lane < 32 : col == 0) && slot < nslots) {
         if (a.row_chunks == 1)
           a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
         else
@@ -476,11 +590,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   __shared__ __attribute__((aligned(16))) uint16_t qbuf[kQBuffers][kQElems];
   __shared__ __attribute__((aligned(16))) float2 sbuf[kQBuffers][128];  // 64 used, lanes 32-63 repeat
   __shared__ __attribute__((aligned(16))) int32_t tbuf[kQBuffers][64];  // tile record, repeated
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // workgroup -> (key block, kv head), the kv head fastest: the earliest key
   // blocks (seen by the most queries) of every head are dispatched first
-  const uint32_t g = blockIdx.x % a.hkv;
-  const int32_t kb0 = int32_t(blockIdx.x / a.hkv) * kKeyBlock2;
+  // (a division by a runtime value runs on the VALU: readfirstlane brings
+  // the results back to scalar registers)
+  const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x % a.hkv);
+  const int32_t kb0 = __builtin_amdgcn_readfirstlane(int32_t(blockIdx.x / a.hkv) * kKeyBlock2);
   const int32_t kw0 = kb0 + int32_t(wave) * 16 * kColTiles;
   const uint32_t col = lane & 15, rgrp = lane >> 4;
 
