@@ -32,6 +32,7 @@
 #include <hip/hip_fp16.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "cbk_common.hpp"
 
@@ -116,27 +117,55 @@ __device__ __forceinline__ void round2(float& x, float& y) {
 // column whose MFMA accumulates each row's sum of (rounded) probabilities
 template <bool F16> constexpr uint32_t kOnesPair = F16 ? 0x3c003c00u : 0x3f803f80u;
 
+// A lane's LDS read offsets within a K or V block, bytes, the same in every
+// buffer: the K fragment of dim step st and the V transposing read of column
+// tile c, both for the first 16-key half (the second half is 16 rows
+// further: the swizzle of row 16 + r equals that of row r).
+template <int D>
+struct BlockOffsets {
+  uint32_t k[D / 32];
+  uint32_t v[D / 16];
+  __device__ __forceinline__ explicit BlockOffsets(uint32_t lane) {
+    const uint32_t row = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) k[st] = (row * D + ((4 * st + grp) ^ lds_swizzle<D>(row)) * 8) * 2;
+    // lane (row, grp) addresses key 4 grp + row / 4, dims 16c + 4 (row % 4) .. + 3
+    // of the row-major V block
+    const uint32_t vkey = 4 * grp + (row >> 2);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const uint32_t dim = 16 * c + 4 * (row & 3);
+      v[c] = (vkey * D + ((dim / 8) ^ lds_swizzle<D>(vkey)) * 8 + (dim & 4)) * 2;
+    }
+  }
+};
+
+// ks, vs: the block's K and V buffers. With the buffer a compile-time choice
+// (the caller's), a read's address is the lane's offset register plus a
+// constant that the DS instruction's offset field carries.
 template <bool F16, int D, int RT, bool MASK>
-__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t* vs, int32_t k0, float scale,
+__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t* vs, const BlockOffsets<D>& off,
+                                             int32_t k0, float scale,
                                              const typename Ops<F16>::A8 (&qf)[RT][D / 32],
                                              const int32_t (&rpos)[RT], float (&m)[RT],
                                              f32x4 (&o)[RT][D / 16], f32x4 (&ol)[RT], uint32_t lane) {
   using O = Ops<F16>;
-  const uint32_t row = lane & 15, grp = lane >> 4;
+  constexpr uint32_t kHalf = 16 * D * 2;  // bytes from a 16-key half to the next
+  const uint32_t grp = lane >> 4;
   // S^T = K . Q^T for every row tile; each K fragment is read from LDS once
   f32x4 s[RT][2];
 #pragma unroll
   for (int t = 0; t < RT; ++t) s[t][0] = s[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int st = 0; st < D / 32; ++st) {
+    const char* kp = reinterpret_cast<const char*>(ks) + off.k[st];
 #pragma unroll
-    for (int st = 0; st < D / 32; ++st) {
-      const uint32_t key = 16 * h + row;
-      const typename O::A8 kf = *reinterpret_cast<const typename O::A8*>(
-          &ks[key * D + ((4 * st + grp) ^ lds_swizzle<D>(key)) * 8]);
+    for (int h = 0; h < 2; ++h) {
+      const typename O::A8 kf = *reinterpret_cast<const typename O::A8*>(kp + h * kHalf);
 #pragma unroll
       for (int t = 0; t < RT; ++t) s[t][h] = O::mma32(kf, qf[t][st], s[t][h]);
     }
+  }
   typename O::A4 pa[RT][2];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
@@ -214,15 +243,12 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
     // lane (row, grp) addresses key 16h + 4 grp + row / 4, dims 16c + 4 (row % 4) .. + 3 of
     // the row-major V block; ds_read_tr16_b64 hands lane j of each 16-lane group element i of
     // its group's lane 4i + j / 4, i.e. V[16h + 4 grp + i][16c + j]
-    const uint32_t dim = 16 * c + 4 * (row & 3);
+    const char* vp = reinterpret_cast<const char*>(vs) + off.v[c];
     s16x4v w[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t vkey = 16 * h + 4 * grp + (row >> 2);
-      const uint16_t* vp = &vs[vkey * D + (((dim / 8) ^ lds_swizzle<D>(vkey)) * 8) + (dim & 4)];
+    for (int h = 0; h < 2; ++h)
       w[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4v*)((__attribute__((address_space(3))) const void*)vp));
-    }
+          (__attribute__((address_space(3))) s16x4v*)((__attribute__((address_space(3))) const void*)(vp + h * kHalf)));
     const typename O::A8 vb =
         __builtin_bit_cast(typename O::A8, __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
@@ -246,15 +272,17 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vbuf[kBuffers][kKeyBlock * D];
   __shared__ int32_t s_max[4];
   using O = Ops<F16>;
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave-uniform values in scalar registers (readfirstlane: a division by a
+  // runtime value runs on the VALU), so what derives from them stays scalar
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t row = lane & 15, grp = lane >> 4;
   // workgroup -> (row tile, kv head), the kv head fastest and the latest
   // tiles (most keys) first: work is dispatched in decreasing order across
   // all heads
-  const uint32_t kvh = blockIdx.x % a.hkv;
+  const uint32_t kvh = __builtin_amdgcn_readfirstlane(blockIdx.x % a.hkv);
   const uint32_t nrows = a.nq * a.group;
   const uint32_t ntiles = (nrows + kRows - 1) / kRows;
-  const uint32_t tile = ntiles - 1 - blockIdx.x / a.hkv;
+  const uint32_t tile = __builtin_amdgcn_readfirstlane(ntiles - 1 - blockIdx.x / a.hkv);
   const uint32_t r_wave = tile * kRows + wave * 16 * RT;
 
   // this lane's rows (one per row tile): (query, head) and their Q fragments
@@ -320,30 +348,62 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
     const uint16_t* kb = a.k + int64_t(k0) * a.k_stride;
     const uint16_t* vb = a.v + int64_t(k0) * a.v_stride;
     const uint32_t lk = lds_address(kbuf[buf]), lv = lds_address(vbuf[buf]);
-    const uint32_t last = uint32_t(min(int32_t(a.nk) - 1 - k0, kKeyBlock - 1));
+    if (k0 + kKeyBlock <= int32_t(a.nk)) {
 #pragma unroll
-    for (uint32_t j = 0; j < kInsts; ++j) {
-      const uint32_t back = krow[j] - min(krow[j], last);  // rows to step back past nk
-      lds_dma16(kb, koff[j] - uint32_t(back * a.k_stride * 2), lk + (wave * kInsts + j) * 1024);
-      lds_dma16(vb, voff[j] - uint32_t(back * a.v_stride * 2), lv + (wave * kInsts + j) * 1024);
+      for (uint32_t j = 0; j < kInsts; ++j) {
+        lds_dma16(kb, koff[j], lk + (wave * kInsts + j) * 1024);
+        lds_dma16(vb, voff[j], lv + (wave * kInsts + j) * 1024);
+      }
+    } else {
+      const uint32_t last = uint32_t(int32_t(a.nk) - 1 - k0);
+#pragma unroll
+      for (uint32_t j = 0; j < kInsts; ++j) {
+        const uint32_t back = krow[j] - min(krow[j], last);  // rows to step back past nk
+        lds_dma16(kb, koff[j] - uint32_t(back * a.k_stride * 2), lk + (wave * kInsts + j) * 1024);
+        lds_dma16(vb, voff[j] - uint32_t(back * a.v_stride * 2), lv + (wave * kInsts + j) * 1024);
+      }
     }
+  };
+  const BlockOffsets<D> off(lane);
+  // this wave's blocks: [0, b_m) are visible to all of its rows, [b_m, b_w)
+  // masked, [b_w, nblocks) past its latest position (skipped; the wave still
+  // takes its part in the requests and barriers). Each kind runs in a loop of
+  // its own: no register copies between variants in the hot loop.
+  const int32_t wmin_s = __builtin_amdgcn_readfirstlane(wmin), wmax_s = __builtin_amdgcn_readfirstlane(wmax);
+  const int32_t b_w = wmax_s < 0 ? 0 : min(wmax_s / kKeyBlock + 1, nblocks);
+  const int32_t b_m = wmax_s < 0 ? 0 : min(int32_t((int64_t(wmin_s) + 1) / kKeyBlock), b_w);
+  // one block, in buffer b % 3: BUF names it at compile time (then every
+  // LDS read address is a lane's offset register plus a constant the DS
+  // instruction's offset field carries), or -1 for a runtime choice
+  auto step = [&](auto kind, auto bufc, int32_t b) {
+    constexpr int K = decltype(kind)::value;  // 0 visible, 1 masked, 2 skipped
+    constexpr int BUF = decltype(bufc)::value;
+    CBK_WAIT_VM_LGKM0(2 * kInsts);  // block b has landed; the newest block may be pending
+    asm volatile("s_barrier" ::: "memory");
+    const int buf = BUF >= 0 ? BUF : b % kBuffers;
+    request(b + 2, (buf + 2) % kBuffers);  // into the buffers computed one block ago
+    if constexpr (K < 2)
+      attend_block<F16, D, RT, K == 1>(kbuf[buf], vbuf[buf], off, b * kKeyBlock, a.scale, qf, rpos, m, o, ol,
+                                       lane);
+  };
+  // blocks [b, end): three at a time from a multiple of 3 (buffers 0, 1, 2
+  // fixed), single blocks at the edges
+  auto run = [&](auto kind, int32_t b, int32_t end) {
+    using any = std::integral_constant<int, -1>;
+    for (; b < end && b % kBuffers != 0; ++b) step(kind, any(), b);
+    for (; b + kBuffers <= end; b += kBuffers) {
+      step(kind, std::integral_constant<int, 0>(), b);
+      step(kind, std::integral_constant<int, 1>(), b + 1);
+      step(kind, std::integral_constant<int, 2>(), b + 2);
+    }
+    for (; b < end; ++b) step(kind, any(), b);
   };
   if (nblocks > 0) {
     request(0, 0);
     request(1, 1);
-    for (int32_t b = 0; b < nblocks; ++b) {
-      CBK_WAIT_VM_LGKM0(2 * kInsts);  // block b has landed; the newest block may be pending
-      asm volatile("s_barrier" ::: "memory");
-      request(b + 2, (b + 2) % kBuffers);  // into the buffers computed one block ago
-      const int32_t k0 = b * kKeyBlock;
-      const int buf = b % kBuffers;
-      if (k0 <= wmax) {
-        if (k0 + kKeyBlock - 1 > wmin)
-          attend_block<F16, D, RT, true>(kbuf[buf], vbuf[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
-        else
-          attend_block<F16, D, RT, false>(kbuf[buf], vbuf[buf], k0, a.scale, qf, rpos, m, o, ol, lane);
-      }
-    }
+    run(std::integral_constant<int, 0>(), 0, b_m);
+    run(std::integral_constant<int, 1>(), b_m, b_w);
+    run(std::integral_constant<int, 2>(), b_w, nblocks);
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight past this point
   }
   __syncthreads();  // every wave is done with the K buffers the output staging reuses
