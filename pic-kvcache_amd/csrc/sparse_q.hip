@@ -647,6 +647,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     qoff[j] = (row * D + ((lane % P) ^ lds_swizzle<D>(row)) * 8) * 2;
   }
   const uint32_t toff = (lane % kTileWords) * 4;
+  // wave 0's statistics request: 8 lanes (128 bytes) per head of the chunk;
+  // with every chunk whole (FULL) the lanes' offsets are the same each unit
+  const uint32_t soff_full = (((lane / 8) % kHeadChunk) * a.nq_pad + (lane % 8) * 2) * 8;
   // Issues unit i (clamped: a request past the end repeats the last unit, so
   // every iteration issues the same number of requests) into buffer b: the
   // Q rows, and on wave 0 the row statistics and the tile record.
@@ -658,10 +661,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 #pragma unroll
     for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(unit, qoff[j], lq + (wave * kInsts + j) * 1024);
     if (wave == 0) {
-      const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
-      const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // 8 lanes (128 bytes) per head
       const float2* st = a.stats + int64_t(g * a.groups + hc * kHeadChunk) * a.nq_pad + qt * kQTile;
-      lds_dma16(st, (hl * a.nq_pad + (lane % 8) * 2) * 8, lds_address(sbuf[b]));
+      uint32_t soff = soff_full;
+      if constexpr (!FULL) {
+        const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
+        const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // heads past the chunk repeat its last
+        soff = (hl * a.nq_pad + (lane % 8) * 2) * 8;
+      }
+      lds_dma16(st, soff, lds_address(sbuf[b]));
       lds_dma4(a.tiles + kTileWords * qt, toff, lds_address(tbuf[b]));
     }
   };
