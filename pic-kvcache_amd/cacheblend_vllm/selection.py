@@ -263,15 +263,16 @@ def sparse_q_full_scores(
     return out, full
 
 
-def sparse_q_masks(gap_mask: torch.Tensor, tail_query_tokens: int, radius: int):
+def sparse_q_masks(gap_mask: torch.Tensor, tail_query_tokens: int, radius: int, gap_count: int | None = None):
     """``(query_mask, forced_mask, has_gap)`` (reference ascend.py:652-671).
 
     Without gaps the last ``min(tail, N)`` tokens are queries and forced;
     with gaps and ``radius`` > 0 the forced set is dilated (``cbk_dilate``).
+    ``gap_count``, when the caller has read it already, spares a host read.
     """
     query_mask = gap_mask.clone()
     forced = gap_mask.clone()
-    has_gap = bool(gap_mask.any().item())
+    has_gap = (gap_count > 0) if gap_count is not None else bool(gap_mask.any().item())
     if not has_gap:
         tail = min(tail_query_tokens, gap_mask.shape[0])
         query_mask[-tail:] = True
@@ -279,6 +280,19 @@ def sparse_q_masks(gap_mask: torch.Tensor, tail_query_tokens: int, radius: int):
     if radius and has_gap:
         forced |= dilate(gap_mask, radius)
     return query_mask, forced, has_gap
+
+
+def sparse_q_query_rows(query_mask: torch.Tensor, has_gap: bool, gap_count: int, tail_query_tokens: int):
+    """The rows of ``query_mask`` in index order (``torch.nonzero``), with
+    their count known from ``sparse_q_masks``' rule -- the gaps, else the
+    tail, all N for a tail of 0 as Python's ``x[-0:]`` is ``x`` -- so the
+    compaction needs no host read of its own."""
+    n = int(query_mask.shape[0])
+    if has_gap:
+        n_rows = gap_count
+    else:
+        n_rows = min(tail_query_tokens, n) if tail_query_tokens else n
+    return torch.nonzero_static(query_mask, size=n_rows).flatten()
 
 
 @dataclass
@@ -343,9 +357,10 @@ class BlendSelector:
         here (the kernel streams K through registers and LDS).
         """
         radius = self.config.overflow_blocks * self.block_size
-        query_mask, forced, has_gap = sparse_q_masks(gap_mask, self.config.tail_query_tokens, radius)
-        sparse = torch.nonzero(query_mask).flatten()
-        gap_count = int(gap_mask.sum().item())
+        gap_count = int(gap_mask.sum().item())  # the one host read before the scores
+        tail = self.config.tail_query_tokens
+        query_mask, forced, has_gap = sparse_q_masks(gap_mask, tail, radius, gap_count=gap_count)
+        sparse = sparse_q_query_rows(query_mask, has_gap, gap_count, tail)
         scores, _ = sparse_q_full_scores(query, key, sparse, absolute_indices, scale,
                                          out_index=absolute_indices)
         stats = {

@@ -89,6 +89,24 @@ def test_cpu_tensors_have_no_fallback():
         scatter_paged_kv(torch.zeros(2, 3, 2), paged, torch.tensor([0, 3, 4]), 2)
 
 
+def test_sparse_q_query_rows_match_nonzero():
+    # the query-row compaction sized from the gap count, without a host read
+    # of its own, against torch.nonzero on the masks of reference
+    # ascend.py:652-671 (gaps; no gaps with a tail shorter, longer, and 0)
+    from cacheblend_vllm.selection import sparse_q_masks, sparse_q_query_rows
+
+    g = torch.Generator().manual_seed(0)
+    cases = [(torch.rand(257, generator=g) < 0.2, 16), (torch.zeros(40, dtype=torch.bool), 7),
+             (torch.zeros(5, dtype=torch.bool), 9), (torch.zeros(6, dtype=torch.bool), 0),
+             (torch.ones(6, dtype=torch.bool), 3)]
+    for gap, tail in cases:
+        count = int(gap.sum())
+        query_mask, _, has_gap = sparse_q_masks(gap, tail, 0, gap_count=count)
+        assert has_gap == bool(gap.any())
+        rows = sparse_q_query_rows(query_mask, has_gap, count, tail)
+        assert torch.equal(rows, torch.nonzero(query_mask).flatten())
+
+
 def test_config_matches_reference_rules():
     # reference tests/test_config_registry.py behaviour: unknown fields fail
     with pytest.raises(ValueError, match="Unknown CacheBlend config fields"):
