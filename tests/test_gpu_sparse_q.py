@@ -80,6 +80,12 @@ def _inputs(n_active, prefix, hq, hkv, d, dtype, seed):
     (torch.bfloat16, 64, 24, 4),
     (torch.float16, 64, 4, 4),
     (torch.bfloat16, 128, 16, 1),
+    # 9-15 heads per KV head: the 32x32 row pass with head slots past the
+    # group; 12 leaves each wave's second pair tile half used, 9 leaves it
+    # unused on three of the four waves (skipped)
+    (torch.bfloat16, 128, 24, 2),
+    (torch.bfloat16, 64, 9, 1),
+    (torch.float16, 128, 12, 1),
 ])
 def test_sparse_q_scores_vs_oracle(dtype, d, hq, hkv):
     n_active, prefix = 1200 if dtype != torch.float32 else 300, 500
