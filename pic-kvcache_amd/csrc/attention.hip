@@ -47,7 +47,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
+// waves per workgroup: 8 at head_dim 128 (128 rows share each K/V block,
+// two workgroups per CU, four waves per SIMD), 4 at head_dim 64 (a 4 KiB
+// block is four 1 KiB requests)
+template <int D> constexpr int kWaves = D == 128 ? 8 : 4;
 constexpr int kRowTiles = 1;  // 16-row tiles per wave (2 needs ~290 registers: one wave per SIMD, slower)
 constexpr int kKeyBlock = 32;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -262,15 +265,20 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
 // (global_load_lds, explicit vmcnt waits, plain s_barrier; see the LDS DMA
 // helpers): the block computed, the next (landed), the one after (in flight).
 template <bool F16, int D, int RT>
-__global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
-  constexpr int kRows = 4 * 16 * RT;  // rows per workgroup
+__global__ __launch_bounds__(64 * kWaves<D>) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_kernel(
+    const AttnArgs a) {
+  constexpr int W = kWaves<D>;
+  constexpr int kRows = W * 16 * RT;  // rows per workgroup
   constexpr uint32_t P = D / 8;                      // 16-byte pieces per key row
-  constexpr uint32_t kInsts = kKeyBlock * P / 64 / 4; // requests per wave per block, each of K and V
+  constexpr uint32_t kInsts = kKeyBlock * P / 64 / W; // requests per wave per block, each of K and V
   constexpr uint32_t kRowsPerInst = 64 / P;
   constexpr int kBuffers = 3;
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[kBuffers][kKeyBlock * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[kBuffers][kKeyBlock * D];
-  __shared__ int32_t s_max[4];
+  static_assert(kInsts >= 1 && W * 16 * D <= 2 * kBuffers * kKeyBlock * D, "wave count vs block and staging");
+  // K blocks, then V blocks; the output staging reuses the whole region
+  __shared__ __attribute__((aligned(16))) uint16_t kvbuf[2][kBuffers][kKeyBlock * D];
+  auto& kbuf = kvbuf[0];
+  auto& vbuf = kvbuf[1];
+  __shared__ int32_t s_max[W];
   using O = Ops<F16>;
   // wave-uniform values in scalar registers (readfirstlane: a division by a
   // runtime value runs on the VALU), so what derives from them stays scalar
@@ -314,7 +322,10 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
   if (lane == 0) s_max[wave] = wmax;
   __syncthreads();
   // workgroup-uniform: a scalar loop bound
-  const int32_t gmax = __builtin_amdgcn_readfirstlane(max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])));
+  int32_t gm = s_max[0];
+#pragma unroll
+  for (int w = 1; w < W; ++w) gm = max(gm, s_max[w]);
+  const int32_t gmax = __builtin_amdgcn_readfirstlane(gm);
   // blocks up to the latest position, within the context
   const int32_t nblocks =
       gmax < 0 ? 0 : min((gmax + kKeyBlock) / kKeyBlock, (int32_t(a.nk) + kKeyBlock - 1) / kKeyBlock);
@@ -382,20 +393,18 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
     asm volatile("s_barrier" ::: "memory");
     const int buf = BUF >= 0 ? BUF : b % kBuffers;
     request(b + 2, (buf + 2) % kBuffers);  // into the buffers computed one block ago
+    uint32_t kb_addr = lds_address(kbuf[buf]), vb_addr = lds_address(vbuf[buf]);
+    asm volatile("" : "+s"(kb_addr), "+s"(vb_addr));
     if constexpr (K < 2)
-      attend_block<F16, D, RT, K == 1>(kbuf[buf], vbuf[buf], off, b * kKeyBlock, a.scale, qf, rpos, m, o, ol,
-                                       lane);
+      attend_block<F16, D, RT, K == 1>(
+          (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)kb_addr,
+          (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)vb_addr, off, b * kKeyBlock,
+          a.scale, qf, rpos, m, o, ol, lane);
   };
   // blocks [b, end): three at a time from a multiple of 3 (buffers 0, 1, 2
   // fixed), single blocks at the edges
   auto run = [&](auto kind, int32_t b, int32_t end) {
     using any = std::integral_constant<int, -1>;
-    for (; b < end && b % kBuffers != 0; ++b) step(kind, any(), b);
-    for (; b + kBuffers <= end; b += kBuffers) {
-      step(kind, std::integral_constant<int, 0>(), b);
-      step(kind, std::integral_constant<int, 1>(), b + 1);
-      step(kind, std::integral_constant<int, 2>(), b + 2);
-    }
     for (; b < end; ++b) step(kind, any(), b);
   };
   if (nblocks > 0) {
@@ -410,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const AttnArgs a) {
 
   // normalize and write, one row tile at a time through the wave's LDS
   // staging area (the K buffers are free now): whole 16-byte pieces per row
-  uint16_t* os = &kbuf[0][0] + wave * 16 * D;
+  uint16_t* os = &kvbuf[0][0][0] + wave * 16 * D;
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     // row sums of the rounded probabilities, already in O's layout
@@ -561,17 +570,19 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
   a.scale = scale;
   const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
   constexpr int RT = kRowTiles;
-  const uint64_t groups = (nrows + 64 * RT - 1) / (64 * RT) * uint64_t(hkv);
-  CBK_REQUIRE(groups * kThreads < (uint64_t(1) << 32), "blend attention: %llu workgroups exceed one launch",
+  const uint32_t waves = head_dim == 128 ? kWaves<128> : kWaves<64>;
+  const uint64_t rows_per_wg = 16 * RT * uint64_t(waves);
+  const uint64_t groups = (nrows + rows_per_wg - 1) / rows_per_wg * uint64_t(hkv);
+  CBK_REQUIRE(groups * 64 * waves < (uint64_t(1) << 32), "blend attention: %llu workgroups exceed one launch",
               (unsigned long long)groups);
-  const dim3 grid(static_cast<uint32_t>(groups));
+  const dim3 grid(static_cast<uint32_t>(groups)), block(64 * waves);
   const bool f16 = dtype == CBK_DTYPE_F16;
   if (head_dim == 128) {
-    if (f16) hipLaunchKernelGGL((attn_kernel<true, 128, RT>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<false, 128, RT>), grid, dim3(kThreads), 0, s, a);
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 128, RT>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 128, RT>), grid, block, 0, s, a);
   } else {
-    if (f16) hipLaunchKernelGGL((attn_kernel<true, 64, RT>), grid, dim3(kThreads), 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<false, 64, RT>), grid, dim3(kThreads), 0, s, a);
+    if (f16) hipLaunchKernelGGL((attn_kernel<true, 64, RT>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<false, 64, RT>), grid, block, 0, s, a);
   }
   return launch_status("blend attention");
 }
