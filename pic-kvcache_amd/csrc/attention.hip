@@ -47,11 +47,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// waves per workgroup: 8 at head_dim 128 (128 rows share each K/V block,
-// two workgroups per CU, four waves per SIMD), 4 at head_dim 64 (a 4 KiB
-// block is four 1 KiB requests)
-template <int D> constexpr int kWaves = D == 128 ? 8 : 4;
-constexpr int kRowTiles = 1;  // 16-row tiles per wave (2 needs ~290 registers: one wave per SIMD, slower)
+// 4 waves per workgroup, each with two 16-row tiles: every K and V fragment
+// read from LDS serves 32 rows, a K/V block 128 (184 registers: two waves
+// per SIMD, two workgroups per CU at head_dim 128). Measured against 8 waves
+// of one tile (four waves per SIMD): 2.02-2.04 vs 2.12-2.15 ms per C3 layer.
+constexpr int kWaves = 4;
+constexpr int kRowTiles = 2;  // 16-row tiles per wave
 constexpr int kKeyBlock = 32;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
@@ -265,9 +266,9 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
 // (global_load_lds, explicit vmcnt waits, plain s_barrier; see the LDS DMA
 // helpers): the block computed, the next (landed), the one after (in flight).
 template <bool F16, int D, int RT>
-__global__ __launch_bounds__(64 * kWaves<D>) __attribute__((amdgpu_waves_per_eu(4, 4))) void attn_kernel(
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel(
     const AttnArgs a) {
-  constexpr int W = kWaves<D>;
+  constexpr int W = kWaves;
   constexpr int kRows = W * 16 * RT;  // rows per workgroup
   constexpr uint32_t P = D / 8;                      // 16-byte pieces per key row
   constexpr uint32_t kInsts = kKeyBlock * P / 64 / W; // requests per wave per block, each of K and V
@@ -570,7 +571,7 @@ extern "C" int cbk_blend_attention(const void* q_dev, int64_t q_row_stride_elems
   a.scale = scale;
   const uint64_t nrows = uint64_t(nq) * uint64_t(a.group);
   constexpr int RT = kRowTiles;
-  const uint32_t waves = head_dim == 128 ? kWaves<128> : kWaves<64>;
+  const uint32_t waves = kWaves;
   const uint64_t rows_per_wg = 16 * RT * uint64_t(waves);
   const uint64_t groups = (nrows + rows_per_wg - 1) / rows_per_wg * uint64_t(hkv);
   CBK_REQUIRE(groups * 64 * waves < (uint64_t(1) << 32), "blend attention: %llu workgroups exceed one launch",
