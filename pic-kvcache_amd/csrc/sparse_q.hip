@@ -284,22 +284,27 @@ __device__ __forceinline__ void rowstats_block_wide(const SqArgs& a, const uint1
 
 // K blocks of 64 keys stream through three LDS buffers by DMA, as the query
 // units do in colsum (see there for the wait and barrier scheme).
-// FULL: the group is exactly 4 * MAXT heads, so every wave has MAXT row tiles
-// (a compile-time count: no branch between the tiles of a block).
-template <typename V, int KSTEPS, int MAXT, int RMODE, bool FULL>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_rowstats_kernel(
-    const SqArgs a) {
+// FULL: the group is exactly (4 / TPW) * MAXT heads, so every wave has MAXT
+// row tiles (a compile-time count: no branch between the tiles of a block).
+// TPW: query tiles per workgroup. With 2, two waves serve each of two
+// adjacent tiles (sorted queries: nearby positions) with twice the head slots,
+// so each K fragment read from LDS serves 64 rows (two waves per SIMD).
+template <typename V, int KSTEPS, int MAXT, int RMODE, bool FULL, int TPW = 1>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TPW == 2 ? 2 : 3, TPW == 2 ? 2 : 3)))
+void sq_rowstats_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per key row
   constexpr uint32_t kInsts = P / 4;              // requests per wave per block (1 KiB each)
   constexpr uint32_t kRowsPerInst = 64 / P;
   constexpr int kBuffers = 3;
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[kBuffers][kKeyBlock1 * D];
-  __shared__ int32_t s_pos[kQTile];
-  __shared__ int32_t s_minmax[2];
+  constexpr int WT = 4 / TPW;  // waves per query tile
+  __shared__ int32_t s_pos[kQTile * TPW];
+  __shared__ int32_t s_minmax[2];  // over the workgroup's tiles
   // the wave index in a scalar register: what derives from it stays scalar
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
+  const uint32_t ngroups = (ntiles + TPW - 1) / TPW;  // workgroups' tile groups
   // workgroup -> (tile, key range, kv head), the kv head fastest and the
   // latest tiles (most keys) first, so that workgroups are dispatched in
   // decreasing order of work across all heads
@@ -307,24 +312,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // the results back to scalar registers)
   const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x % a.hkv);
   const uint32_t chunk = __builtin_amdgcn_readfirstlane((blockIdx.x / a.hkv) % a.row_chunks);
-  const uint32_t qt = __builtin_amdgcn_readfirstlane(ntiles - 1 - blockIdx.x / (a.hkv * a.row_chunks));
+  const uint32_t qt_first = TPW * __builtin_amdgcn_readfirstlane(ngroups - 1 - blockIdx.x / (a.hkv * a.row_chunks));
+  const uint32_t wt = wave / WT, wv = wave % WT;  // this wave's tile in the workgroup, its place there
+  const uint32_t qt = qt_first + wt;               // this wave's tile (past ntiles: an odd last group)
+  const bool tile_ok = qt < ntiles;
   const uint32_t q0 = qt * kQTile;
-  if (threadIdx.x < kQTile) s_pos[threadIdx.x] = query_pos(a, q0 + threadIdx.x);
+  if (threadIdx.x < kQTile * TPW) s_pos[threadIdx.x] = query_pos(a, qt_first * kQTile + threadIdx.x);
   __syncthreads();
   if (threadIdx.x == 0) {
     int32_t lo = 0x7fffffff, hi = -1;
-    for (int i = 0; i < kQTile; ++i) {
-      if (q0 + i < a.nq) {
-        lo = min(lo, s_pos[i]);
-        hi = max(hi, s_pos[i]);
+    for (int u = 0; u < TPW; ++u) {
+      int32_t tlo = 0x7fffffff, thi = -1;
+      for (int i = 0; i < kQTile; ++i) {
+        if ((qt_first + u) * kQTile + i < a.nq) {
+          tlo = min(tlo, s_pos[u * kQTile + i]);
+          thi = max(thi, s_pos[u * kQTile + i]);
+        }
+      }
+      lo = min(lo, tlo);
+      hi = max(hi, thi);
+      if (g == 0 && chunk == 0 && qt_first + u < ntiles) {
+        a.tiles[kTileWords * (qt_first + u) + kQTile] = tlo;
+        a.tiles[kTileWords * (qt_first + u) + kQTile + 1] = thi;
       }
     }
     s_minmax[0] = lo;
     s_minmax[1] = hi;
-    if (g == 0 && chunk == 0) {
-      a.tiles[kTileWords * qt + kQTile] = lo;
-      a.tiles[kTileWords * qt + kQTile + 1] = hi;
-    }
   }
   __syncthreads();
   // workgroup-uniform, and scalar: the key-block loop and its branches stay
@@ -339,7 +352,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // 16 heads per KV head 7% faster; at 8 heads the 16x16 form measured 1-3%
   // faster, the 32x32 form's busier co-execution lowering the clock that
   // the power limit allows).
-  constexpr bool WIDE = MAXT == 4;
+  constexpr bool WIDE = MAXT == 4 && TPW == 1;
   constexpr int NT = WIDE ? MAXT / 2 : MAXT;    // row tiles
   constexpr int NR = WIDE ? 1 : 4;              // rows per lane and tile
   constexpr int NS = WIDE ? D / 16 : KSTEPS;    // MFMA steps over the head dim
@@ -348,28 +361,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   const uint32_t d0 = WIDE ? 8 * (lane >> 5) : 8 * rgrp;  // this lane's dims within a step
   int32_t rpos[NR];
 #pragma unroll
-  for (int i = 0; i < NR; ++i) rpos[i] = s_pos[WIDE ? col : 4 * rgrp + i];
+  for (int i = 0; i < NR; ++i) rpos[i] = s_pos[wt * kQTile + (WIDE ? col : 4 * rgrp + i)];
   const uint32_t qi = q0 + col;
 
   V afrag[NT][NS];
   float m[NT][NR], l[NT][NR];
-  const int nslots = FULL ? MAXT : (a.groups > wave) ? int((a.groups - wave + 3) / 4) : 0;
+  const int nslots = FULL ? MAXT : (a.groups > wv) ? int((a.groups - wv + WT - 1) / WT) : 0;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int slot = WIDE ? 2 * t + int(rgrp & 1) : t;
     const char* row = (slot < nslots && qi < a.nq)
-                          ? query_row(a, qi, g * a.groups + wave + 4 * slot, 2) : nullptr;
+                          ? query_row(a, qi, g * a.groups + wv + WT * slot, 2) : nullptr;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
       afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (kStepDims * s + d0) * 2) : V(0);
     // the dense copy colsum streams (zeros past nq)
-    if (slot < nslots && chunk == 0) {
-      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wave + 4 * slot) * (kQTile * D) + col * D;
+    if (slot < nslots && chunk == 0 && tile_ok) {
+      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wv + WT * slot) * (kQTile * D) + col * D;
 #pragma unroll
       for (int s = 0; s < NS; ++s) *reinterpret_cast<V*>(dst + kStepDims * s + d0) = afrag[t][s];
     }
   }
-  if (g == 0 && chunk == 0 && threadIdx.x < kQTile) a.tiles[kTileWords * qt + threadIdx.x] = s_pos[threadIdx.x];
+  if (g == 0 && chunk == 0 && threadIdx.x < kQTile * TPW && qt_first + threadIdx.x / kQTile < ntiles)
+    a.tiles[kTileWords * (qt_first + threadIdx.x / kQTile) + threadIdx.x % kQTile] = s_pos[threadIdx.x];
   // nothing of the compiler's own in flight once the requests start
   CBK_WAIT_VM_LGKM0(0);
 
@@ -480,9 +494,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         stats_merge(mm, ll, mo, lo);
       }
       const int slot = WIDE ? 2 * t + int(rgrp & 1) : t;
-      const uint32_t h = g * a.groups + wave + 4 * slot;
+      const uint32_t h = g * a.groups + wv + WT * slot;
       const uint32_t q = q0 + (WIDE ? col : 4 * rgrp + i);  // rows past nq too: colsum reads whole tiles
-      if ((WIDE ? lane < 32 : col == 0) && slot < nslots) {
+      if ((WIDE ? lane < 32 : col == 0) && slot < nslots && tile_ok) {
         if (a.row_chunks == 1)
           a.stats[int64_t(h) * a.nq_pad + q] = row_stats(mm, ll);
         else
@@ -835,8 +849,8 @@ int device_cus(int* cus) {
 // slot are dispatched in decreasing order of work.
 constexpr uint32_t kRowChunkTarget = 3;  // rowstats workgroups per resident slot (about)
 
-uint32_t row_chunks(uint32_t units, int cus) {
-  const uint32_t slots = 3u * uint32_t(cus);  // rowstats: three workgroups per CU
+uint32_t row_chunks(uint32_t units, int cus, uint32_t per_cu) {
+  const uint32_t slots = per_cu * uint32_t(cus);  // rowstats workgroups resident per CU
   const uint32_t k = units ? (kRowChunkTarget * slots + units - 1) / units : 1u;
   return std::max(1u, std::min(kMaxRowChunks, k));
 }
@@ -846,21 +860,25 @@ template <typename V, int RMODE, int KS>
 int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   const uint64_t ntiles = (a.nq + kQTile - 1) / kQTile;
   const uint64_t kblocks = (a.nk + kKeyBlock2 - 1) / kKeyBlock2;
-  a.row_chunks = row_chunks(uint32_t(ntiles * a.hkv), cus);
+  // 8 heads per KV head: two tiles per workgroup, four head slots per wave
+  // (two workgroups per CU); otherwise one tile (three per CU)
+  const bool pair = a.groups == 8;
+  const uint64_t tgroups = pair ? (ntiles + 1) / 2 : ntiles;
+  a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, pair ? 2u : 3u);
   // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
-  CBK_REQUIRE(ntiles * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
+  CBK_REQUIRE(tgroups * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
                   kblocks * a.hkv * kThreads < (uint64_t(1) << 32) &&
                   uint64_t(a.hq) * a.nq_pad < (uint64_t(1) << 32),
               "sparse_q: %llu query tiles x %llu key blocks x %u kv heads exceed one launch",
               (unsigned long long)ntiles, (unsigned long long)kblocks, a.hkv);
-  const dim3 g1(uint32_t(ntiles * a.hkv * a.row_chunks));
+  const dim3 g1(uint32_t(tgroups * a.hkv * a.row_chunks));
   const dim3 g2(uint32_t(kblocks * a.hkv));
   if (a.groups == 4)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 4)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
-  else if (a.groups == 8)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
+  else if (pair)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true, 2>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 8)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups == 16)
