@@ -7,8 +7,8 @@
 // with r rounding to the input dtype (the reference's bf16/f16 einsum output
 // and its "* scale"), the softmax in float32, G = Hq / Hkv.
 //
-// One workgroup (4 waves) per (64 rows of (query, group head), kv head):
-// row r of the 64 is query r / G, head kv * G + r % G, so the K/V tiles
+// One workgroup (4 waves) per (128 rows of (query, group head), kv head):
+// row r of the 128 is query r / G, head kv * G + r % G, so the K/V tiles
 // staged in LDS serve all G heads of several queries. Per 32-key block:
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K rows, B = Q rows,
 //                   both 16-byte loads of 8 consecutive dims; the result
@@ -21,8 +21,10 @@
 //                   contraction runs in that key order); B needs those keys
 //                   of one dim, which two ds_read_tr16_b64 gather from the
 //                   row-major V block
-// K/V blocks stream through three LDS buffers each by DMA (global_load_lds);
-// the row tiles with the latest positions (most keys) are scheduled first.
+// software-pipelined: the step of block b issues S^T of block b+1 and P . V
+// of block b-1 beside the softmax of block b. K/V blocks stream through
+// rings of three LDS buffers by DMA (global_load_lds); the row tiles with the
+// latest positions (most keys) are scheduled first.
 // MFMA layout (checked on gfx950): 16x16x32 A[i][k] in lane i+16*(k/8)
 // element k%8, B[k][j] in lane j+16*(k/8); D[i][j] in lane j+16*(i/4),
 // register i%4.
@@ -48,8 +50,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 4 waves per workgroup, each with two 16-row tiles: every K and V fragment
-// read from LDS serves 32 rows, a K/V block 128 (184 registers: two waves
-// per SIMD, two workgroups per CU at head_dim 128). Measured against 8 waves
+// read from LDS serves 32 rows, a K/V block 128 (217 registers with the
+// software pipeline: two waves per SIMD, two workgroups per CU at head_dim
+// 128). Measured against 8 waves
 // of one tile (four waves per SIMD): 2.02-2.04 vs 2.12-2.15 ms per C3 layer.
 constexpr int kWaves = 4;
 constexpr int kRowTiles = 2;  // 16-row tiles per wave
@@ -144,20 +147,13 @@ struct BlockOffsets {
   }
 };
 
-// ks, vs: the block's K and V buffers. With the buffer a compile-time choice
-// (the caller's), a read's address is the lane's offset register plus a
-// constant that the DS instruction's offset field carries.
-template <bool F16, int D, int RT, bool MASK>
-__device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t* vs, const BlockOffsets<D>& off,
-                                             int32_t k0, float scale,
-                                             const typename Ops<F16>::A8 (&qf)[RT][D / 32],
-                                             const int32_t (&rpos)[RT], float (&m)[RT],
-                                             f32x4 (&o)[RT][D / 16], f32x4 (&ol)[RT], uint32_t lane) {
+// S^T = K . Q^T of one block (K buffer ks) for every row tile; each K
+// fragment is read from LDS once.
+template <bool F16, int D, int RT>
+__device__ __forceinline__ void qk_block(const uint16_t* ks, const BlockOffsets<D>& off,
+                                         const typename Ops<F16>::A8 (&qf)[RT][D / 32], f32x4 (&s)[RT][2]) {
   using O = Ops<F16>;
   constexpr uint32_t kHalf = 16 * D * 2;  // bytes from a 16-key half to the next
-  const uint32_t grp = lane >> 4;
-  // S^T = K . Q^T for every row tile; each K fragment is read from LDS once
-  f32x4 s[RT][2];
 #pragma unroll
   for (int t = 0; t < RT; ++t) s[t][0] = s[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -170,11 +166,18 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
       for (int t = 0; t < RT; ++t) s[t][h] = O::mma32(kf, qf[t][st], s[t][h]);
     }
   }
-  typename O::A4 pa[RT][2];
+}
+
+// The block's logits in place of its S^T: x = r(r(dot) * scale), as the
+// dtype's einsum and multiply produce them (MASK: -inf past each row's
+// position); lm[t] = this lane's maximum over its logits of row tile t, taken
+// before the second rounding (rounding is monotonic, and the reference
+// maximum only needs to bound the logits within the rescale headroom).
+template <bool F16, int RT, bool MASK>
+__device__ __forceinline__ void logits_block(f32x4 (&s)[RT][2], int32_t k0, float scale, const int32_t (&rpos)[RT],
+                                             float (&lm)[RT], uint32_t grp) {
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    // y = r(dot) * scale; the logits are x = r(y), as the dtype's einsum and
-    // multiply produce them
     float y[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -188,58 +191,52 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
           if (k0 + 16 * h + int32_t(4 * grp) + i > rpos[t]) y[h][i] = kNegInf;
       }
     }
-    // This lane's max over its 8 logits, taken before the second rounding
-    // (rounding is monotonic, and the reference max only needs to bound the
-    // logits within the rescale headroom).
-    const float lm = fmaxf(fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3])),
-                           fmaxf(fmaxf(y[1][0], y[1][1]), fmaxf(y[1][2], y[1][3])));
-    float x[2][4];
+    lm[t] = fmaxf(fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3])),
+                  fmaxf(fmaxf(y[1][0], y[1][1]), fmaxf(y[1][2], y[1][3])));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      x[h][0] = y[h][0]; x[h][1] = y[h][1]; x[h][2] = y[h][2]; x[h][3] = y[h][3];
-      round2<F16>(x[h][0], x[h][1]);
-      round2<F16>(x[h][2], x[h][3]);
+      round2<F16>(y[h][0], y[h][1]);
+      round2<F16>(y[h][2], y[h][3]);
+      s[t][h] = f32x4{y[h][0], y[h][1], y[h][2], y[h][3]};
     }
-    // Lazy rescaling: exponents stay relative to a reference max m that is
-    // raised -- and O rescaled -- only when some lane sees a logit above
-    // m + kRescale (log2 units); otherwise p <= 2^kRescale. The row max across
-    // the row's 4 lane groups is only needed then.
-    if (__any(lm * kLog2e > m[t] + kRescale)) {
-      float bm = lm;
-      bm = fmaxf(bm, __shfl_xor(bm, 16));
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
-      const float mn = fmaxf(m[t], bm * kLog2e + 1.f);  // +1: covers the second rounding
-      const float alpha = mn == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[t] - mn);
-      m[t] = mn;
-      float ao[4];
+  }
+}
+
+// p = 2^(x log2 e - m), rounded to the dtype: the A operand of P . V (the
+// two 16-key halves' registers, concatenated).
+template <bool F16, int RT>
+__device__ __forceinline__ void probs_block(const f32x4 (&x)[RT][2], const float (&m)[RT],
+                                            typename Ops<F16>::A8 (&pa)[RT]) {
+  using O = Ops<F16>;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha, int(4 * grp + i));
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        o[t][c][0] *= ao[0]; o[t][c][1] *= ao[1]; o[t][c][2] *= ao[2]; o[t][c][3] *= ao[3];
-      }
-      ol[t][0] *= ao[0]; ol[t][1] *= ao[1]; ol[t][2] *= ao[2]; ol[t][3] *= ao[3];
-    }
+  for (int t = 0; t < RT; ++t) {
     const float ms = m[t] == kNegInf ? 0.f : m[t];
+    typename O::A4 ph[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       float p[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[h][i], kLog2e, -ms));
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[t][h][i], kLog2e, -ms));
       const u32x2 pk = u32x2{O::pack(p[0], p[1]), O::pack(p[2], p[3])};
-      pa[t][h] = __builtin_bit_cast(typename O::A4, pk);
+      ph[h] = __builtin_bit_cast(typename O::A4, pk);
     }
+    pa[t] = __builtin_shufflevector(ph[0], ph[1], 0, 1, 2, 3, 4, 5, 6, 7);
   }
-  // O += P . V and the row sums l += P . 1, one 16x16x32 MFMA per 16-dim column
-  // tile for the block's 32 keys (two 16x16x16 MFMAs cost as much each). The
-  // contraction runs in this lane layout's key order: k-slot 8 grp + e holds
-  // key 4 grp + e for e < 4 and 16 + 4 grp + e - 4 after, in P (the S^T
-  // registers of the two 16-key halves, concatenated) and in V (two
-  // transposing reads, one per half, concatenated).
+}
+
+// O += P . V and the row sums l += P . 1, one 16x16x32 MFMA per 16-dim column
+// tile for the block's 32 keys (two 16x16x16 MFMAs cost as much each). The
+// contraction runs in this lane layout's key order: k-slot 8 grp + e holds
+// key 4 grp + e for e < 4 and 16 + 4 grp + e - 4 after, in P (the S^T
+// registers of the two 16-key halves, concatenated) and in V (two
+// transposing reads, one per half, concatenated).
+template <bool F16, int D, int RT>
+__device__ __forceinline__ void pv_block(const uint16_t* vs, const BlockOffsets<D>& off,
+                                         const typename Ops<F16>::A8 (&pa)[RT], f32x4 (&o)[RT][D / 16],
+                                         f32x4 (&ol)[RT]) {
+  using O = Ops<F16>;
+  constexpr uint32_t kHalf = 16 * D * 2;
   typedef short s16x4v __attribute__((ext_vector_type(4)));
-  typename O::A8 pa8[RT];
-#pragma unroll
-  for (int t = 0; t < RT; ++t) pa8[t] = __builtin_shufflevector(pa[t][0], pa[t][1], 0, 1, 2, 3, 4, 5, 6, 7);
   const typename O::A8 ones = __builtin_bit_cast(
       typename O::A8, u32x4{kOnesPair<F16>, kOnesPair<F16>, kOnesPair<F16>, kOnesPair<F16>});
 #pragma unroll
@@ -256,15 +253,15 @@ __device__ __forceinline__ void attend_block(const uint16_t* ks, const uint16_t*
     const typename O::A8 vb =
         __builtin_bit_cast(typename O::A8, __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-    for (int t = 0; t < RT; ++t) o[t][c] = O::mma32(pa8[t], vb, o[t][c]);
+    for (int t = 0; t < RT; ++t) o[t][c] = O::mma32(pa[t], vb, o[t][c]);
   }
 #pragma unroll
-  for (int t = 0; t < RT; ++t) ol[t] = O::mma32(pa8[t], ones, ol[t]);
+  for (int t = 0; t < RT; ++t) ol[t] = O::mma32(pa[t], ones, ol[t]);
 }
 
-// K and V blocks of 32 keys stream through three LDS buffers each by DMA
+// K and V blocks of 32 keys stream through rings of three LDS buffers by DMA
 // (global_load_lds, explicit vmcnt waits, plain s_barrier; see the LDS DMA
-// helpers): the block computed, the next (landed), the one after (in flight).
+// helpers): K three blocks ahead of the step that reads it, V one.
 template <bool F16, int D, int RT>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel(
     const AttnArgs a) {
@@ -352,68 +349,209 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     koff[j] = uint32_t((krow[j] * a.k_stride + kvh * D + piece * 8) * 2);
     voff[j] = uint32_t((krow[j] * a.v_stride + kvh * D + piece * 8) * 2);
   }
-  // block b (clamped: a request past the end repeats the last block) into
-  // buffer buf; rows past nk of the last block repeat its last key (masked)
-  auto request = [&](int32_t b, int buf) {
+  // K of block b into K buffer b % 3, V of block b into V buffer b % 3
+  // (clamped: a request past the end repeats the last block); rows past nk
+  // of the last block repeat its last key (masked)
+  auto request = [&](int32_t b, const uint16_t* src, int64_t stride, const uint32_t (&offs)[kInsts],
+                     uint16_t (&bufs)[kBuffers][kKeyBlock * D]) {
+    const uint32_t l = lds_address(bufs[b % kBuffers]);
     b = min(b, nblocks - 1);
     const int32_t k0 = b * kKeyBlock;
-    const uint16_t* kb = a.k + int64_t(k0) * a.k_stride;
-    const uint16_t* vb = a.v + int64_t(k0) * a.v_stride;
-    const uint32_t lk = lds_address(kbuf[buf]), lv = lds_address(vbuf[buf]);
+    const uint16_t* base = src + int64_t(k0) * stride;
     if (k0 + kKeyBlock <= int32_t(a.nk)) {
 #pragma unroll
-      for (uint32_t j = 0; j < kInsts; ++j) {
-        lds_dma16(kb, koff[j], lk + (wave * kInsts + j) * 1024);
-        lds_dma16(vb, voff[j], lv + (wave * kInsts + j) * 1024);
-      }
+      for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(base, offs[j], l + (wave * kInsts + j) * 1024);
     } else {
       const uint32_t last = uint32_t(int32_t(a.nk) - 1 - k0);
 #pragma unroll
       for (uint32_t j = 0; j < kInsts; ++j) {
         const uint32_t back = krow[j] - min(krow[j], last);  // rows to step back past nk
-        lds_dma16(kb, koff[j] - uint32_t(back * a.k_stride * 2), lk + (wave * kInsts + j) * 1024);
-        lds_dma16(vb, voff[j] - uint32_t(back * a.v_stride * 2), lv + (wave * kInsts + j) * 1024);
+        lds_dma16(base, offs[j] - uint32_t(back * stride * 2), l + (wave * kInsts + j) * 1024);
       }
     }
   };
   const BlockOffsets<D> off(lane);
   // this wave's blocks: [0, b_m) are visible to all of its rows, [b_m, b_w)
   // masked, [b_w, nblocks) past its latest position (skipped; the wave still
-  // takes its part in the requests and barriers). Each kind runs in a loop of
-  // its own: no register copies between variants in the hot loop.
+  // takes its part in the requests and barriers).
   const int32_t wmin_s = __builtin_amdgcn_readfirstlane(wmin), wmax_s = __builtin_amdgcn_readfirstlane(wmax);
   const int32_t b_w = wmax_s < 0 ? 0 : min(wmax_s / kKeyBlock + 1, nblocks);
   const int32_t b_m = wmax_s < 0 ? 0 : min(int32_t((int64_t(wmin_s) + 1) / kKeyBlock), b_w);
-  // one block, in buffer b % 3: BUF names it at compile time (then every
-  // LDS read address is a lane's offset register plus a constant the DS
-  // instruction's offset field carries), or -1 for a runtime choice
-  auto step = [&](auto kind, auto bufc, int32_t b) {
-    constexpr int K = decltype(kind)::value;  // 0 visible, 1 masked, 2 skipped
-    constexpr int BUF = decltype(bufc)::value;
-    CBK_WAIT_VM_LGKM0(2 * kInsts);  // block b has landed; the newest block may be pending
-    asm volatile("s_barrier" ::: "memory");
-    const int buf = BUF >= 0 ? BUF : b % kBuffers;
-    request(b + 2, (buf + 2) % kBuffers);  // into the buffers computed one block ago
-    uint32_t kb_addr = lds_address(kbuf[buf]), vb_addr = lds_address(vbuf[buf]);
-    asm volatile("" : "+s"(kb_addr), "+s"(vb_addr));
-    if constexpr (K < 2)
-      attend_block<F16, D, RT, K == 1>(
-          (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)kb_addr,
-          (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)vb_addr, off, b * kKeyBlock,
-          a.scale, qf, rpos, m, o, ol, lane);
+  // Software pipeline: step b takes S^T of block b + 1 on the MFMAs while
+  // the VALU turns block b's S^T into logits, then P . V of block b - 1
+  // while the VALU turns block b's logits into probabilities: the matrix
+  // cores and the VALU work on independent data in one instruction stream
+  // (MFMA/VALU co-execution 23% -> 42% of the MFMA busy time; under the
+  // power limit the clock fell 6%, so 2.11-2.12 -> 2.05-2.07 ms per C3 layer
+  // in same-box runs). K(b + 1) and V(b - 1) are read in step b.
+  // Lazy rescaling: exponents stay relative to a reference max m that is
+  // raised -- and O rescaled -- only when some lane sees a logit above
+  // m + kRescale (log2 units); otherwise p <= 2^kRescale. The row max across
+  // the row's 4 lane groups is only needed then. A raise found in step b
+  // rescales O in step b + 1, between P . V of block b - 1 (relative to the
+  // old m) and P . V of block b (relative to the new one): each step has one
+  // uniform branch, between its two halves.
+  bool pending = false;     // O still to be rescaled by alpha
+  float alpha[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) alpha[t] = 1.f;
+  auto rescale_o = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      float ao[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ao[i] = __shfl(alpha[t], int(4 * grp + i));
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        o[t][c][0] *= ao[0]; o[t][c][1] *= ao[1]; o[t][c][2] *= ao[2]; o[t][c][3] *= ao[3];
+      }
+      ol[t][0] *= ao[0]; ol[t][1] *= ao[1]; ol[t][2] *= ao[2]; ol[t][3] *= ao[3];
+    }
   };
-  // blocks [b, end): three at a time from a multiple of 3 (buffers 0, 1, 2
-  // fixed), single blocks at the edges
-  auto run = [&](auto kind, int32_t b, int32_t end) {
-    using any = std::integral_constant<int, -1>;
-    for (; b < end; ++b) step(kind, any(), b);
+  // The steps' request streams: K three blocks ahead of the step, V one,
+  // clamped at the last block (every block before it is whole). slot[0..2]
+  // are the K buffers of blocks b, b + 1, b + 2 (the V buffer of a block is
+  // kVOffset bytes after its K buffer).
+  constexpr uint32_t kSlot = kKeyBlock * D * 2, kVOffset = kBuffers * kSlot;
+  const int64_t kstep = int64_t(kKeyBlock) * a.k_stride * 2, vstep = int64_t(kKeyBlock) * a.v_stride * 2;
+  const bool last_whole = nblocks * kKeyBlock <= int32_t(a.nk);
+  const char* kg = reinterpret_cast<const char*>(a.k) + int64_t(min(3, nblocks - 1)) * kstep;
+  const char* vg = reinterpret_cast<const char*>(a.v) + int64_t(min(1, nblocks - 1)) * vstep;
+  uint32_t slot[3] = {lds_address(kbuf[0]), lds_address(kbuf[1]), lds_address(kbuf[2])};
+  auto stream = [&](int32_t j, const char*& g, int64_t stride_bytes, int64_t stride, const uint32_t (&offs)[kInsts],
+                    uint32_t l) __attribute__((always_inline)) {
+    const bool inner = j < nblocks - 1;
+    if (inner || last_whole) {
+#pragma unroll
+      for (uint32_t i = 0; i < kInsts; ++i) lds_dma16(g, offs[i], l + (wave * kInsts + i) * 1024);
+    } else {
+      const uint32_t last = uint32_t(int32_t(a.nk) - 1 - (nblocks - 1) * kKeyBlock);
+#pragma unroll
+      for (uint32_t i = 0; i < kInsts; ++i) {
+        const uint32_t back = krow[i] - min(krow[i], last);  // rows to step back past nk
+        lds_dma16(g, offs[i] - uint32_t(back * stride * 2), l + (wave * kInsts + i) * 1024);
+      }
+    }
+    if (inner) g += stride_bytes;
+  };
+  // KIND: 0 visible, 1 masked, 2 P . V of the wave's last block only, 3 no
+  // work; FIRST: no block before. sc holds S^T of block b, pp P of block
+  // b - 1; the step leaves S^T of block b + 1 in sn and P of block b in pc
+  // (two register sets taken in turn: no copies between steps).
+  auto step = [&](auto kind, auto first, int32_t b, f32x4 (&sc)[RT][2], f32x4 (&sn)[RT][2],
+                  typename O::A8 (&pp)[RT], typename O::A8 (&pc)[RT]) __attribute__((always_inline)) {
+    constexpr int KIND = decltype(kind)::value;
+    constexpr bool FIRST = decltype(first)::value;
+    CBK_WAIT_VM_LGKM0(2 * kInsts);  // K(b + 1) and V(b - 1) have landed
+    asm volatile("s_barrier" ::: "memory");
+    stream(b + 3, kg, kstep, a.k_stride, koff, slot[0]);             // into the K buffer block b used
+    stream(b + 1, vg, vstep, a.v_stride, voff, slot[1] + kVOffset);  // into the V buffer block b - 2 used
+    uint32_t kb_addr = slot[1], vb_addr = slot[2] + kVOffset;
+    const uint32_t s0 = slot[0];
+    slot[0] = slot[1];
+    slot[1] = slot[2];
+    slot[2] = s0;
+    if constexpr (KIND < 3) {
+      asm volatile("" : "+s"(kb_addr), "+s"(vb_addr));
+      const uint16_t* ks = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)kb_addr;
+      const uint16_t* vs = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)vb_addr;
+      if constexpr (KIND < 2) {
+        qk_block<F16, D, RT>(ks, off, qf, sn);
+        float lm[RT];
+        logits_block<F16, RT, KIND == 1>(sc, b * kKeyBlock, a.scale, rpos, lm, grp);
+        bool over = false;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) over |= lm[t] * kLog2e > m[t] + kRescale;
+        if (pending || __any(over)) {
+          if (pending) rescale_o();
+          pending = false;
+#pragma unroll
+          for (int t = 0; t < RT; ++t) {
+            alpha[t] = 1.f;
+            if (__any(lm[t] * kLog2e > m[t] + kRescale)) {
+              float bm = lm[t];
+              bm = fmaxf(bm, __shfl_xor(bm, 16));
+              bm = fmaxf(bm, __shfl_xor(bm, 32));
+              const float mn = fmaxf(m[t], bm * kLog2e + 1.f);  // +1: covers the second rounding
+              alpha[t] = mn == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[t] - mn);
+              m[t] = mn;
+              pending = true;
+            }
+          }
+        }
+        probs_block<F16, RT>(sc, m, pc);
+        if constexpr (!FIRST) pv_block<F16, D, RT>(vs, off, pp, o, ol);
+        // P of block b is computed here, beside P . V of block b - 1 (the
+        // compiler would otherwise sink it to its use in the next step)
+#pragma unroll
+        for (int t = 0; t < RT; ++t) asm volatile("" : "+v"(pc[t]));
+      } else if constexpr (!FIRST) {
+        if (pending) rescale_o();
+        pending = false;
+        pv_block<F16, D, RT>(vs, off, pp, o, ol);
+      }
+    }
+  };
+  using visible = std::integral_constant<int, 0>;
+  using masked = std::integral_constant<int, 1>;
+  using last = std::integral_constant<int, 2>;
+  using none = std::integral_constant<int, 3>;
+  using yes = std::true_type;
+  using no = std::false_type;
+  f32x4 sa[RT][2], sb[RT][2];
+  typename O::A8 pa[RT], pb[RT];
+  // steps [b, end) of one kind, two at a time; S^T of block b in sa and P of
+  // block b - 1 in pa before and after
+  auto run = [&](auto kind, int32_t& b, int32_t end) __attribute__((always_inline)) {
+    for (; b + 1 < end; b += 2) {
+      step(kind, no(), b, sa, sb, pa, pb);
+      step(kind, no(), b + 1, sb, sa, pb, pa);
+    }
+    if (b < end) {
+      step(kind, no(), b++, sa, sb, pa, pb);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        sa[t][0] = sb[t][0];
+        sa[t][1] = sb[t][1];
+        pa[t] = pb[t];
+      }
+    }
   };
   if (nblocks > 0) {
-    request(0, 0);
-    request(1, 1);
-    run(std::integral_constant<int, 0>(), 0, b_m);
-    run(std::integral_constant<int, 1>(), b_m, b_w);
-    run(std::integral_constant<int, 2>(), b_w, nblocks);
+    // K of blocks 0-2 and V of block 0 ahead of step 0; then every wave
+    // takes steps 0 .. nblocks (the requests and barriers of each)
+    request(0, a.k, a.k_stride, koff, kbuf);
+    request(1, a.k, a.k_stride, koff, kbuf);
+    request(2, a.k, a.k_stride, koff, kbuf);
+    request(0, a.v, a.v_stride, voff, vbuf);
+    CBK_WAIT_VM_LGKM0(3 * kInsts);  // K(0) has landed
+    asm volatile("s_barrier" ::: "memory");
+    if (b_w > 0) {
+      qk_block<F16, D, RT>((const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)lds_address(
+                               kbuf[0]),
+                           off, qf, sa);
+    }
+    int32_t b = 0;
+    auto first = [&](auto kind) __attribute__((always_inline)) {
+      step(kind, yes(), b++, sa, sb, pa, pb);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        sa[t][0] = sb[t][0];
+        sa[t][1] = sb[t][1];
+        pa[t] = pb[t];
+      }
+    };
+    if (b_m > 0)
+      first(visible());
+    else if (b_w > 0)
+      first(masked());
+    run(visible(), b, b_m);
+    run(masked(), b, b_w);
+    if (b_w > 0)
+      step(last(), no(), b++, sa, sb, pa, pb);
+    else
+      step(none(), yes(), b++, sa, sb, pa, pb);
+    for (; b <= nblocks; ++b) step(none(), no(), b, sa, sb, pa, pb);
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight past this point
   }
   __syncthreads();  // every wave is done with the K buffers the output staging reuses

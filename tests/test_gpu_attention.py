@@ -149,3 +149,25 @@ def test_blend_attention_partial_key_blocks(nq, nk, d):
     print(f"nq={q.shape[0]} nk={nk} d={d}", flush=True)
     got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, 0.7)
     _check(got, _oracle(q, k, v, pos, 0.7, "bf16"), f"nq={q.shape[0]} nk={nk} d={d}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_blend_attention_rising_row_maxima(dtype):
+    """Logits that rise along the keys: the running maximum is raised block
+    after block (every block over the first 320 keys, every few blocks over
+    the next 512), then stays; half of the heads see the logits falling
+    instead (a maximum in the first block, never raised). Exact dots: q is
+    +-1/8 in every dim, key j is t_j / 8 in every dim, so q.k_j = +-2 t_j."""
+    nq, nk, hq, hkv, d = 200, 1200, 8, 2, 128
+    g = torch.Generator().manual_seed(77)
+    j = torch.arange(nk)
+    t = torch.where(j < 320, j // 16 - 16, 4 + (j - 320) // 64)
+    t = torch.where(j < 832, t, torch.randint(-16, 13, (nk,), generator=g))
+    k = (t[:, None, None] / 8).expand(nk, hkv, d).to(dtype)
+    sign = torch.tensor([1.0, -1.0]).repeat(hq // 2)
+    q = (sign[None, :, None] / 8).expand(nq, hq, d).to(dtype)
+    v = torch.randn(nk, hkv, d, generator=g).to(dtype)
+    pos = torch.randperm(nk, generator=g)[:nq].sort().values
+    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, 2.0)
+    rounding = "bf16" if dtype == torch.bfloat16 else "f16"
+    _check(got, _oracle(q, k, v, pos, 2.0, rounding), f"rising maxima {dtype}")
