@@ -60,6 +60,7 @@ def _check(got, want_mass, label):
     (torch.bfloat16, 8, 8, 64),
     (torch.float16, 16, 2, 128),
     (torch.bfloat16, 12, 4, 64),   # G = 3: row tiles straddle queries unevenly
+    (torch.float16, 8, 2, 64),
 ])
 def test_blend_attention_matches_oracle(dtype, hq, hkv, d):
     nq, nk = 300, 1500
@@ -151,14 +152,15 @@ def test_blend_attention_partial_key_blocks(nq, nk, d):
     _check(got, _oracle(q, k, v, pos, 0.7, "bf16"), f"nq={q.shape[0]} nk={nk} d={d}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_blend_attention_rising_row_maxima(dtype):
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 128), (torch.bfloat16, 64)])
+def test_blend_attention_rising_row_maxima(dtype, d):
     """Logits that rise along the keys: the running maximum is raised block
     after block (every block over the first 320 keys, every few blocks over
     the next 512), then stays; half of the heads see the logits falling
     instead (a maximum in the first block, never raised). Exact dots: q is
-    +-1/8 in every dim, key j is t_j / 8 in every dim, so q.k_j = +-2 t_j."""
-    nq, nk, hq, hkv, d = 200, 1200, 8, 2, 128
+    +-1/8 in every dim, key j is t_j / 8 in every dim, so q.k_j = +-d t_j / 64
+    (scale 256 / d: logits +-4 t_j at both head sizes)."""
+    nq, nk, hq, hkv = 200, 1200, 8, 2
     g = torch.Generator().manual_seed(77)
     j = torch.arange(nk)
     t = torch.where(j < 320, j // 16 - 16, 4 + (j - 320) // 64)
@@ -168,6 +170,7 @@ def test_blend_attention_rising_row_maxima(dtype):
     q = (sign[None, :, None] / 8).expand(nq, hq, d).to(dtype)
     v = torch.randn(nk, hkv, d, generator=g).to(dtype)
     pos = torch.randperm(nk, generator=g)[:nq].sort().values
-    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, 2.0)
+    scale = 256.0 / d  # the same logits at both head sizes
+    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, scale)
     rounding = "bf16" if dtype == torch.bfloat16 else "f16"
-    _check(got, _oracle(q, k, v, pos, 2.0, rounding), f"rising maxima {dtype}")
+    _check(got, _oracle(q, k, v, pos, scale, rounding), f"rising maxima {dtype} d={d}")
