@@ -186,14 +186,16 @@ def test_sparse_q_full_layer6_properties():
     assert np.array_equal(again.cpu().numpy().astype(np.float64), full)
 
 
+@pytest.mark.parametrize("hq", [8, 16])
 @pytest.mark.parametrize("n_active,prefix,d", [(1, 0, 128), (5, 0, 64), (17, 40, 128), (63, 1, 64),
                                                 (64, 0, 128), (65, 63, 128), (200, 3, 64)])
-def test_sparse_q_small_contexts(n_active, prefix, d):
+def test_sparse_q_small_contexts(n_active, prefix, d, hq):
     """1 to 265 keys and 1 to 200 queries: partial 64-key blocks (rows past
     the context repeat the last key and are masked), single and partial
     16-query tiles (rows past the queries are zeros, masked in the column
-    pass)."""
-    hq, hkv = 8, 2
+    pass). 16 query heads over 2 KV heads take the row pass that pairs
+    adjacent tiles: 1 and 5 tiles leave the last pair's second tile empty."""
+    hkv = 2
     g = torch.Generator().manual_seed(n_active * 7 + prefix)
     nk = prefix + n_active
     q = (torch.randn(n_active, hq, d, generator=g) / d ** 0.5).to(torch.bfloat16)
