@@ -383,7 +383,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   // cores and the VALU work on independent data in one instruction stream
   // (MFMA/VALU co-execution 23% -> 42% of the MFMA busy time; under the
   // power limit the clock fell 6%, so 2.11-2.12 -> 2.05-2.07 ms per C3 layer
-  // in same-box runs). K(b + 1) and V(b - 1) are read in step b.
+  // in same-box runs). K(b + 1) and V(b - 1) are read in step b. The loops
+  // take six steps at a time, so that the ring buffers and the register sets
+  // of every step are known at compile time: no per-read address adds
+  // (1.99 -> 1.93 ms per C3 layer in same-box runs).
   // Lazy rescaling: exponents stay relative to a reference max m that is
   // raised -- and O rescaled -- only when some lane sees a logit above
   // m + kRescale (log2 units); otherwise p <= 2^kRescale. The row max across
@@ -409,15 +412,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     }
   };
   // The steps' request streams: K three blocks ahead of the step, V one,
-  // clamped at the last block (every block before it is whole). slot[0..2]
-  // are the K buffers of blocks b, b + 1, b + 2 (the V buffer of a block is
-  // kVOffset bytes after its K buffer).
+  // clamped at the last block (every block before it is whole). Block j's K
+  // goes to K buffer j % 3, its V to V buffer j % 3 (kVOffset bytes after
+  // that K buffer).
   constexpr uint32_t kSlot = kKeyBlock * D * 2, kVOffset = kBuffers * kSlot;
   const int64_t kstep = int64_t(kKeyBlock) * a.k_stride * 2, vstep = int64_t(kKeyBlock) * a.v_stride * 2;
   const bool last_whole = nblocks * kKeyBlock <= int32_t(a.nk);
   const char* kg = reinterpret_cast<const char*>(a.k) + int64_t(min(3, nblocks - 1)) * kstep;
   const char* vg = reinterpret_cast<const char*>(a.v) + int64_t(min(1, nblocks - 1)) * vstep;
-  uint32_t slot[3] = {lds_address(kbuf[0]), lds_address(kbuf[1]), lds_address(kbuf[2])};
   auto stream = [&](int32_t j, const char*& g, int64_t stride_bytes, int64_t stride, const uint32_t (&offs)[kInsts],
                     uint32_t l) __attribute__((always_inline)) {
     const bool inner = j < nblocks - 1;
@@ -435,24 +437,37 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     if (inner) g += stride_bytes;
   };
   // KIND: 0 visible, 1 masked, 2 P . V of the wave's last block only, 3 no
-  // work; FIRST: no block before. sc holds S^T of block b, pp P of block
-  // b - 1; the step leaves S^T of block b + 1 in sn and P of block b in pc
-  // (two register sets taken in turn: no copies between steps).
-  auto step = [&](auto kind, auto first, int32_t b, f32x4 (&sc)[RT][2], f32x4 (&sn)[RT][2],
+  // work; FIRST: no block before; PHASE: b % 6 when known at compile time
+  // (then every LDS address is a lane's offset plus a constant the DS
+  // instruction's offset field carries), or -1. sc holds S^T of block b, pp
+  // P of block b - 1; the step leaves S^T of block b + 1 in sn and P of
+  // block b in pc (two register sets taken in turn: no copies between
+  // steps).
+  auto step = [&](auto kind, auto first, auto phase, int32_t b, f32x4 (&sc)[RT][2], f32x4 (&sn)[RT][2],
                   typename O::A8 (&pp)[RT], typename O::A8 (&pc)[RT]) __attribute__((always_inline)) {
     constexpr int KIND = decltype(kind)::value;
     constexpr bool FIRST = decltype(first)::value;
+    constexpr int PHASE = decltype(phase)::value;
     CBK_WAIT_VM_LGKM0(2 * kInsts);  // K(b + 1) and V(b - 1) have landed
     asm volatile("s_barrier" ::: "memory");
-    stream(b + 3, kg, kstep, a.k_stride, koff, slot[0]);             // into the K buffer block b used
-    stream(b + 1, vg, vstep, a.v_stride, voff, slot[1] + kVOffset);  // into the V buffer block b - 2 used
-    uint32_t kb_addr = slot[1], vb_addr = slot[2] + kVOffset;
-    const uint32_t s0 = slot[0];
-    slot[0] = slot[1];
-    slot[1] = slot[2];
-    slot[2] = s0;
-    if constexpr (KIND < 3) {
+    uint32_t kb_addr, vb_addr, kw_addr, vw_addr;
+    if constexpr (PHASE >= 0) {
+      kw_addr = lds_address(kbuf[PHASE % 3]);
+      vw_addr = lds_address(vbuf[(PHASE + 1) % 3]);
+      kb_addr = lds_address(kbuf[(PHASE + 1) % 3]);
+      vb_addr = lds_address(vbuf[(PHASE + 2) % 3]);
+    } else {
+      const uint32_t r = uint32_t(b) % 3;
+      const uint32_t k0 = lds_address(kbuf[0]);
+      kw_addr = k0 + r * kSlot;
+      kb_addr = k0 + (r == 2 ? 0 : r + 1) * kSlot;
+      vw_addr = kb_addr + kVOffset;
+      vb_addr = k0 + (r == 0 ? 2 : r - 1) * kSlot + kVOffset;
       asm volatile("" : "+s"(kb_addr), "+s"(vb_addr));
+    }
+    stream(b + 3, kg, kstep, a.k_stride, koff, kw_addr);  // into the K buffer block b used
+    stream(b + 1, vg, vstep, a.v_stride, voff, vw_addr);  // into the V buffer block b - 2 used
+    if constexpr (KIND < 3) {
       const uint16_t* ks = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)kb_addr;
       const uint16_t* vs = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)vb_addr;
       if constexpr (KIND < 2) {
@@ -500,22 +515,32 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   using no = std::false_type;
   f32x4 sa[RT][2], sb[RT][2];
   typename O::A8 pa[RT], pb[RT];
-  // steps [b, end) of one kind, two at a time; S^T of block b in sa and P of
-  // block b - 1 in pa before and after
-  auto run = [&](auto kind, int32_t& b, int32_t end) __attribute__((always_inline)) {
-    for (; b + 1 < end; b += 2) {
-      step(kind, no(), b, sa, sb, pa, pb);
-      step(kind, no(), b + 1, sb, sa, pb, pa);
-    }
-    if (b < end) {
-      step(kind, no(), b++, sa, sb, pa, pb);
+  using any = std::integral_constant<int, -1>;
+  // one step with its buffers chosen at run time, S^T of block b in sa and P
+  // of block b - 1 in pa before and after
+  auto single = [&](auto kind, int32_t& b) __attribute__((always_inline)) {
+    step(kind, no(), any(), b++, sa, sb, pa, pb);
 #pragma unroll
-      for (int t = 0; t < RT; ++t) {
-        sa[t][0] = sb[t][0];
-        sa[t][1] = sb[t][1];
-        pa[t] = pb[t];
-      }
+    for (int t = 0; t < RT; ++t) {
+      sa[t][0] = sb[t][0];
+      sa[t][1] = sb[t][1];
+      pa[t] = pb[t];
     }
+  };
+  // steps [b, end) of one kind: six at a time from a multiple of 6 (the
+  // three-buffer rings and the two register sets back where they started),
+  // single steps at the edges
+  auto run = [&](auto kind, int32_t& b, int32_t end) __attribute__((always_inline)) {
+    while (b < end && b % 6 != 0) single(kind, b);
+    for (; b + 6 <= end; b += 6) {
+      step(kind, no(), std::integral_constant<int, 0>(), b, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 1>(), b + 1, sb, sa, pb, pa);
+      step(kind, no(), std::integral_constant<int, 2>(), b + 2, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 3>(), b + 3, sb, sa, pb, pa);
+      step(kind, no(), std::integral_constant<int, 4>(), b + 4, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 5>(), b + 5, sb, sa, pb, pa);
+    }
+    while (b < end) single(kind, b);
   };
   if (nblocks > 0) {
     // K of blocks 0-2 and V of block 0 ahead of step 0; then every wave
@@ -533,7 +558,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     }
     int32_t b = 0;
     auto first = [&](auto kind) __attribute__((always_inline)) {
-      step(kind, yes(), b++, sa, sb, pa, pb);
+      step(kind, yes(), any(), b++, sa, sb, pa, pb);
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
         sa[t][0] = sb[t][0];
@@ -548,10 +573,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     run(visible(), b, b_m);
     run(masked(), b, b_w);
     if (b_w > 0)
-      step(last(), no(), b++, sa, sb, pa, pb);
+      step(last(), no(), any(), b++, sa, sb, pa, pb);
     else
-      step(none(), yes(), b++, sa, sb, pa, pb);
-    for (; b <= nblocks; ++b) step(none(), no(), b, sa, sb, pa, pb);
+      step(none(), yes(), any(), b++, sa, sb, pa, pb);
+    for (; b <= nblocks; ++b) step(none(), no(), any(), b, sa, sb, pa, pb);
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight past this point
   }
   __syncthreads();  // every wave is done with the K buffers the output staging reuses
