@@ -50,7 +50,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 4 waves per workgroup, each with two 16-row tiles: every K and V fragment
-// read from LDS serves 32 rows, a K/V block 128 (217 registers with the
+// read from LDS serves 32 rows, a K/V block 128 (234 registers with the
 // software pipeline: two waves per SIMD, two workgroups per CU at head_dim
 // 128). Measured against 8 waves
 // of one tile (four waves per SIMD): 2.02-2.04 vs 2.12-2.15 ms per C3 layer.
