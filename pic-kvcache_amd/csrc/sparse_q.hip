@@ -664,14 +664,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // wave 0's statistics request: 8 lanes (128 bytes) per head of the chunk;
   // with every chunk whole (FULL) the lanes' offsets are the same each unit
   const uint32_t soff_full = (((lane / 8) % kHeadChunk) * a.nq_pad + (lane % 8) * 2) * 8;
-  // Issues unit i (clamped: a request past the end repeats the last unit, so
-  // every iteration issues the same number of requests) into buffer b: the
-  // Q rows, and on wave 0 the row statistics and the tile record.
-  auto request = [&](int32_t i, int b) {
-    i = min(i, nunits - 1);
-    const uint32_t qt = uint32_t(ntiles - 1 - i / int32_t(nchunks)), hc = uint32_t(i) % nchunks;
+  // Issues the unit of tile qt, head chunk hc (a request past the last unit
+  // repeats it, so every iteration issues the same number of requests) into
+  // buffer B: the Q rows, and on wave 0 the row statistics and the tile record.
+  auto request = [&](int32_t qt, uint32_t hc, auto bc) __attribute__((always_inline)) {
+    constexpr int B = decltype(bc)::value;
     const uint16_t* unit = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + hc * kHeadChunk) * (kQTile * D);
-    const uint32_t lq = lds_address(qbuf[b]);
+    const uint32_t lq = lds_address(qbuf[B]);
 #pragma unroll
     for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(unit, qoff[j], lq + (wave * kInsts + j) * 1024);
     if (wave == 0) {
@@ -682,37 +681,66 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // heads past the chunk repeat its last
         soff = (hl * a.nq_pad + (lane % 8) * 2) * 8;
       }
-      lds_dma16(st, soff, lds_address(sbuf[b]));
-      lds_dma4(a.tiles + kTileWords * qt, toff, lds_address(tbuf[b]));
+      lds_dma16(st, soff, lds_address(sbuf[B]));
+      lds_dma4(a.tiles + kTileWords * qt, toff, lds_address(tbuf[B]));
+    }
+  };
+  // units in order: the head chunks of tile ntiles - 1, then of the tile
+  // below, down to tile tlo (stepped without divisions)
+  auto next = [&](int32_t& qt, uint32_t& hc) __attribute__((always_inline)) {
+    if (++hc == nchunks) {
+      hc = 0;
+      --qt;
     }
   };
   if (nunits > 0) {
-    request(0, 0);
-    request(1, 1);
-    for (int32_t it = 0; it < nunits; ++it) {
+    int32_t qt_c = ntiles - 1, qt_r = ntiles - 1;  // unit it, and the unit requested in iteration it
+    uint32_t hc_c = 0, hc_r = 0;
+    auto request_next = [&](int32_t i, auto bc) __attribute__((always_inline)) {
+      if (i < nunits) {
+        request(qt_r, hc_r, bc);
+        next(qt_r, hc_r);
+      } else {
+        request(tlo, nchunks - 1, bc);
+      }
+    };
+    request_next(0, std::integral_constant<int, 0>());
+    request_next(1, std::integral_constant<int, 1>());
+    // unit it in buffer B = it % 3, known at compile time in a loop of three
+    // iterations: every LDS address is a lane's offset plus a constant
+    auto iteration = [&](int32_t it, auto bc) __attribute__((always_inline)) {
+      constexpr int B = decltype(bc)::value;
       // unit it has landed once at most the newest unit's requests are pending
       if (wave == 0)
         CBK_WAIT_VM_LGKM0(kInsts + 2);
       else
         CBK_WAIT_VM_LGKM0(kInsts);
       asm volatile("s_barrier" ::: "memory");
-      request(it + 2, (it + 2) % kQBuffers);  // into the buffer computed one unit ago
-      const int b = it % kQBuffers;
-      const int32_t qt = ntiles - 1 - it / int32_t(nchunks);
-      const uint32_t hc = uint32_t(it) % nchunks;
-      const int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[b][kQTile]);  // uniform: scalar
-      const int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[b][kQTile + 1]);
+      request_next(it + 2, std::integral_constant<int, (B + 2) % kQBuffers>());  // the buffer computed one unit ago
+      const int32_t qt = qt_c;
+      const uint32_t hc = hc_c;
+      next(qt_c, hc_c);
+      const int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile]);  // uniform: scalar
+      const int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile + 1]);
       if (tmax >= kw0) {
         int32_t rpos[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rpos[i] = tbuf[b][4 * rgrp + i];
+        for (int i = 0; i < 4; ++i) rpos[i] = tbuf[B][4 * rgrp + i];
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
         if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt) * kQTile + kQTile > a.nq)
-          colsum_unit<V, KSTEPS, RMODE, true, FULL>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, true, FULL>(a, qbuf[B], sbuf[B], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
         else
-          colsum_unit<V, KSTEPS, RMODE, false, FULL>(a, qbuf[b], sbuf[b], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, false, FULL>(a, qbuf[B], sbuf[B], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
       }
+    };
+    int32_t it = 0;
+    for (; it + 3 <= nunits; it += 3) {
+      iteration(it, std::integral_constant<int, 0>());
+      iteration(it + 1, std::integral_constant<int, 1>());
+      iteration(it + 2, std::integral_constant<int, 2>());
     }
+    if (it < nunits) iteration(it++, std::integral_constant<int, 0>());
+    if (it < nunits) iteration(it++, std::integral_constant<int, 1>());
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight when the workgroup ends
   }
   // column totals: the 4 lane groups hold the same column
