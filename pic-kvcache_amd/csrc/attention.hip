@@ -58,6 +58,7 @@ constexpr int kWaves = 4;
 constexpr int kRowTiles = 2;  // 16-row tiles per wave
 constexpr int kKeyBlock = 32;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kRescale = 8.f;  // log2 headroom of the lazy softmax rescaling
 
@@ -203,20 +204,19 @@ __device__ __forceinline__ void logits_block(f32x4 (&s)[RT][2], int32_t k0, floa
 }
 
 // p = 2^(x log2 e - m), rounded to the dtype: the A operand of P . V (the
-// two 16-key halves' registers, concatenated).
+// two 16-key halves' registers, concatenated); nms = -m (0 while m is -inf).
 template <bool F16, int RT>
-__device__ __forceinline__ void probs_block(const f32x4 (&x)[RT][2], const float (&m)[RT],
+__device__ __forceinline__ void probs_block(const f32x4 (&x)[RT][2], const float (&nms)[RT],
                                             typename Ops<F16>::A8 (&pa)[RT]) {
   using O = Ops<F16>;
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    const float ms = m[t] == kNegInf ? 0.f : m[t];
     typename O::A4 ph[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       float p[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[t][h][i], kLog2e, -ms));
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(x[t][h][i], kLog2e, nms[t]));
       const u32x2 pk = u32x2{O::pack(p[0], p[1]), O::pack(p[2], p[3])};
       ph[h] = __builtin_bit_cast(typename O::A4, pk);
     }
@@ -328,11 +328,16 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   const int32_t nblocks =
       gmax < 0 ? 0 : min((gmax + kKeyBlock) / kKeyBlock, (int32_t(a.nk) + kKeyBlock - 1) / kKeyBlock);
 
-  float m[RT];
+  // per row tile: the reference max m (log2 units), -m for the exponents
+  // (0 while m is -inf), and the logit above which m is raised,
+  // (m + kRescale) ln 2 (all three change only when m is raised)
+  float m[RT], nms[RT], thr[RT];
   f32x4 o[RT][D / 16], ol[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     m[t] = kNegInf;
+    nms[t] = 0.f;
+    thr[t] = kNegInf;
     ol[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) o[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -474,27 +479,29 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
         qk_block<F16, D, RT>(ks, off, qf, sn);
         float lm[RT];
         logits_block<F16, RT, KIND == 1>(sc, b * kKeyBlock, a.scale, rpos, lm, grp);
-        bool over = false;
+        uint64_t over = 0;
 #pragma unroll
-        for (int t = 0; t < RT; ++t) over |= lm[t] * kLog2e > m[t] + kRescale;
-        if (pending || __any(over)) {
+        for (int t = 0; t < RT; ++t) over |= __ballot(lm[t] > thr[t]);
+        if (pending || over != 0) {
           if (pending) rescale_o();
           pending = false;
 #pragma unroll
           for (int t = 0; t < RT; ++t) {
             alpha[t] = 1.f;
-            if (__any(lm[t] * kLog2e > m[t] + kRescale)) {
+            if (__any(lm[t] > thr[t])) {
               float bm = lm[t];
               bm = fmaxf(bm, __shfl_xor(bm, 16));
               bm = fmaxf(bm, __shfl_xor(bm, 32));
               const float mn = fmaxf(m[t], bm * kLog2e + 1.f);  // +1: covers the second rounding
               alpha[t] = mn == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[t] - mn);
               m[t] = mn;
+              nms[t] = -mn;
+              thr[t] = (mn + kRescale) * kLn2;
               pending = true;
             }
           }
         }
-        probs_block<F16, RT>(sc, m, pc);
+        probs_block<F16, RT>(sc, nms, pc);
         if constexpr (!FIRST) pv_block<F16, D, RT>(vs, off, pp, o, ol);
         // P of block b is computed here, beside P . V of block b - 1 (the
         // compiler would otherwise sink it to its use in the next step)
