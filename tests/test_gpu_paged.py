@@ -13,10 +13,13 @@ DEV = torch.device("cuda", 0)
 
 
 def _np(t: torch.Tensor) -> np.ndarray:
-    """Bit pattern view on the host (bf16/f16 as uint16, f32 as f32)."""
+    """Bit pattern view on the host (bf16/f16 as uint16, 8-bit floats as
+    uint8, f32 as f32)."""
     t = t.detach().cpu()
     if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16)
+    if t.element_size() == 1 and t.dtype != torch.uint8:
+        return t.view(torch.uint8).numpy()
     return t.numpy()
 
 
@@ -182,3 +185,41 @@ def test_store_workload_round_trip_full_size():
     sample = torch.randperm(8192)[:256]
     want = O.gather_paged_kv(_np(pool), slots[sample].numpy(), 16)
     np.testing.assert_array_equal(_np(chunks[:, sample]), want)
+
+
+_RANDOM_DTYPES = [torch.uint8, torch.bfloat16, torch.float16, torch.float32] + (
+    [torch.float8_e4m3fn] if hasattr(torch, "float8_e4m3fn") else [])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_gather_scatter_random_shapes(seed):
+    """Seeded random layouts, dtypes (8-bit float KV caches included), block
+    sizes, head shapes and token counts, with random bit patterns (NaNs
+    included): the copies move bytes, bit-exact against the oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    layout = ["merged_first", "merged_block", "separate"][int(rng.integers(3))]
+    dtype = _RANDOM_DTYPES[seed % len(_RANDOM_DTYPES)]
+    nb = int(rng.integers(2, 300))
+    bs = int(rng.choice([1, 8, 16, 32]))
+    h = int(rng.integers(1, 9))
+    d = int(rng.choice([7, 64, 96, 128, 256]))
+    tokens = int(rng.integers(1, min(nb * bs, 3000) + 1))
+    print(f"seed={seed} layout={layout} dtype={dtype} nb={nb} bs={bs} h={h} d={d} tokens={tokens}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    es = torch.empty((), dtype=dtype).element_size()
+    raw = torch.randint(0, 256, (2 * nb * bs * h * d * es,), dtype=torch.uint8, generator=g)
+    base = raw.view(dtype).reshape(2, nb, bs, h, d).to(DEV)
+    paged = _layout(base, layout)
+    perm = torch.randperm(nb * bs, generator=g)
+    slots = perm[:tokens]
+    got = KL.gather_paged_kv(paged, slots.to(DEV), bs)
+    want = O.gather_paged_kv(_oracle_layer(paged), slots.numpy(), bs)
+    assert np.array_equal(_np(got).view(np.uint8), np.ascontiguousarray(want).view(np.uint8))
+    fresh_raw = torch.randint(0, 256, (got.numel() * es,), dtype=torch.uint8, generator=g)
+    fresh = fresh_raw.view(dtype).reshape(got.shape).to(DEV)
+    new_slots = perm[-tokens:]
+    expect = _oracle_layer(paged)
+    O.scatter_paged_kv(_np(fresh), expect, new_slots.numpy(), bs)
+    KL.scatter_paged_kv(fresh, paged, new_slots, bs)
+    for p_, e in (zip(paged, expect) if isinstance(paged, list) else [(paged, expect)]):
+        assert np.array_equal(_np(p_).view(np.uint8), np.ascontiguousarray(e).view(np.uint8))
