@@ -174,3 +174,24 @@ def test_blend_attention_rising_row_maxima(dtype, d):
     got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, scale)
     rounding = "bf16" if dtype == torch.bfloat16 else "f16"
     _check(got, _oracle(q, k, v, pos, scale, rounding), f"rising maxima {dtype} d={d}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_blend_attention_random_shapes(seed):
+    """Seeded random shapes: 1-200 queries at sorted or unsorted positions
+    over 1-1500 keys, 1-8 query heads per KV head, head_dim 64 or 128, bf16
+    or f16, scales from 0.05 to 2."""
+    rng = np.random.default_rng(500 + seed)
+    nk = int(rng.integers(1, 1501))
+    nq = int(rng.integers(1, min(nk, 200) + 1))
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4, 8]))
+    d = int(rng.choice([64, 128]))
+    dtype = [torch.bfloat16, torch.float16][seed % 2]
+    scale = float(rng.uniform(0.05, 2.0))
+    sorted_positions = bool(rng.integers(2))
+    q, k, v, pos = _case(nq, nk, hq, hkv, d, dtype, seed=seed, sorted_positions=sorted_positions)
+    label = f"seed={seed} nq={nq} nk={nk} hq={hq} hkv={hkv} d={d} {dtype} scale={scale:.3f} sorted={sorted_positions}"
+    print(label, flush=True)
+    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, scale)
+    _check(got, _oracle(q, k, v, pos, scale, "bf16" if dtype == torch.bfloat16 else "f16"), label)
