@@ -289,8 +289,17 @@ __device__ __forceinline__ void rowstats_block_wide(const SqArgs& a, const uint1
 // TPW: query tiles per workgroup. With 2, two waves serve each of two
 // adjacent tiles (sorted queries: nearby positions) with twice the head slots,
 // so each K fragment read from LDS serves 64 rows (two waves per SIMD).
+// Two waves per SIMD for paired tiles (238 registers at head_dim 128) and
+// for four head slots per wave at head_dim 128 (236 registers; three waves
+// per SIMD spilled 224 bytes per lane); three waves per SIMD otherwise (two
+// head slots at head_dim 128 spill 96 bytes per lane there, yet two waves
+// per SIMD measured slower: 2.21-2.23 vs 1.99-2.00 ms at 5 heads per KV
+// head, 1.35 vs 1.30 ms at 6, on 32K-key layers).
+constexpr bool rs_two_waves(int tpw, int maxt, int ksteps) {
+  return tpw == 2 || (ksteps == 4 && maxt == 4);
+}
 template <typename V, int KSTEPS, int MAXT, int RMODE, bool FULL, int TPW = 1>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TPW == 2 || MAXT == 4 ? 2 : 3, TPW == 2 || MAXT == 4 ? 2 : 3)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(rs_two_waves(TPW, MAXT, KSTEPS) ? 2 : 3, rs_two_waves(TPW, MAXT, KSTEPS) ? 2 : 3)))
 void sq_rowstats_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per key row
@@ -351,9 +360,9 @@ void sq_rowstats_kernel(const SqArgs a) {
   // (157 against 168 registers and half the spills of the 16x16 form there:
   // 16 heads per KV head 7% faster; at 8 heads the 16x16 form measured 1-3%
   // faster, the 32x32 form's busier co-execution lowering the clock that
-  // the power limit allows). MAXT = 4 runs two waves per SIMD: 236
-  // registers and no spills, 3.26-3.28 -> 2.96-3.06 ms on a 64-head,
-  // 32K-key layer against three waves per SIMD with 224 bytes of spills.
+  // the power limit allows). At head_dim 128, MAXT = 4 runs two waves per
+  // SIMD: 236 registers and no spills, 3.26-3.28 -> 2.96-3.06 ms on a
+  // 64-head, 32K-key layer against three waves with 224 bytes of spills.
   constexpr bool WIDE = MAXT == 4 && TPW == 1;
   constexpr int NT = WIDE ? MAXT / 2 : MAXT;    // row tiles
   constexpr int NR = WIDE ? 1 : 4;              // rows per lane and tile
@@ -894,7 +903,7 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   // (two workgroups per CU); otherwise one tile (three per CU)
   const bool pair = a.groups == 8;
   const uint64_t tgroups = pair ? (ntiles + 1) / 2 : ntiles;
-  a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, pair || a.groups > 8 ? 2u : 3u);
+  a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, pair || (a.groups > 8 && KS == 4) ? 2u : 3u);
   // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
   CBK_REQUIRE(tgroups * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
                   kblocks * a.hkv * kThreads < (uint64_t(1) << 32) &&
