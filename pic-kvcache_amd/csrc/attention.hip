@@ -52,8 +52,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // 4 waves per workgroup, each with two 16-row tiles: every K and V fragment
 // read from LDS serves 32 rows, a K/V block 128 (234 registers with the
 // software pipeline: two waves per SIMD, two workgroups per CU at head_dim
-// 128). Measured against 8 waves
-// of one tile (four waves per SIMD): 2.02-2.04 vs 2.12-2.15 ms per C3 layer.
+// 128; 152-157 registers and three waves per SIMD at head_dim 64, which
+// measured 1.28-1.31 ms against 1.44 ms at two on a 32-head, 8-KV-head,
+// 32K-key layer). Measured against 8 waves of one tile (four waves per
+// SIMD): 2.02-2.04 vs 2.12-2.15 ms per C3 layer.
 constexpr int kWaves = 4;
 constexpr int kRowTiles = 2;  // 16-row tiles per wave
 constexpr int kKeyBlock = 32;
@@ -263,7 +265,7 @@ __device__ __forceinline__ void pv_block(const uint16_t* vs, const BlockOffsets<
 // (global_load_lds, explicit vmcnt waits, plain s_barrier; see the LDS DMA
 // helpers): K three blocks ahead of the step that reads it, V one.
 template <bool F16, int D, int RT>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel(
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : 2, D == 64 ? 3 : 2))) void attn_kernel(
     const AttnArgs a) {
   constexpr int W = kWaves;
   constexpr int kRows = W * 16 * RT;  // rows per workgroup
