@@ -243,3 +243,33 @@ def test_sparse_q_rows_far_above_their_first_block(big_key):
     assert seen > 0
     print(f"big key {big_key}: {seen} of every third query see it; score {full[big_key]:.1f}", flush=True)
     assert full[big_key] > 0.8 * seen * hq   # the big key takes most of those rows' mass
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_sparse_q_random_shapes(seed):
+    """Seeded random shapes: 1-16 query heads per KV head over 1-4 KV heads,
+    head_dim 64 or 128, bf16 or f16, 1-600 queries picked anywhere in a
+    context of up to 2500 keys, an arbitrary first absolute position."""
+    rng = np.random.default_rng(700 + seed)
+    hkv = int(rng.integers(1, 5))
+    hq = hkv * int(rng.integers(1, 17))
+    d = int(rng.choice([64, 128]))
+    dtype = [torch.bfloat16, torch.float16][seed % 2]
+    prefix = int(rng.integers(0, 1000))
+    n_active = int(rng.integers(1, 1501))
+    nk = prefix + n_active
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(n_active, hq, d, generator=g) / d ** 0.5).to(dtype)
+    k = (torch.randn(nk, hkv, d, generator=g) / d ** 0.5).to(dtype)
+    absolute = torch.arange(prefix, nk)
+    n_rows = int(rng.integers(1, min(n_active, 600) + 1))
+    rows = torch.from_numpy(np.sort(rng.choice(n_active, n_rows, replace=False))).long()
+    label = f"seed={seed} hq={hq} hkv={hkv} d={d} {dtype} keys={nk} queries={n_rows}"
+    print(label, flush=True)
+    _, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, d ** -0.5, want_full=True)
+    qf, kf = q.float().numpy(), k.float().numpy()
+    # the oracle rounds logits to bf16 only: f16 is compared with unrounded logits
+    want = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], d ** -0.5,
+                                  dtype == torch.bfloat16)
+    np.testing.assert_allclose(full.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
+    assert abs(float(full.sum()) - n_rows * hq) < 1e-3 * n_rows * hq
