@@ -102,12 +102,13 @@ class CacheBlendConnectorV1(_Base, *(() if _HMA is object else (_HMA,))):
         self._recompute_on_failure = getattr(transfer, "kv_load_failure_policy", None) == "recompute"
         self.engine_id = str(transfer.engine_id)
         self.block_size = int(vllm_config.cache_config.block_size)
+        self.tp_size = int(vllm_config.parallel_config.tensor_parallel_size)
         if int(vllm_config.parallel_config.pipeline_parallel_size) != 1:
             raise ValueError("CacheBlendConnectorV1 currently requires pipeline_parallel_size=1")
-        self.model_scope = self.config.model_scope or str(
-            getattr(vllm_config.model_config, "model", "unknown-model")
-        )
+        self.model_scope = self.config.model_scope or self._make_model_scope(vllm_config)
         self._trace = PipelineTracer("scheduler" if role is KVConnectorRole.SCHEDULER else "worker")
+        self._trace.emit("connector_initialized", engine_id=self.engine_id,
+                         model_scope=self.model_scope, role=str(role), tp_size=self.tp_size)
         self._store: PinnedChunkStore | None = None
         self._writer: StoreStreamWriter | None = None
         self._slab: PinnedChunkSlab | None = None
@@ -116,6 +117,19 @@ class CacheBlendConnectorV1(_Base, *(() if _HMA is object else (_HMA,))):
         self._executor = None
         self._load_stream = None
         self._load_errors: set[int] = set()
+
+    @staticmethod
+    def _make_model_scope(vllm_config) -> str:
+        """The store's namespace when ``model_scope`` is not configured
+        (reference connector.py:158-166): model name, revision, dtype and
+        tensor-parallel size, so chunks of another revision, dtype or TP
+        split never match. Written ``<model>@<revision>|<dtype>|tp=<tp>``."""
+        model_config = vllm_config.model_config
+        name = getattr(model_config, "model", "unknown-model")
+        revision = getattr(model_config, "revision", "")
+        dtype = getattr(model_config, "dtype", "unknown")
+        tp = int(vllm_config.parallel_config.tensor_parallel_size)
+        return f"{name}@{revision}|{dtype}|tp={tp}"
 
     # ---------------------------------------------------------- worker
 

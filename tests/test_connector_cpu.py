@@ -4,6 +4,7 @@ layerwise executor in (reference connector.py:75-83, 868-882;
 registry.py:13-41)."""
 
 import gc
+import json
 from types import SimpleNamespace
 
 import pytest
@@ -40,6 +41,35 @@ def test_scheduler_methods_are_control_plane():
     # the scheduler role registers nothing
     conn.register_kv_caches({"model.layers.0.attn": torch.zeros(2, 1, 16, 1, 8)})
     conn.close()
+
+
+def test_model_scope_default_and_initialized_event(tmp_path, monkeypatch):
+    """Reference connector.py:130-144, 158-166: the default store scope is
+    ``<model>@<revision>|<dtype>|tp=<tp>`` and every connector announces
+    itself with a ``connector_initialized`` trace event."""
+    monkeypatch.setenv("CACHEBLEND_TRACE_DIR", str(tmp_path))
+    cfg = _config("eng")
+    cfg.model_config = SimpleNamespace(model="Qwen/Qwen3-8B", revision="main", dtype=torch.bfloat16)
+    cfg.parallel_config.tensor_parallel_size = 2
+    conn = CacheBlendConnectorV1(cfg, KVConnectorRole.WORKER)
+    assert conn.model_scope == "Qwen/Qwen3-8B@main|torch.bfloat16|tp=2"
+    assert conn.tp_size == 2
+    conn.close()
+    # a configured scope wins; missing model fields fall back as the reference's do
+    cfg2 = _config()
+    cfg2.kv_transfer_config.kv_connector_extra_config = {"model_scope": "fixed"}
+    assert CacheBlendConnectorV1(cfg2, KVConnectorRole.SCHEDULER).model_scope == "fixed"
+    cfg3 = _config()
+    cfg3.model_config = SimpleNamespace()
+    assert CacheBlendConnectorV1(cfg3, KVConnectorRole.SCHEDULER).model_scope == "unknown-model@|unknown|tp=1"
+    records = [json.loads(line) for f in sorted(tmp_path.iterdir()) for line in f.read_text().splitlines()]
+    init = [r for r in records if r["event"] == "connector_initialized"]
+    assert len(init) == 3
+    first = next(r for r in init if r["component"] == "worker")
+    assert first["engine_id"] == "eng" and first["tp_size"] == 2
+    assert first["model_scope"] == "Qwen/Qwen3-8B@main|torch.bfloat16|tp=2"
+    assert first["role"] == str(KVConnectorRole.WORKER)
+    assert {r["role"] for r in init} == {str(KVConnectorRole.WORKER), str(KVConnectorRole.SCHEDULER)}
 
 
 def test_pipeline_parallel_is_rejected():
