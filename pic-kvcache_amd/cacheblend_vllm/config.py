@@ -3,14 +3,36 @@
 Same field names, defaults and validation errors as the reference
 ``CacheBlendConfig`` (cacheblend_vllm/config.py:10-96), so an existing
 ``kv_connector_extra_config`` JSON loads unchanged; unknown fields are an
-error there and here. One field is added: ``load_staging_layers``, the depth
-of the loader's device ring of hit stagings.
+error there and here, so a config written for one loads in the other. The
+MI355X loader's one extra knob, the depth of its device ring of hit
+stagings, is read from the environment (``load_staging_layers``) instead of
+being a field.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass, fields
+import os
 from typing import Any
+
+# Layers of hit staging one request's DMA ring holds on the device (at least
+# 2, default 4). Not a config field: the reference's unknown-field rule
+# would reject a config that names it.
+LOAD_STAGING_LAYERS_ENV = "CACHEBLEND_LOAD_STAGING_LAYERS"
+
+
+def load_staging_layers() -> int:
+    """``CACHEBLEND_LOAD_STAGING_LAYERS`` (default 4, at least 2)."""
+    raw = os.environ.get(LOAD_STAGING_LAYERS_ENV, "").strip()
+    if not raw:
+        return 4
+    try:
+        value = int(raw)
+    except ValueError:
+        raise ValueError(f"{LOAD_STAGING_LAYERS_ENV} must be an integer, got {raw!r}") from None
+    if value < 2:
+        raise ValueError(f"{LOAD_STAGING_LAYERS_ENV} must be at least 2, got {value}")
+    return value
 
 
 @dataclass(frozen=True, slots=True)
@@ -38,9 +60,6 @@ class CacheBlendConfig:
     strict_version_check: bool = True
     ipc_root: str = "/tmp/cacheblend-v1"
     model_scope: str | None = None
-    # MI355X loader: layers of hit staging one request's DMA ring holds on
-    # the device (at least 2; not in the reference, which stages one layer)
-    load_staging_layers: int = 4
 
     @classmethod
     def from_extra_config(cls, values: dict[str, Any] | None) -> "CacheBlendConfig":
@@ -85,7 +104,6 @@ class CacheBlendConfig:
             (self.tail_query_tokens >= 0, "tail_query_tokens cannot be negative"),
             (self.selection_strategy == "kv_deviation" or self.tail_query_tokens > 0,
              "Sparse-Q selection requires tail_query_tokens > 0"),
-            (self.load_staging_layers >= 2, "load_staging_layers must be at least 2"),
         )
         for ok, message in checks:
             if not ok:

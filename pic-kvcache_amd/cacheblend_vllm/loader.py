@@ -36,7 +36,7 @@ import numpy as np
 import torch
 
 from . import _native
-from .config import CacheBlendConfig
+from .config import CacheBlendConfig, load_staging_layers
 from .kv_layout import kv_desc, kv_planes
 from .rope import cos_sin_table, rope_style
 from .streams import COPY, LOAD, side_stream
@@ -137,7 +137,8 @@ class PagedBlendLoader:
         DMA, "auto" reads in place only when the DMA commands would average
         fewer than ``dma_min_run_bytes`` each, where per-command DMA cost
         (about 9 us, the time of 0.5 MB) dominates.
-        ``dma_staging_layers`` (default ``config.load_staging_layers``, 4):
+        ``dma_staging_layers`` (default: ``CACHEBLEND_LOAD_STAGING_LAYERS``
+        from the environment, else 4):
         layers of hits the device ring the DMA fills holds (at least 2, at
         most the layer count). The host refills a slot only after the
         assembly that read it, so the copies run at most that many layers
@@ -188,7 +189,7 @@ class PagedBlendLoader:
         # fences a slot's reuse (_hit_free) when the ring wraps
         self._hit_ring: torch.Tensor | None = None
         self._hit_free: dict[int, torch.cuda.Event] = {}
-        layers = config.load_staging_layers if dma_staging_layers is None else int(dma_staging_layers)
+        layers = load_staging_layers() if dma_staging_layers is None else int(dma_staging_layers)
         if layers < 2:
             raise ValueError("dma_staging_layers must be at least 2")
         self._ring_layers = layers

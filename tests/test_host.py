@@ -121,6 +121,33 @@ def test_config_matches_reference_rules():
     assert cfg.ratio_for(5) == 0.3 and cfg.ratio_for(1) == 0.1 and cfg.ratio_for(None) == 0.1
 
 
+def test_config_fields_are_the_reference_fields_and_staging_depth_is_an_env_knob(monkeypatch):
+    """The field table is reference config.py:10-35 exactly, so a config that
+    names the loader's ring depth is rejected by both; the depth comes from
+    CACHEBLEND_LOAD_STAGING_LAYERS instead."""
+    from dataclasses import fields
+
+    from cacheblend_vllm.config import LOAD_STAGING_LAYERS_ENV, load_staging_layers
+
+    assert [f.name for f in fields(CacheBlendConfig)] == [
+        "chunk_size", "local_cpu_gb", "min_retrieve_tokens", "min_hit_ratio", "min_saved_tokens",
+        "max_apc_prefix_to_hit_ratio", "check_layers", "recompute_ratios", "selection_strategy",
+        "query_score_chunk_size", "overflow_blocks", "tail_query_tokens", "save_decode_cache",
+        "tp_global_selection", "event_pipeline", "fused_segment_copy", "cache_attention_mask",
+        "lookup_timeout_ms", "store_workers", "max_inflight_store_batches", "strict_version_check",
+        "ipc_root", "model_scope"]
+    with pytest.raises(ValueError, match="Unknown CacheBlend config fields"):
+        CacheBlendConfig.from_extra_config({"load_staging_layers": 3})
+    monkeypatch.delenv(LOAD_STAGING_LAYERS_ENV, raising=False)
+    assert load_staging_layers() == 4
+    monkeypatch.setenv(LOAD_STAGING_LAYERS_ENV, "7")
+    assert load_staging_layers() == 7
+    for bad in ("1", "x"):
+        monkeypatch.setenv(LOAD_STAGING_LAYERS_ENV, bad)
+        with pytest.raises(ValueError, match=LOAD_STAGING_LAYERS_ENV):
+            load_staging_layers()
+
+
 def test_plan_invariants_and_gap_runs():
     sid = lambda start, n: SegmentId("m", start, start, n)  # noqa: E731
     plan = BlendPlan(2, 20, 6, (BlendSegment(sid(0, 4), 4), BlendSegment(sid(8, 2), 12)))
