@@ -62,19 +62,17 @@ class TokenRangeMatcher:
 
     def make_record(self, model_scope: str, source_start: int,
                     tokens: Sequence[int]) -> FingerprintRecord:
-        """Reference matcher.py:34-51."""
-        if len(tokens) != self.chunk_size:
+        """A chunk's record, keyed as the store keys it (reference
+        matcher.py:34-51): the id is (scope, content hash of the tokens as
+        Python ints, start, length), and only whole ``chunk_size`` chunks
+        have one."""
+        chunk = tuple(map(int, tokens))
+        if len(chunk) != self.chunk_size:
             raise ValueError(
-                f"fingerprint requires exactly {self.chunk_size} tokens, got {len(tokens)}"
+                f"fingerprint requires exactly {self.chunk_size} tokens, got {len(chunk)}"
             )
-        token_tuple = tuple(int(token) for token in tokens)
-        segment_id = SegmentId(
-            model_scope=model_scope,
-            content_hash=content_hash(token_tuple),
-            source_start=source_start,
-            token_count=len(token_tuple),
-        )
-        return FingerprintRecord(segment_id=segment_id, tokens=token_tuple)
+        sid = SegmentId(model_scope, content_hash(chunk), source_start, self.chunk_size)
+        return FingerprintRecord(sid, chunk)
 
     def register(self, record: FingerprintRecord) -> None:
         """Reference matcher.py:53-63: re-registering an identical record is a
