@@ -30,7 +30,10 @@ Pinning (what checks each function, all in tests/test_oracle.py):
   215-253), brute-force window scan.
 * sparse_q_full_scores: reference closed-form test (tests/test_ascend.py:
   157-212), float64 dense softmax, column sums equal query count (softmax rows
-  sum to one).
+  sum to one); the bf16 and f16 logit rounding, placed before the scale, to
+  within float32 summation noise of torch's CPU kernels run in the order of
+  ascend.py:688-698 at scale 0.37 (rounding after the scale, or no rounding,
+  is far off).
 * kdev_scores: float64 closed form on integer-valued data where float32 is
   exact, zero on identical inputs.
 * relocate_key: reference known answer against fresh RoPE
@@ -322,18 +325,28 @@ def sparse_q_full_scores(
     scale: float,
     round_logits_bf16: bool,
     chunk: int = 8,
+    *,
+    logit_dtype: str | None = None,
+    round_after_scale: bool = False,
 ) -> np.ndarray:
     """Per-key causal attention mass summed over heads and queries.
 
     Follows cacheblend_vllm/ascend.py:683-698. ``query`` is ``[Q, Hq, D]``
     float32 (the selected sparse queries), ``key`` is ``[K, Hkv, D]`` float32.
     Query head ``h`` reads KV head ``h // (Hq // Hkv)`` (692). Logits are the
-    matmul output rounded to bf16 when the inputs are bf16 (694: a bf16
-    ``matmul`` then ``.float()``), then ``* scale`` in float32 (695), then keys
-    ``k > position_q`` are set to ``finfo(float32).min`` (696-697), then a
-    float32 softmax over all K keys, summed over (kv head, group, query)
-    (698). Returns ``full_scores[K]`` float32.
+    matmul output rounded to the input dtype (694: a bf16 or f16 ``matmul``
+    then ``.float()``; ``logit_dtype`` "bf16" or "f16", or
+    ``round_logits_bf16``; no rounding for float32 inputs), then ``* scale``
+    in float32 (695), then keys ``k > position_q`` are set to
+    ``finfo(float32).min`` (696-697), then a float32 softmax over all K keys,
+    summed over (kv head, group, query) (698). Returns ``full_scores[K]``
+    float32. ``round_after_scale`` swaps the rounding and the scale -- not
+    what the reference does; it exists so a test can show that the rounding
+    position is pinned.
     """
+    if logit_dtype is None and round_logits_bf16:
+        logit_dtype = "bf16"
+    rnd = {None: None, "bf16": round_bf16, "f16": round_f16}[logit_dtype]
     q = np.asarray(query, dtype=np.float32)
     k = np.asarray(key, dtype=np.float32)
     nq, hq, d = q.shape
@@ -354,9 +367,12 @@ def sparse_q_full_scores(
         end = min(start + chunk, nq)
         qc = q[start:end].reshape(end - start, hkv, groups, d).transpose(1, 2, 0, 3)
         logits = np.matmul(qc, kt[:, None]).astype(np.float32)  # [Hkv, G, c, K]
-        if round_logits_bf16:
-            logits = round_bf16(logits)
-        logits = logits * s32
+        if round_after_scale:
+            logits = logits * s32
+        if rnd is not None:
+            logits = rnd(logits)
+        if not round_after_scale:
+            logits = logits * s32
         mask = pos[start:end, None] < key_pos[None, :]
         logits = np.where(mask[None, None], fmin, logits).astype(np.float32)
         row_max = logits.max(axis=-1, keepdims=True)
@@ -378,6 +394,7 @@ def sparse_q_scores(
     tail_query_tokens: int,
     chunk: int = 8,
     round_logits_bf16: bool = False,
+    logit_dtype: str | None = None,
 ) -> tuple[np.ndarray, np.ndarray, dict]:
     """``(scores[N], forced[N], stats)`` of ``_sparse_q_scores``.
 
@@ -397,6 +414,7 @@ def sparse_q_scores(
         scale,
         round_logits_bf16,
         chunk,
+        logit_dtype=logit_dtype,
     )
     gap_count = int(gap.sum())
     stats = {

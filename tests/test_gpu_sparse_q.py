@@ -18,6 +18,8 @@ from cacheblend_vllm.config import CacheBlendConfig
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 RTOL = 1e-2
+# logits are rounded to the input dtype before the scale (ascend.py:694-695)
+LOGIT_DTYPE = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: None}
 
 
 def test_reference_closed_form_known_answer(golden):
@@ -96,13 +98,8 @@ def test_sparse_q_scores_vs_oracle(dtype, d, hq, hkv):
     got, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, scale,
                                        out_index=absolute, want_full=True)
     qf, kf = q.float().numpy(), k.float().numpy()
-    if dtype == torch.float16:
-        # oracle rounds logits to bf16 only: emulate f16 logit rounding by
-        # comparing against unrounded float32 logits within the tolerance
-        want_full = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], scale, False)
-    else:
-        want_full = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], scale,
-                                           dtype == torch.bfloat16)
+    want_full = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], scale, False,
+                                       logit_dtype=LOGIT_DTYPE[dtype])
     full = full.cpu().numpy()
     err = np.max(np.abs(full - want_full) / np.maximum(np.abs(want_full), 1e-30))
     print(f"max relative score error {err:.3e}", flush=True)
@@ -161,29 +158,55 @@ def test_sparse_q_tail_fallback_no_gaps():
     np.testing.assert_allclose(scores.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
 
 
-def test_sparse_q_full_layer6_properties():
-    """The layer-6 Sparse-Q shape (4096 gap queries over a 98,304-key causal
-    context, 32 query heads on 4 KV heads of 128 bf16): the column sums add up
-    to queries x heads (every softmax row sums to one), scores are finite and
-    non-negative, keys after the last query position get nothing, and the
-    launch is deterministic."""
-    from cacheblend_vllm import synthetic
+def test_sparse_q_full_layer6_vs_oracle_and_properties():
+    """The layer-6 Sparse-Q shape: 4096 gap queries over a 98,304-key causal
+    context, 32 query heads on 4 KV heads of 128 bf16.
 
+    * 96 of the gap queries (the last one, at position 98,303, among them)
+      against the oracle at the full context: all 98,304 column sums within
+      1e-2 relative;
+    * linearity at the full 4096 queries: the scores of all of them equal
+      the scores of those 96 plus the scores of the other 4000 (column sums
+      add over queries), so a key range or workspace offset that goes wrong
+      only at the full query count shows;
+    * the column sums add up to queries x heads (every softmax row sums to
+      one), scores are finite and non-negative, keys after the last query
+      get nothing, and the launch is deterministic."""
     nk, hq, hkv, d, nq = 98304, 32, 4, 128, 4096
+    scale = d ** -0.5
     g = torch.Generator(device=DEV).manual_seed(0)
     query = (torch.randn((nk, hq, d), generator=g, device=DEV) / d ** 0.5).to(torch.bfloat16)
     key = (torch.randn((nk, hkv, d), generator=g, device=DEV) / d ** 0.5).to(torch.bfloat16)
     gap = synthetic.sparse_q_layout(nk, nq, seed=0)
-    rows = torch.from_numpy(np.flatnonzero(gap)).to(DEV)
+    all_rows = np.flatnonzero(gap)
+    assert all_rows[-1] == nk - 1
+    rng = np.random.default_rng(6)
+    pick = np.sort(np.concatenate(([nq - 1], rng.choice(nq - 1, 95, replace=False))))
+    sub_rows, rest_rows = all_rows[pick], np.delete(all_rows, pick)
     absolute = torch.arange(nk, device=DEV)
-    _, full = S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, want_full=True)
-    full = full.cpu().numpy().astype(np.float64)
-    assert np.isfinite(full).all() and (full >= 0).all()
-    assert abs(full.sum() - nq * hq) < 1e-3 * nq * hq
-    last = int(rows.max())
-    assert (full[last + 1:] == 0).all()
-    _, again = S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, want_full=True)
-    assert np.array_equal(again.cpu().numpy().astype(np.float64), full)
+
+    def scores(rows):
+        _, full = S.sparse_q_full_scores(query, key, torch.from_numpy(rows).to(DEV), absolute, scale,
+                                         want_full=True)
+        return full.cpu().numpy()
+
+    full = scores(all_rows)
+    sub = scores(sub_rows)
+    rest = scores(rest_rows)
+    print(f"full-context oracle check: {sub_rows.size} queries at {sub_rows.min()}..{sub_rows.max()}",
+          flush=True)
+    want = O.sparse_q_full_scores(query[torch.from_numpy(sub_rows).to(DEV)].float().cpu().numpy(),
+                                  key.float().cpu().numpy(), sub_rows, scale, True)
+    err = np.max(np.abs(sub - want) / np.maximum(want, 1e-30))
+    print(f"max relative score error over {nk} keys: {err:.3e}", flush=True)
+    np.testing.assert_allclose(sub, want, rtol=RTOL, atol=1e-6)
+    # linearity over the query set at the full size
+    np.testing.assert_allclose(full, sub + rest, rtol=1e-4, atol=1e-6)
+    full64 = full.astype(np.float64)
+    assert np.isfinite(full64).all() and (full64 >= 0).all()
+    assert abs(full64.sum() - nq * hq) < 1e-3 * nq * hq
+    assert (full[all_rows.max() + 1:] == 0).all()
+    assert np.array_equal(scores(all_rows), full)
 
 
 @pytest.mark.parametrize("hq", [8, 16])
@@ -268,8 +291,7 @@ def test_sparse_q_random_shapes(seed):
     print(label, flush=True)
     _, full = S.sparse_q_full_scores(q.to(DEV), k.to(DEV), rows, absolute, d ** -0.5, want_full=True)
     qf, kf = q.float().numpy(), k.float().numpy()
-    # the oracle rounds logits to bf16 only: f16 is compared with unrounded logits
-    want = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], d ** -0.5,
-                                  dtype == torch.bfloat16)
+    want = O.sparse_q_full_scores(qf[rows.numpy()], kf, absolute.numpy()[rows.numpy()], d ** -0.5, False,
+                                  logit_dtype=LOGIT_DTYPE[dtype])
     np.testing.assert_allclose(full.cpu().numpy(), want, rtol=RTOL, atol=1e-6)
     assert abs(float(full.sum()) - n_rows * hq) < 1e-3 * n_rows * hq

@@ -11,6 +11,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 import oracle as O
 
@@ -274,6 +275,50 @@ def test_sparse_q_bf16_logit_rounding_is_applied():
     np.testing.assert_allclose(rounded, [0.5, 0.5], rtol=1e-6)
     exact = O.sparse_q_full_scores(q, k, pos, 1.0, round_logits_bf16=False)
     assert exact[0] > 0.5
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_sparse_q_logit_rounding_order_matches_torch_cpu_chain(dtype):
+    """ascend.py:688-698 run on torch's CPU kernels -- a 16-bit ``matmul``,
+    ``.float()``, ``mul_(scale)``, the causal ``masked_fill_``, ``softmax``,
+    the sum -- at scale 0.37 against the oracle: the rounding to the input
+    dtype sits before the scale. Rounding after the scale, or not rounding,
+    moves most columns by far more than the float32 summation noise the
+    oracle shows."""
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    g = torch.Generator().manual_seed(3)
+    nq, hq, hkv, d, nk, scale = 24, 8, 2, 64, 300, 0.37
+    q = (torch.randn(nq, hq, d, generator=g) * 0.6).to(tdt)
+    k = (torch.randn(nk, hkv, d, generator=g) * 0.6).to(tdt)
+    pos = torch.sort(torch.randperm(nk, generator=g)[:nq]).values
+    groups = hq // hkv
+    kt = k.permute(1, 2, 0).contiguous()
+    full = torch.zeros(nk)
+    key_pos = torch.arange(nk)
+    for start in range(0, nq, 8):
+        end = min(start + 8, nq)
+        qc = q[start:end].view(end - start, hkv, groups, d).permute(1, 2, 0, 3).contiguous()
+        logits = torch.matmul(qc, kt[:, None]).float()
+        logits.mul_(scale)
+        logits.masked_fill_((pos[start:end, None] < key_pos[None, :])[None, None],
+                            torch.finfo(logits.dtype).min)
+        full.add_(torch.softmax(logits, dim=-1).sum(dim=(0, 1, 2)))
+    want = full.numpy()
+    live = int(pos.max()) + 1  # keys past the last query carry no mass
+    assert np.all(want[live:] == 0) and np.all(want[:live] > 0)
+    qf, kf = q.float().numpy(), k.float().numpy()
+
+    def rel(got):
+        assert np.all(got[live:] == 0)
+        return np.abs(got[:live] - want[:live]) / want[:live]
+
+    oracle = O.sparse_q_full_scores(qf, kf, pos.numpy(), scale, False, logit_dtype=dtype)
+    assert rel(oracle).max() < 2e-6
+    after = O.sparse_q_full_scores(qf, kf, pos.numpy(), scale, False, logit_dtype=dtype,
+                                   round_after_scale=True)
+    unrounded = O.sparse_q_full_scores(qf, kf, pos.numpy(), scale, False)
+    for wrong in (after, unrounded):
+        assert (rel(wrong) > 1e-5).mean() > 0.5
 
 
 def test_kdev_scores_closed_form():
