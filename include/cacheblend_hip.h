@@ -229,15 +229,43 @@ size_t cbk_select_workspace_bytes(int64_t n);
  * Replaces Qwen3BlendExecutor._select (cacheblend_vllm/ascend.py:757-796) at
  * TP1, composed with the overflow dilation of _sparse_q_scores
  * (ascend.py:662-671) when radius > 0. Masks are uint8 (0/1).
+ *
+ * A count of -1 means the one-launch select gave up and wrote no index: it
+ * runs every 2048-token tile in its own workgroup with grid barriers between
+ * phases, launched only when the occupancy query says all the workgroups fit
+ * on the device at once; workgroups of kernels on other streams can still
+ * hold the CUs, and a barrier that waits about 2^22 polls for the missing
+ * workgroups marks the launch failed (every workgroup then writes -1 and
+ * exits). The count is device memory, so only a caller that reads it can
+ * react: run cbk_select_ex with CBK_SELECT_MULTI_LAUNCH on the same scores
+ * (the Python select() and kdev_select() do this). Callers that cannot read
+ * it in between (graph capture) pass CBK_SELECT_MULTI_LAUNCH up front.
  */
 int cbk_select(const float* scores_dev, const uint8_t* gap_dev, const uint8_t* forced_dev,
                int64_t n, int64_t radius, double ratio, int64_t* out_idx_dev,
                int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                cbk_stream_t stream);
 
+/* cbk_select_ex / cbk_kdev_select_ex flags. */
+/* The five-launch select (one launch per radix phase, no grid barrier, no
+ * co-residency assumption; about 25 us slower at 64K tokens): never -1. */
+#define CBK_SELECT_MULTI_LAUNCH 1u
+/* Tests only: the one-launch select's first barrier expects one arrival more
+ * than the grid makes and polls 0 times, so every workgroup gives up at once
+ * and exits normally; the count is -1. */
+#define CBK_SELECT_TEST_GIVE_UP 2u
+
+/* cbk_select with CBK_SELECT_* flags (cbk_select is flags 0). */
+int cbk_select_ex(const float* scores_dev, const uint8_t* gap_dev, const uint8_t* forced_dev,
+                  int64_t n, int64_t radius, double ratio, int64_t* out_idx_dev,
+                  int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+                  uint32_t flags, cbk_stream_t stream);
+
 /*
  * K-deviation selection in one call: cbk_kdev_scores (scores_dev receives
- * the scores) followed by cbk_select on them, with no host round trip.
+ * the scores) followed by cbk_select on them, with no host round trip. The
+ * count follows cbk_select's contract (-1: run cbk_select_ex with
+ * CBK_SELECT_MULTI_LAUNCH on scores_dev).
  */
 int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
                     int64_t cached_row_stride_elems, int64_t cached_num_rows,
@@ -247,6 +275,15 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                     double ratio, float* scores_dev, int64_t* out_idx_dev,
                     int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                     cbk_stream_t stream);
+
+/* cbk_kdev_select with CBK_SELECT_* flags (cbk_kdev_select is flags 0). */
+int cbk_kdev_select_ex(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
+                       int64_t cached_row_stride_elems, int64_t cached_num_rows,
+                       const int64_t* cached_rows_dev, int64_t cached_row0, int64_t n, int64_t width,
+                       int32_t dtype, const uint8_t* gap_dev, const uint8_t* forced_dev,
+                       int64_t radius, double ratio, float* scores_dev, int64_t* out_idx_dev,
+                       int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+                       uint32_t flags, cbk_stream_t stream);
 
 /* Largest n cbk_kdev_select_noalloc accepts. */
 #define CBK_NOALLOC_SELECT_MAX_TOKENS 1048576
@@ -259,7 +296,11 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
  * (5.11 MiB per GPU, held until the process ends); larger n is rejected
  * with CBK_ERR_INVALID. The caller passes every input and output. Calls
  * that overlap on one GPU (concurrent streams) race on the shared array;
- * calls in sequence do not (each clears the counters it needs).
+ * calls in sequence do not (each clears the counters it needs). The count
+ * follows cbk_select's contract: -1 (the one-launch select could not hold
+ * the device) wrote no index; scores_dev is complete, so a caller that can
+ * allocate selects again with cbk_select_ex(CBK_SELECT_MULTI_LAUNCH), and
+ * one that cannot repeats the call once the device is less busy.
  */
 int cbk_kdev_select_noalloc(const void* fresh_dev, int64_t fresh_row_stride_elems,
                             const void* cached_dev, int64_t cached_row_stride_elems,

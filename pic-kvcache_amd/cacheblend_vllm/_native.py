@@ -25,6 +25,8 @@ CBK_ERR_WORKSPACE = -4
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 MAX_DILATION_RADIUS = 4096
+SELECT_MULTI_LAUNCH = 1  # CBK_SELECT_MULTI_LAUNCH
+SELECT_TEST_GIVE_UP = 2  # CBK_SELECT_TEST_GIVE_UP
 
 c_i64 = ctypes.c_int64
 c_i32 = ctypes.c_int32
@@ -81,6 +83,19 @@ _SIGNATURES = {
         [
             c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32,
             c_vp, c_vp, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp,
+        ],
+    ),
+    "cbk_select_ex": (
+        ctypes.c_int,
+        [c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, ctypes.c_size_t,
+         ctypes.c_uint32, c_vp],
+    ),
+    "cbk_kdev_select_ex": (
+        ctypes.c_int,
+        [
+            c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_i32,
+            c_vp, c_vp, c_i64, ctypes.c_double, c_vp, c_vp, c_vp, c_vp, ctypes.c_size_t,
+            ctypes.c_uint32, c_vp,
         ],
     ),
     "cbk_kdev_select_noalloc": (

@@ -88,9 +88,17 @@ def select_async(
     ratio: float,
     forced_mask: torch.Tensor | None = None,
     radius: int = 0,
+    flags: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Selection without a host sync: ``(indices[N] int64, count[1] int64)``;
-    the first ``count`` entries of ``indices`` are the sorted selection."""
+    the first ``count`` entries of ``indices`` are the sorted selection.
+
+    The count is -1 when the one-launch select could not hold the device (its
+    workgroups must all be resident at once; kernels on other streams can
+    keep CUs busy past its bounded wait) and wrote no index. ``select`` reads
+    the count and then runs the multi-launch select; a caller of this
+    function that cannot read it in between -- under graph capture, say --
+    passes ``flags=_native.SELECT_MULTI_LAUNCH``, which never returns -1."""
     n = int(scores.shape[0])
     _native.require_device(scores, "scores")
     if scores.ndim != 1:
@@ -104,16 +112,19 @@ def select_async(
     forced = None if forced_mask is None else _mask_u8(forced_mask.to(scores.device), n, "forced_mask")
     out = torch.empty(max(n, 1), dtype=torch.long, device=scores.device)
     count = torch.empty(1, dtype=torch.long, device=scores.device)
+    _launch_select(scores, gap, forced, n, radius, ratio, out, count, flags)
+    return out, count
+
+
+def _launch_select(scores, gap, forced, n, radius, ratio, out, count, flags):
     lib = _native.load()
-    nbytes = lib.cbk_select_workspace_bytes(n)
-    ws = _native.workspace(scores.device, nbytes)
-    rc = lib.cbk_select(
+    ws = _native.workspace(scores.device, lib.cbk_select_workspace_bytes(n))
+    rc = lib.cbk_select_ex(
         scores.data_ptr(), gap.data_ptr(), _native.ptr(forced), n, int(radius), float(ratio),
-        out.data_ptr(), count.data_ptr(), ws.data_ptr(), ws.numel(),
+        out.data_ptr(), count.data_ptr(), ws.data_ptr(), ws.numel(), int(flags),
         _native.stream_handle(scores.device),
     )
     _native.check(rc, "select")
-    return out, count
 
 
 def select(
@@ -122,22 +133,30 @@ def select(
     ratio: float,
     forced_mask: torch.Tensor | None = None,
     radius: int = 0,
+    flags: int = 0,
 ) -> torch.Tensor:
     """Sorted int64 indices of ``gap | forced | dilate(gap, radius) | top-k``.
 
     Reference ``_select`` (ascend.py:757-796) at TP1, with the budget
-    ``int((N - #gap) * ratio)`` clamped to ``[1, available]``.
+    ``int((N - #gap) * ratio)`` clamped to ``[1, available]``. A one-launch
+    select that gave up (count -1) is run again as the multi-launch select.
     """
-    out, count = select_async(scores, gap_mask, ratio, forced_mask, radius)
-    return out[: _selected_count(count)]
-
-
-def _selected_count(count: torch.Tensor) -> int:
-    """The device count a selection wrote; negative means its one-launch
-    kernel's blocks could not all be resident (it gave up, nothing valid)."""
+    out, count = select_async(scores, gap_mask, ratio, forced_mask, radius, flags)
     value = int(count.item())
     if value < 0:
-        raise RuntimeError("selection failed: its grid barrier timed out (blocks not co-resident)")
+        n = int(scores.shape[0])
+        dev = scores.device
+        forced = None if forced_mask is None else _mask_u8(forced_mask.to(dev), n, "forced_mask")
+        _launch_select(scores.float().contiguous(), _mask_u8(gap_mask.to(dev), n, "gap_mask"), forced,
+                       n, radius, ratio, out, count, _native.SELECT_MULTI_LAUNCH)
+        value = _checked_count(count)
+    return out[:value]
+
+
+def _checked_count(count: torch.Tensor) -> int:
+    value = int(count.item())
+    if value < 0:  # the multi-launch select never writes -1
+        raise RuntimeError(f"selection wrote a count of {value}")
     return value
 
 
@@ -149,11 +168,13 @@ def kdev_select(
     ratio: float,
     radius: int = 0,
     row0: int = 0,
+    flags: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """K-deviation scores and their selection in one call (``cbk_kdev_select``).
 
     Returns ``(selected, scores)``; ``radius`` > 0 also forces every token
-    within ``radius`` of a gap (overflow blocks).
+    within ``radius`` of a gap (overflow blocks). A one-launch select that
+    gave up (count -1) is run again on the scores as the multi-launch select.
     """
     fresh = _row_view(fresh, "fresh K")
     cached = _row_view(cached, "cached K")
@@ -173,14 +194,18 @@ def kdev_select(
     lib = _native.load()
     nbytes = lib.cbk_select_workspace_bytes(n)
     ws = _native.workspace(fresh.device, nbytes)
-    rc = lib.cbk_kdev_select(
+    rc = lib.cbk_kdev_select_ex(
         fresh.data_ptr(), fresh.stride(0), cached.data_ptr(), cached.stride(0), cached.shape[0],
         _native.ptr(idx), row0, n, fresh.shape[1], _native.DTYPE_CODES[fresh.dtype],
         gap.data_ptr(), None, int(radius), float(ratio), scores.data_ptr(), out.data_ptr(),
-        count.data_ptr(), ws.data_ptr(), ws.numel(), _native.stream_handle(fresh.device),
+        count.data_ptr(), ws.data_ptr(), ws.numel(), int(flags), _native.stream_handle(fresh.device),
     )
     _native.check(rc, "kdev_select")
-    return out[: _selected_count(count)], scores
+    value = int(count.item())
+    if value < 0:
+        _launch_select(scores, gap, None, n, radius, ratio, out, count, _native.SELECT_MULTI_LAUNCH)
+        value = _checked_count(count)
+    return out[:value], scores
 
 
 def dilate(gap_mask: torch.Tensor, radius: int) -> torch.Tensor:
@@ -357,7 +382,12 @@ class BlendSelector:
         here (the kernel streams K through registers and LDS).
         """
         radius = self.config.overflow_blocks * self.block_size
-        gap_count = int(gap_mask.sum().item())  # the one host read before the scores
+        if gap_mask.dtype != torch.bool:
+            gap_mask = gap_mask != 0
+        # the one host read before the scores; count_nonzero, as the masks
+        # treat any nonzero entry as set (a sum would overcount 2s and size
+        # the query compaction past the set rows)
+        gap_count = int(gap_mask.count_nonzero().item())
         tail = self.config.tail_query_tokens
         query_mask, forced, has_gap = sparse_q_masks(gap_mask, tail, radius, gap_count=gap_count)
         sparse = sparse_q_query_rows(query_mask, has_gap, gap_count, tail)
@@ -431,6 +461,12 @@ class BlendSelector:
             result.sparse_q_selected, result.sparse_q_stats = self.sparse_q_select(
                 q.reshape(-1, num_heads, head_size), score_keys.view(-1, num_kv_heads, head_size),
                 absolute_indices, active_gap_mask, scale, layer_id)
+        if strategy == "sparse_q" and tracer is not None and tracer.enabled:
+            # reference ascend.py:627-635 emits this once the Sparse-Q set is
+            # applied to the check layer's output; the set is final here
+            tracer.emit("selection_finished", request_id=request_id, layer_id=layer_id,
+                        strategy="sparse_q", selected_tokens=result.sparse_q_selected.numel(),
+                        **result.sparse_q_stats)
         if strategy == "compare" and tracer is not None and tracer.enabled:
             dev, sq = result.deviation_selected, result.sparse_q_selected
             size = max(int(dev.max()) if dev.numel() else -1, int(sq.max()) if sq.numel() else -1) + 1

@@ -168,8 +168,9 @@ constexpr uint32_t kHeader = 8512; // words cleared by the zero kernel
 enum : uint32_t {
   C_GAP = 0, C_BASE, C_T_PREP, C_T_P2, C_T_P3, C_T_TIES, C_T_COUNT,
   C_TOPK, C_PREFIX1, C_KREM1, C_PREFIX2, C_KREM2, C_THRESH, C_NEED, C_TOTAL,
-  // one-launch select: grid barrier arrivals / generation, candidates, error
-  C_BAR = 16, C_GEN, C_CANDS, C_ERR
+  // one-launch select: grid barrier arrivals (bit 31: the barrier failed),
+  // candidates
+  C_BAR = 16, C_GEN, C_CANDS
 };
 // candidates the one-launch select finishes in LDS (keys sharing the k-th
 // key's 12- or 24-bit prefix)
@@ -224,6 +225,11 @@ struct SelArgs {
   uint32_t* cand_key;
   uint32_t* cand_idx;
   uint32_t vec_ok;  // scores 16-byte and masks 8-byte aligned
+  // grid barrier of the one-launch select: polls before giving up, and
+  // arrivals expected beyond the grid's own (0; a test sets 1 with a spin
+  // limit of 0 so every block gives up at once and exits normally)
+  uint32_t spin_limit;
+  uint32_t bar_extra;
 };
 
 __device__ __forceinline__ uint32_t order_key(float s) {
@@ -573,32 +579,45 @@ __global__ __launch_bounds__(kSelThreads) void sel_write_kernel(const SelArgs a)
 // ---------------------------------------------------------------------
 
 constexpr uint32_t kBarrierSpins = 1u << 22;
+constexpr uint32_t kBarrierFailed = 0x80000000u;
 
 // Grid-wide barrier over `nblocks` co-resident blocks. C_BAR counts every
-// block's arrivals over the launch (zeroed before it): barrier number
-// `round` (1, 2, ...) is passed once it reaches round * nblocks. Arrival is
-// a posted atomic, so a block waits one round trip for the last arrival.
-// Returns false when the select failed: a barrier that waited longer than
-// kBarrierSpins polls (blocks not co-resident), flagged in C_ERR so every
-// block stops.
-__device__ bool grid_barrier(uint32_t* ctrl, uint32_t nblocks, uint32_t round, uint32_t* lds_flag) {
+// block's arrivals over the launch (zeroed before it) in bits 0-30: barrier
+// number `round` (1, 2, ...) is passed once the count reaches round *
+// nblocks (+ bar_extra). Arrival is a posted atomic, so a block waits one
+// round trip for the last arrival. A block that has polled spin_limit times
+// without seeing the count complete marks the barrier failed (bit 31), by a
+// compare-and-swap that succeeds only while the count is short. All blocks
+// therefore agree: a block passes only on a count that reached the target
+// with bit 31 clear, after which the mark can no longer be set; a block
+// fails only on seeing the mark, after which the count can no longer pass
+// (every later arrival and poll sees bit 31). Returns false on failure:
+// the blocks were not all resident (or a test forced it), every block then
+// writes a count of -1 and exits.
+__device__ bool grid_barrier(uint32_t* ctrl, uint32_t nblocks, uint32_t round, const SelArgs& a,
+                             uint32_t* lds_flag) {
   __syncthreads();
   if (threadIdx.x == 0) {
     __threadfence();  // this block's global writes before its arrival
-    __hip_atomic_fetch_add(ctrl + C_BAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t target = round * nblocks;
-    uint32_t ok = 1, spins = 0;
-    while (__hip_atomic_load(ctrl + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++spins > kBarrierSpins ||
-          __hip_atomic_load(ctrl + C_ERR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-        atomicOr(ctrl + C_ERR, 1u);
-        ok = 0;
+    const uint32_t target = round * nblocks + a.bar_extra;
+    uint32_t v = __hip_atomic_fetch_add(ctrl + C_BAR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    uint32_t spins = 0;
+    while (!(v & kBarrierFailed) && v < target) {
+      if (spins++ >= a.spin_limit) {
+        // give up: mark the barrier failed unless the count completes first
+        while (!(v & kBarrierFailed) && v < target) {
+          if (__hip_atomic_compare_exchange_strong(ctrl + C_BAR, &v, v | kBarrierFailed, __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            v |= kBarrierFailed;
+          }
+        }
         break;
       }
       __builtin_amdgcn_s_sleep(1);
+      v = __hip_atomic_load(ctrl + C_BAR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __threadfence();  // the other blocks' writes after the barrier
-    *lds_flag = ok;
+    *lds_flag = (v & kBarrierFailed) ? 0u : 1u;
   }
   __syncthreads();
   return *lds_flag != 0;
@@ -915,7 +934,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
     const uint32_t c = hist[i] + (i == (kKeyNegInf >> 20) ? counts[1] : 0u);
     if (c) atomicAdd(&a.ws[kH1 + i], c);
   }
-  if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+  if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
     if (threadIdx.x == 0) *a.out_count = -1;
     return;
   }
@@ -962,7 +981,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       __syncthreads();
       for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads)
         if (hist[i]) atomicAdd(&a.ws[kH2 + i], hist[i]);
-      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
@@ -984,7 +1003,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         __syncthreads();
         for (uint32_t i = threadIdx.x; i < 256; i += kSelThreads)
           if (hist[i]) atomicAdd(&a.ws[kH3 + i], hist[i]);
-        if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+        if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
           if (threadIdx.x == 0) *a.out_count = -1;
           return;
         }
@@ -1035,7 +1054,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
           ++pos;
         }
       }
-      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
@@ -1162,7 +1181,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       uint32_t rank = block_exclusive_scan<kSelThreads>(ties, scan, &tile_ties);
       block_exclusive_scan<kSelThreads>(sure, scan, &tile_sure);
       if (threadIdx.x == 0) a.tile_ties[tile] = tile_ties;
-      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
@@ -1189,7 +1208,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       uint32_t tile_count;
       block_exclusive_scan<kSelThreads>(count, scan, &tile_count);
       if (threadIdx.x == 0) a.tile_cnt[tile] = tile_count;
-      if (!grid_barrier(ctrl, ntiles, ++bar_round, &flag)) {
+      if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
@@ -1218,7 +1237,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
 __global__ void write_zero_count_kernel(int64_t* out_count) { *out_count = 0; }
 
 int check_select(const float* scores, const uint8_t* gap, int64_t n, int64_t radius, double ratio,
-                 int64_t* out_idx, int64_t* out_count, void* ws, size_t ws_bytes) {
+                 int64_t* out_idx, int64_t* out_count, void* ws, size_t ws_bytes, uint32_t flags) {
+  CBK_REQUIRE((flags & ~uint32_t(CBK_SELECT_MULTI_LAUNCH | CBK_SELECT_TEST_GIVE_UP)) == 0,
+              "unknown select flags 0x%x", unsigned(flags));
+  CBK_REQUIRE((flags & CBK_SELECT_MULTI_LAUNCH) == 0 || (flags & CBK_SELECT_TEST_GIVE_UP) == 0,
+              "CBK_SELECT_TEST_GIVE_UP needs the one-launch select");
   CBK_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "n out of range");
   CBK_REQUIRE(out_count != nullptr, "out_count is NULL");
   CBK_REQUIRE(radius >= 0 && radius <= CBK_MAX_DILATION_RADIUS,
@@ -1286,11 +1309,12 @@ int launch_onepass(const SelArgs& a, int64_t n, int64_t radius, hipStream_t stre
 }
 
 // header_zeroed: an earlier launch on the stream cleared the kHeader counter
-// words (the fused K-deviation launch does)
+// words (the fused K-deviation launch does). flags: CBK_SELECT_* bits.
 int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced, int64_t n,
                   int64_t radius, double ratio, int64_t* out_idx, int64_t* out_count, void* ws,
-                  size_t ws_bytes, hipStream_t stream, bool header_zeroed = false) {
-  if (int rc = check_select(scores, gap, n, radius, ratio, out_idx, out_count, ws, ws_bytes)) return rc;
+                  size_t ws_bytes, hipStream_t stream, bool header_zeroed, uint32_t flags) {
+  if (int rc = check_select(scores, gap, n, radius, ratio, out_idx, out_count, ws, ws_bytes, flags))
+    return rc;
   if (n == 0) {
     hipLaunchKernelGGL(write_zero_count_kernel, dim3(1), dim3(1), 0, stream, out_count);
     return launch_status("select (empty)");
@@ -1319,11 +1343,16 @@ int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced
   a.cand_idx = a.cand_key + kCandCap;
   a.vec_ok = (reinterpret_cast<uintptr_t>(scores) % 16 == 0 && reinterpret_cast<uintptr_t>(gap) % 8 == 0 &&
               reinterpret_cast<uintptr_t>(forced) % 8 == 0) ? 1u : 0u;
+  const bool give_up = (flags & CBK_SELECT_TEST_GIVE_UP) != 0;
+  a.spin_limit = give_up ? 0u : kBarrierSpins;
+  a.bar_extra = give_up ? 1u : 0u;
   if (!header_zeroed) hipLaunchKernelGGL(sel_zero_kernel, dim3(1), dim3(kSelThreads), 0, stream, a.ws);
-  // one cooperative launch when every tile's block can be resident at once
-  int rc = launch_onepass<8>(a, n, radius, stream);
-  if (rc == kNotLaunched) rc = launch_onepass<32>(a, n, radius, stream);
-  if (rc != kNotLaunched) return rc;
+  // one launch when every tile's block can be resident at once
+  if ((flags & CBK_SELECT_MULTI_LAUNCH) == 0) {
+    int rc = launch_onepass<8>(a, n, radius, stream);
+    if (rc == kNotLaunched) rc = launch_onepass<32>(a, n, radius, stream);
+    if (rc != kNotLaunched) return rc;
+  }
   const dim3 grid(L.nblocks), block(kSelThreads);
   const size_t prep_lds = (4096 + 16 + kSelTile + 2 * size_t(radius) + 1) * sizeof(uint32_t);
   hipLaunchKernelGGL(sel_prepare_kernel, grid, block, prep_lds, stream, a);
@@ -1439,14 +1468,22 @@ size_t cbk_select_workspace_bytes(int64_t n) {
   return size_t(cbk::sel_layout(n).bytes);
 }
 
+int cbk_select_ex(const float* scores_dev, const uint8_t* gap_dev, const uint8_t* forced_dev,
+                  int64_t n, int64_t radius, double ratio, int64_t* out_idx_dev,
+                  int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+                  uint32_t flags, cbk_stream_t stream) {
+  cbk::clear_error();
+  return cbk::launch_select(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
+                            out_count_dev, workspace_dev, workspace_bytes,
+                            static_cast<hipStream_t>(stream), false, flags);
+}
+
 int cbk_select(const float* scores_dev, const uint8_t* gap_dev, const uint8_t* forced_dev,
                int64_t n, int64_t radius, double ratio, int64_t* out_idx_dev,
                int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                cbk_stream_t stream) {
-  cbk::clear_error();
-  return cbk::launch_select(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
-                            out_count_dev, workspace_dev, workspace_bytes,
-                            static_cast<hipStream_t>(stream));
+  return cbk_select_ex(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
+                       out_count_dev, workspace_dev, workspace_bytes, 0u, stream);
 }
 
 int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
@@ -1456,10 +1493,23 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                     int64_t radius, double ratio, float* scores_dev, int64_t* out_idx_dev,
                     int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
                     cbk_stream_t stream) {
+  return cbk_kdev_select_ex(fresh_dev, fresh_row_stride_elems, cached_dev, cached_row_stride_elems,
+                            cached_num_rows, cached_rows_dev, cached_row0, n, width, dtype, gap_dev,
+                            forced_dev, radius, ratio, scores_dev, out_idx_dev, out_count_dev,
+                            workspace_dev, workspace_bytes, 0u, stream);
+}
+
+int cbk_kdev_select_ex(const void* fresh_dev, int64_t fresh_row_stride_elems, const void* cached_dev,
+                       int64_t cached_row_stride_elems, int64_t cached_num_rows,
+                       const int64_t* cached_rows_dev, int64_t cached_row0, int64_t n, int64_t width,
+                       int32_t dtype, const uint8_t* gap_dev, const uint8_t* forced_dev,
+                       int64_t radius, double ratio, float* scores_dev, int64_t* out_idx_dev,
+                       int64_t* out_count_dev, void* workspace_dev, size_t workspace_bytes,
+                       uint32_t flags, cbk_stream_t stream) {
   cbk::clear_error();
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = cbk::check_select(scores_dev, gap_dev, n, radius, ratio, out_idx_dev, out_count_dev,
-                                 workspace_dev, workspace_bytes))
+                                 workspace_dev, workspace_bytes, flags))
     return rc;
   const bool zero = n > 0;  // the score launch clears the selection counters
   if (int rc = cbk::launch_kdev(fresh_dev, fresh_row_stride_elems, cached_dev,
@@ -1469,7 +1519,7 @@ int cbk_kdev_select(const void* fresh_dev, int64_t fresh_row_stride_elems, const
                                 zero ? cbk::kHeader : 0u))
     return rc;
   return cbk::launch_select(scores_dev, gap_dev, forced_dev, n, radius, ratio, out_idx_dev,
-                            out_count_dev, workspace_dev, workspace_bytes, s, zero);
+                            out_count_dev, workspace_dev, workspace_bytes, s, zero, flags);
 }
 
 int cbk_kdev_select_noalloc(const void* fresh_dev, int64_t fresh_row_stride_elems,

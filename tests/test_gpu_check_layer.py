@@ -1,6 +1,8 @@
 """GPU parity: row write-back (block-size-1, K-only descriptors) and the check
 layer's selection block in its three strategies, against the oracle."""
 
+import json
+
 import numpy as np
 import pytest
 import torch
@@ -108,8 +110,18 @@ def test_check_layer_sparse_q_overwrites_and_selects(strategy, tmp_path, monkeyp
         dev_want = O.select(O.kdev_scores(k.float().numpy(), old.float().numpy()[absolute.numpy()]),
                             gap.numpy(), 0.15)
         np.testing.assert_array_equal(res.deviation_selected.cpu().numpy(), dev_want)
-        events = [line for f in tmp_path.iterdir() for line in f.read_text().splitlines()]
-        assert any('"selection_compared"' in e for e in events)
+    events = [json.loads(line) for f in tmp_path.iterdir() for line in f.read_text().splitlines()]
+    names = [e["event"] for e in events]
+    if strategy == "compare":
+        assert "selection_compared" in names and "selection_finished" not in names
+    else:
+        # reference ascend.py:627-635: the Sparse-Q set and its stats
+        (done,) = [e for e in events if e["event"] == "selection_finished"]
+        assert done["request_id"] == "r" and done["layer_id"] == 1 and done["strategy"] == "sparse_q"
+        assert done["selected_tokens"] == len(got)
+        for key in ("active_tokens", "gap_tokens", "cached_tokens", "sparse_query_tokens",
+                    "tail_fallback", "overflow_blocks"):
+            assert done[key] == res.sparse_q_stats[key], key
 
 
 def test_k_only_gather_through_row_table():

@@ -110,7 +110,7 @@ def test_connector_drop_in_save_then_blend_load(monkeypatch, tmp_path):
 
     # a new prompt reuses chunks 3 and 1 at other offsets behind a 32-token APC prefix
     new_prompt = list(range(50, 82)) + prompt[192:256] + list(range(7, 47)) + prompt[64:128] + [5] * 20
-    segments = conn._store.match("test-model", new_prompt, 32)
+    segments = conn._store.match(conn.model_scope, new_prompt, 32)
     assert [(s.source_start, s.target_start) for s in segments] == [(192, 32), (64, 136)]
     assert conn._store.pin("b", segments) == segments   # what the lookup server does
     plan = BlendPlan(32, len(new_prompt), 128, segments)
@@ -188,7 +188,7 @@ def test_evicted_chunks_wait_for_in_flight_loads():
     loaded_ptrs = {t.data_ptr() for sid in loaded for t in conn._store._entries[sid].layers.values()}
     assert conn._store.current_bytes == conn._store.max_bytes
 
-    segments = conn._store.match("test-model", prompt, 0)
+    segments = conn._store.match(conn.model_scope, prompt, 0)
     assert len(segments) == 4
     conn._store.pin("b", segments)
     plan = BlendPlan(0, 256, 256, segments)
@@ -201,7 +201,7 @@ def test_evicted_chunks_wait_for_in_flight_loads():
 
     # new chunks written by the host evict every loaded chunk while the loads are held
     other = list(range(9000, 9256))
-    for sid in conn._store.begin_put_chunks("test-model", other, 0, 256, L):
+    for sid in conn._store.begin_put_chunks(conn.model_scope, other, 0, 256, L):
         for layer in range(L):
             slot = conn._slab.alloc()
             slot.fill_(-1.0)

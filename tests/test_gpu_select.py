@@ -2,10 +2,9 @@
 
 Index sets are bit-exact for identical scores (the selection is integer work
 on float keys). K-deviation scores match within 1e-5 relative (the float32
-summation order differs); the index set computed from GPU scores must equal
-the oracle's outside the epsilon band at the k-th score (a token may differ
-only if its oracle score lies within twice the largest score difference of
-the k-th candidate score).
+summation order differs); at the headline size the index set computed from
+GPU scores equals the oracle's bit for bit, with the epsilon band around the
+k-th score shown to hold the k-th alone.
 """
 
 import numpy as np
@@ -13,6 +12,7 @@ import pytest
 import torch
 
 import oracle as O
+from cacheblend_vllm import _native
 from cacheblend_vllm import kv_layout as KL
 from cacheblend_vllm import selection as S
 from cacheblend_vllm import synthetic
@@ -159,25 +159,80 @@ def test_kdev_select_full_size_index_set(overflow_blocks):
     want_same = O.select(scores.cpu().numpy(), gap_np, 0.15, forced)
     np.testing.assert_array_equal(selected.cpu().numpy(), want_same)
     # oracle scores agree within tolerance ...
+    got_scores = scores.cpu().numpy()
     want_scores = O.kdev_scores(fresh.float().cpu().numpy(), cached.float().cpu().numpy())
-    np.testing.assert_allclose(scores.cpu().numpy(), want_scores, rtol=SCORE_RTOL)
-    # ... and the index sets agree outside the epsilon band at the k-th score:
-    # a token may differ only if its oracle score lies within twice the
-    # largest score difference of the k-th candidate score
+    np.testing.assert_allclose(got_scores, want_scores, rtol=SCORE_RTOL)
+    # ... and, on these fixed inputs, the index set is the oracle's bit for
+    # bit. Measured on the CPU: the k-th candidate score is 2332 float32 ulps
+    # (overflow 0) and 51 ulps (overflow 1) from its neighbours, while the
+    # float32 summation order moves a score by at most a few ulps; so the
+    # band of candidates within twice the largest relative score error of
+    # the k-th holds the k-th alone.
     want = O.select(want_scores, gap_np, 0.15, forced)
     base = gap_np | (forced if forced is not None else False)
     cand = np.sort(want_scores[~base])[::-1]
     k = O.select_budget(n, int(gap_np.sum()), int(base.sum()), 0.15)
-    eps = float(np.max(np.abs(scores.cpu().numpy() - want_scores)))
-    band = np.abs(want_scores - cand[k - 1]) <= 2 * eps
+    kth = cand[k - 1]
+    live = ~base & (want_scores > 0)
+    rel_err = float(np.max(np.abs(got_scores[live] - want_scores[live]) / want_scores[live]))
+    band = ~base & (np.abs(want_scores - kth) <= 2 * rel_err * kth)
     disagree = np.setxor1d(selected.cpu().numpy(), want)
-    print(f"k={k} eps={eps:.3e} band={int(band.sum())} disagreements={disagree.size}", flush=True)
-    assert band.sum() < 64
-    assert np.all(band[disagree])
-    assert selected.numel() == want.size
+    print(f"k={k} kth={kth:.7g} max rel score error {rel_err:.3e} band={int(band.sum())} "
+          f"disagreements={disagree.size}", flush=True)
+    assert int(band.sum()) == 1
+    assert disagree.size == 0
+    np.testing.assert_array_equal(selected.cpu().numpy(), want)
     # determinism run to run
     again, _ = S.kdev_select(fresh, cached, None, gap, 0.15, radius=radius)
     assert torch.equal(again, selected)
+
+
+@pytest.mark.parametrize("n", [1000, 4097, 65536])
+def test_one_launch_select_gives_up_cleanly_then_falls_back(n):
+    """The one-launch select's bounded wait made to give up from the host
+    (CBK_SELECT_TEST_GIVE_UP: the first barrier expects one arrival more than
+    the grid makes and polls zero times, so every workgroup exits normally):
+    the count comes back -1 with no index written, and ``select`` /
+    ``kdev_select`` then run the multi-launch select, whose result is the
+    oracle's bit for bit."""
+    rng = np.random.default_rng(900 + n)
+    scores = (rng.standard_normal(n) ** 2).astype(np.float32)
+    gap = rng.random(n) < 0.2
+    want = O.select(scores, gap, 0.15, O.dilate(gap, 16))
+    s_dev, g_dev = torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV)
+    # through the C ABI, with the outputs prefilled: -1 and no index written
+    lib = _native.load()
+    out = torch.full((n,), -5, dtype=torch.long, device=DEV)
+    count = torch.full((1,), -7, dtype=torch.long, device=DEV)
+    ws = torch.empty(lib.cbk_select_workspace_bytes(n), dtype=torch.uint8, device=DEV)
+    rc = lib.cbk_select_ex(s_dev.data_ptr(), g_dev.view(torch.uint8).data_ptr(), None, n, 16, 0.15,
+                           out.data_ptr(), count.data_ptr(), ws.data_ptr(), ws.numel(),
+                           _native.SELECT_TEST_GIVE_UP, _native.stream_handle(DEV))
+    _native.check(rc, "select_ex")
+    torch.cuda.synchronize()
+    assert int(count.item()) == -1
+    assert bool((out == -5).all())
+    got = S.select(s_dev, g_dev, 0.15, radius=16, flags=_native.SELECT_TEST_GIVE_UP)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    multi, mcount = S.select_async(s_dev, g_dev, 0.15, radius=16, flags=_native.SELECT_MULTI_LAUNCH)
+    np.testing.assert_array_equal(multi[: int(mcount.item())].cpu().numpy(), want)
+    fresh, cached, kgap = synthetic.kdev_inputs(n, 4, 128, torch.bfloat16, DEV, seed=n)
+    sel_fb, sc_fb = S.kdev_select(fresh, cached, None, kgap, 0.15, radius=16, flags=_native.SELECT_TEST_GIVE_UP)
+    kgap_np = kgap.cpu().numpy()
+    np.testing.assert_array_equal(sel_fb.cpu().numpy(),
+                                  O.select(sc_fb.cpu().numpy(), kgap_np, 0.15, O.dilate(kgap_np, 16)))
+    sel, sc = S.kdev_select(fresh, cached, None, kgap, 0.15, radius=16)
+    assert torch.equal(sc.view(torch.int32), sc_fb.view(torch.int32))
+    assert torch.equal(sel, sel_fb)
+
+
+def test_select_flag_checks():
+    s_dev = torch.rand(100, device=DEV)
+    g_dev = torch.zeros(100, dtype=torch.bool, device=DEV)
+    with pytest.raises(ValueError, match="unknown select flags"):
+        S.select_async(s_dev, g_dev, 0.15, flags=8)
+    with pytest.raises(ValueError, match="needs the one-launch select"):
+        S.select_async(s_dev, g_dev, 0.15, flags=_native.SELECT_TEST_GIVE_UP | _native.SELECT_MULTI_LAUNCH)
 
 
 def test_selector_kv_deviation_block_matches_reference_composition():
