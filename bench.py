@@ -213,6 +213,7 @@ def main() -> int:
         reload_slots = synthetic.block_slots(perm[1024:1536], BS, T).to(dev)
         result.update(extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev,
                              reload_slots, (gather_ms, scatter_ms)))
+        result.update(_headline_scalars(result))
 
     if not args.skip_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, synthetic)
@@ -327,6 +328,46 @@ def extras(torch, KL, S, synthetic, layers, cache, src_slots, staging, args, dev
     return out
 
 
+def _headline_scalars(r: dict) -> dict:
+    """Each configuration's headline figure as a top-level scalar (readers of
+    the JSON line that keep scalars only still see them)."""
+    out = {}
+
+    def put(name, *path):
+        node = r
+        for key in path:
+            if not isinstance(node, dict) or key not in node:
+                return
+            node = node[key]
+        out[name] = node
+
+    put("scatter_frac", "scatter_kernel", "frac")
+    put("per_layer_gather_frac", "per_layer_gather", "frac_of_hbm_peak")
+    put("per_layer_scatter_frac", "per_layer_scatter", "frac_of_hbm_peak")
+    put("host_link_d2h_frac", "host_link", "d2h_frac")
+    put("host_link_h2d_frac", "host_link", "h2d_frac")
+    put("kdev_us_per_64k", "kdev_select", "us_per_64k_tokens")
+    put("kdev_score_kernel_us", "kdev_select", "score_kernel_us")
+    put("sparse_q_ms", "sparse_q", "score_ms")
+    put("sparse_q_ms_min", "sparse_q", "score_ms_min")
+    put("sparse_q_mfma_frac", "sparse_q", "mfma_frac_of_bf16_peak")
+    put("attention_ms", "blend_attention", "ms")
+    put("attention_ms_min", "blend_attention", "ms_min")
+    put("attention_mfma_frac", "blend_attention", "mfma_frac_of_bf16_peak")
+    # the store's default transfer (StoreStreamWriter slab_transfer="dma")
+    put("store_d2h_GBps", "store_pipeline", "dma", "d2h_GBps")
+    put("store_d2h_GBps_mean", "store_pipeline", "dma", "d2h_GBps_mean")
+    put("store_host_link_frac", "store_pipeline", "dma", "host_link_frac")
+    put("store_hidden_frac", "store_pipeline", "with_gemm_compute", "dma", "store_hidden_frac")
+    put("reload_h2d_GBps", "store_pipeline", "reload_h2d", "h2d_GBps")
+    put("reload_host_link_frac", "store_pipeline", "reload_h2d", "host_link_frac")
+    put("blend_load_h2d_GBps", "blend_load", "dma", "h2d_GBps")
+    put("blend_load_host_link_frac", "blend_load", "dma", "host_link_frac")
+    put("blend_load_hidden_frac", "blend_load", "dma", "busy_wait", "load_hidden_frac")
+    put("commit_scatter_frac", "blend_load", "commit_scatter", "frac_of_hbm_peak")
+    return out
+
+
 def token_matcher_bench(args, n_tokens=131072, n_chunks=512, chunk=256):
     """Scheduler lookup (host code): find 256-token stored chunks at any
     offset of a 128K-token prompt, half of it made of registered chunks
@@ -396,9 +437,14 @@ def sparse_q(torch, S, synthetic, dev):
     flops_pass = 2.0 * d * hq * float((pos + 1).sum())
     scale = d ** -0.5
     fn = lambda: S.sparse_q_full_scores(query, key, rows, absolute, scale, out_index=absolute)  # noqa: E731
-    fn()
-    fn()
-    ms = min(event_time_ms(torch, fn, 3) for _ in range(3))  # steady state: best of 3 rounds of 3
+    # steady state: after a second of other kernels over the same tensors and
+    # 8 calls (the first rounds after a cold start ran up to 9% slower), the
+    # mean of 5 rounds of 3 calls, the fastest round beside it
+    _settle(torch, (query, key), 1.0)
+    for _ in range(8):
+        fn()
+    rounds = [event_time_ms(torch, fn, 3) for _ in range(5)]
+    ms, ms_min = statistics.fmean(rounds), min(rounds)
     sel = S.BlendSelector(CacheBlendConfig.from_extra_config(
         {"selection_strategy": "sparse_q", "check_layers": [1]}), 16)
     sel.sparse_q_select(query, key, absolute, gap, scale, 1)  # first call: workspaces, code loading
@@ -415,9 +461,12 @@ def sparse_q(torch, S, synthetic, dev):
     return {
         "queries": nq, "keys": nk, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
         "score_ms": round(ms, 3),
+        "score_ms_min": round(ms_min, 3),
+        "score_ms_rounds": [round(r, 3) for r in rounds],
         "algorithmic_flops": flops_pass,
         "TFLOPs": round(achieved, 1),
         "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4),
+        "mfma_frac_of_bf16_peak_min_time": round(flops_pass / (ms_min / 1e3) / 1e12 / 2500.0, 4),
         "executed_two_pass_TFLOPs": round(2 * achieved, 1),
         "exp_per_s": round(2 * hq * float((pos + 1).sum()) / (ms / 1e3), 1),
         "select_total_ms_with_masks_and_sync": round(total_ms, 3),
@@ -448,13 +497,19 @@ def blend_attention_bench(torch, dev):
     d, hq = q.shape[2], q.shape[1]
     flops = 4.0 * d * hq * float((pos_np + 1).sum())
     fn = lambda: blend_attention(q, k, v, pos, d ** -0.5)  # noqa: E731
-    fn()
-    fn()
-    ms = min(event_time_ms(torch, fn, 3) for _ in range(3))  # steady state: best of 3 rounds of 3
+    # steady state: after a second of other kernels over the same tensors and
+    # 8 calls, the mean of 5 rounds of 3 calls, the fastest round beside it
+    _settle(torch, (q, k, v), 1.0)
+    for _ in range(8):
+        fn()
+    rounds = [event_time_ms(torch, fn, 3) for _ in range(5)]
+    ms, ms_min = statistics.fmean(rounds), min(rounds)
     achieved = flops / (ms / 1e3) / 1e12
     return {"queries": q.shape[0], "keys": k.shape[0], "q_heads": hq, "kv_heads": k.shape[1], "head_dim": d,
-            "ms": round(ms, 3), "flops": flops, "TFLOPs": round(achieved, 1),
-            "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4)}
+            "ms": round(ms, 3), "ms_min": round(ms_min, 3), "ms_rounds": [round(r, 3) for r in rounds],
+            "flops": flops, "TFLOPs": round(achieved, 1),
+            "mfma_frac_of_bf16_peak": round(achieved / 2500.0, 4),
+            "mfma_frac_of_bf16_peak_min_time": round(flops / (ms_min / 1e3) / 1e12 / 2500.0, 4)}
 
 
 def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
@@ -514,10 +569,14 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     result = {"layers": L, "tokens": T, "bytes_d2h": nbytes}
     for mode in ("host_write", "dma", "reference"):
         times = [once(mode) for _ in range(4)]
-        best = min(t for t, _ in times[1:])  # rep 0 also pins the slab's arenas / warms the pools
-        result[mode] = {"ms": round(best * 1e3, 3), "first_rep_ms": round(times[0][0] * 1e3, 3),
+        steady = [t for t, _ in times[1:]]  # rep 0 also pins the slab's arenas / warms the pools
+        best, mean = min(steady), statistics.fmean(steady)
+        result[mode] = {"ms": round(best * 1e3, 3), "mean_ms": round(mean * 1e3, 3),
+                        "first_rep_ms": round(times[0][0] * 1e3, 3),
                         "chunks_committed": times[-1][1], "d2h_GBps": round(nbytes / best / 1e9, 2),
-                        "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4)}
+                        "d2h_GBps_mean": round(nbytes / mean / 1e9, 2),
+                        "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4),
+                        "host_link_frac_mean": round(nbytes / mean / 1e9 / HOST_LINK_PEAK_GBPS, 4)}
     # overlap with compute
     torch.mm(a, b, out=c)
     torch.cuda.synchronize()
@@ -575,8 +634,10 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
         reload()
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
-    best = min(times)
-    result["reload_h2d"] = {"ms": round(best * 1e3, 3), "h2d_GBps": round(nbytes / best / 1e9, 2),
+    best, mean = min(times), statistics.fmean(times)
+    result["reload_h2d"] = {"ms": round(best * 1e3, 3), "mean_ms": round(mean * 1e3, 3),
+                            "h2d_GBps": round(nbytes / best / 1e9, 2),
+                            "h2d_GBps_mean": round(nbytes / mean / 1e9, 2),
                             "host_link_frac": round(nbytes / best / 1e9 / HOST_LINK_PEAK_GBPS, 4),
                             "launches": L, "bit_exact_layers_checked": [0, L - 1]}
     store.release("reload")
@@ -857,13 +918,19 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     key = (torch.randn((nk, hkv, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
     rows = torch.from_numpy(np.flatnonzero(synthetic.sparse_q_layout(nk, 4096, seed=0))).to(dev)
     absolute = torch.arange(nk, device=dev)
-    for _ in range(max(1, args.steps // 2)):
+    # steady state: the Sparse-Q and attention calls follow a few seconds of
+    # other kernels over the same tensors (page tables and clocks settled)
+    _settle(torch, (query, key))
+    # 8 warm-up calls, then the steady-state calls (the bench line times the
+    # same sequence: settle, 8 calls, then its timed rounds)
+    for _ in range(8 + max(5, args.steps // 2)):
         S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, out_index=absolute)
     del query, key
     from cacheblend_vllm.attention import blend_attention
 
     aq, ak, av, apos, _ = _attention_inputs(torch, dev)
-    for _ in range(max(1, args.steps // 2)):
+    _settle(torch, (aq, ak, av))
+    for _ in range(8 + max(5, args.steps // 2)):
         blend_attention(aq, ak, av, apos, 128 ** -0.5)
     del aq, ak, av
     _profile_host_link(torch, synthetic, cache, src_slots, args, dev)
@@ -872,6 +939,17 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
         "gathers and scatters, C3 commits, store gather into host chunks, blend assembly from "
         "host chunks), sparse_q, attention")
     return 0
+
+
+def _settle(torch, tensors, seconds: float = 2.0) -> None:
+    """Reductions over ``tensors`` for about ``seconds`` (torch's own kernels):
+    their pages are mapped and the clocks are at their working level before
+    the kernels under study run."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for t in tensors:
+            t.view(-1)[::7].float().sum()
+        torch.cuda.synchronize()
 
 
 def _profile_commit(torch, synthetic, args, dev):
@@ -1146,14 +1224,14 @@ def cpu_baseline(torch, synthetic):
                         "else its CPU affinity)",
         **host,
         "c1_plumbing_us": round(c1_med * 1e6, 1),
-        "c3_blend_load": {"ms_per_layer": round(c3_layer_s * 1e3, 2),
-                          "hit_GBps": round(hit * 2 * H3 * D * 2 / c3_layer_s / 1e9, 3),
-                          "est_48_layers_ms": round(48 * c3_layer_s * 1e3, 1),
-                          "sample": f"2 of 48 layers, median of {c3_runs} runs"},
+        "c3_ms_per_layer": round(c3_layer_s * 1e3, 2),
+        "c3_hit_GBps": round(hit * 2 * H3 * D * 2 / c3_layer_s / 1e9, 3),
+        "c3_est_48_layers_ms": round(48 * c3_layer_s * 1e3, 1),
+        "c3_sample": f"2 of 48 layers, median of {c3_runs} runs",
         "kdev_select_us_per_64k_tokens": round(c4_med * 1e6, 1),
-        "c5_sparse_q": {"ms_per_chunk": round(c5_chunk_s * 1e3, 2),
-                        "est_full_ms": round(512 * c5_chunk_s * 1e3, 1),
-                        "sample": "16 of 512 chunks of 8 queries (evenly spaced), scaled x32"},
+        "c5_ms_per_chunk": round(c5_chunk_s * 1e3, 2),
+        "c5_est_full_ms": round(512 * c5_chunk_s * 1e3, 1),
+        "c5_sample": "16 of 512 chunks of 8 queries (evenly spaced), scaled x32",
     }
 
 

@@ -590,14 +590,18 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
         round_pair<RMODE>(r[0], r[1]);
         round_pair<RMODE>(r[2], r[3]);
         const int32_t key = kw0 + c * 16 + int32_t(col);
-        float sum = acc_col[c];
+        float p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float p = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i]));
-          if constexpr (MASK) p = key > rpos[i] ? 0.f : p;
-          sum += p;
+          p[i] = __builtin_amdgcn_exp2f(fmaf(r[i], a.c2, -mrow[i]));
+          if constexpr (MASK) p[i] = key > rpos[i] ? 0.f : p[i];
         }
-        acc_col[c] = sum;
+        // a pair tree, not a chain of four adds into the column sum: 1-1.4%
+        // off the C5 column pass (its sums on the matrix core, by an
+        // identity-A 4x4x4 MFMA that adds a lane's four bf16 values to its
+        // own accumulators, measured 3.7% slower: the matrix core's work grew
+        // by 6% while the VALU's shrank by 10%)
+        acc_col[c] += (p[0] + p[1]) + (p[2] + p[3]);
       }
     }
   }
