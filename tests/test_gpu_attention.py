@@ -13,7 +13,8 @@ the rounding of the probabilities. With N(0,1) inputs the dot products reach
 ~45, where a bf16 ulp is 0.25: a dot product within float32 accumulation
 error of a rounding boundary can round either way (in the reference's own
 torch matmul as well), moving that key's weight by ~2%. That case is checked
-separately with a bound on the fraction of such elements."""
+separately: each element within the tolerance plus the most such logits of
+its row can move it."""
 
 import numpy as np
 import pytest
@@ -102,17 +103,58 @@ def test_blend_attention_closed_forms_and_errors():
     assert blend_attention(q[:0].to(DEV), k.to(DEV), v.to(DEV), pos[:0], 1.0).shape == (0, 8, d)
 
 
+def _rounding_allowance(q, k, v, pos, scale, mass):
+    """Per output element, the most that logits whose bf16 rounding the inputs
+    do not fix can move it. A logit is unfixed when its exact dot product lies
+    within (D - 1) * 2^-24 * sum_i |q_i k_i| of a bf16 rounding midpoint -- the
+    first-order error bound of any order of fp32 additions of the D exact bf16
+    products -- so an fp32 sum in another order (the reference's torch matmul
+    and the MFMA sum add in different orders) may land on either side. Flipping it moves the
+    rounded dot by one bf16 ulp u, the logit w = r(r(dot) * scale) by at most
+    u * scale + ulp(w), its probability p_k by a factor up to e^dw, and the
+    other probabilities by the renormalisation; so an output element moves by
+    at most sum_k p_k (e^dw_k - 1) (|v_k| + mass) over the row's unfixed keys."""
+    qf, kf, vf = q.double().numpy(), k.double().numpy(), v.double().numpy()
+    nq, hq, d = qf.shape
+    g = hq // kf.shape[1]
+    visible = pos.numpy()[:, None] >= np.arange(kf.shape[0])[None, :]
+    allow = np.zeros((nq, hq, d))
+    unfixed_rows = 0
+    for h in range(hq):
+        kh, vh = kf[:, h // g, :], np.abs(vf[:, h // g, :])
+        dot = qf[:, h, :] @ kh.T
+        err = (d - 1) * 2.0 ** -24 * (np.abs(qf[:, h, :]) @ np.abs(kh).T)
+        bits = np.abs(dot).astype(np.float32).view(np.uint32) & np.uint32(0xFFFF0000)
+        lo = bits.view(np.float32).astype(np.float64)
+        ulp = (bits + np.uint32(0x10000)).view(np.float32).astype(np.float64) - lo
+        unfixed = visible & (np.abs(np.abs(dot) - (lo + ulp / 2)) <= err)
+        unfixed_rows += int(unfixed.any(axis=1).sum())
+        w = O.round_bf16(O.round_bf16(dot) * np.float32(scale)).astype(np.float64)
+        w = np.where(visible, w, -np.inf)
+        e = np.exp(w - w.max(axis=1, keepdims=True))
+        p = e / e.sum(axis=1, keepdims=True)
+        ulp_w = np.abs(w) * 2.0 ** -7  # a bf16 ulp of the logit, at most
+        dw = ulp * scale + np.where(visible, ulp_w, 0.0)
+        move = np.where(unfixed, p * np.expm1(dw), 0.0)               # [nq, nk]
+        allow[:, h, :] = move @ vh + move.sum(axis=1, keepdims=True) * mass[:, h, :]
+    return allow, unfixed_rows
+
+
 def test_blend_attention_gaussian_inputs_rounding_boundary_bound():
-    """N(0,1) queries/keys (unscaled, |dot| up to ~45): all but a small
-    fraction of elements within the parity tolerance, none far off."""
+    """N(0,1) queries/keys (unscaled, |dot| up to ~45, where a bf16 ulp is
+    0.25): every output element within the parity tolerance plus what the
+    row's logits with an unfixed rounding can move it (_rounding_allowance)."""
     nq, nk, hq, hkv, d = 300, 1500, 32, 4, 128
     q, k, v, pos = _case(nq, nk, hq, hkv, d, torch.bfloat16, seed=21, exact_dots=False)
     got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, d ** -0.5).float().cpu().numpy()
     want, mass = _oracle(q, k, v, pos, d ** -0.5)
-    ratio = np.abs(got - want) / np.maximum(mass, 1e-30)
-    outside = ratio > RTOL
-    print(f"gaussian: {outside.mean():.2e} of elements outside, max ratio {ratio.max():.3e}", flush=True)
-    assert outside.mean() < 1e-4
+    allow, unfixed_rows = _rounding_allowance(q.float(), k.float(), v.float(), pos, d ** -0.5, mass)
+    err = np.abs(got - want)
+    ratio = err / np.maximum(mass, 1e-30)
+    outside = err > RTOL * mass + 1e-7
+    print(f"gaussian: {int(outside.sum())} elements outside the tolerance, {unfixed_rows} of "
+          f"{nq * hq} rows with an unfixed rounding, max ratio {ratio.max():.3e}", flush=True)
+    assert np.all(err <= RTOL * mass + allow + 1e-7)
     assert ratio.max() < 5e-2
 
 

@@ -200,6 +200,23 @@ def test_sparse_q_full_layer6_vs_oracle_and_properties():
     err = np.max(np.abs(sub - want) / np.maximum(want, 1e-30))
     print(f"max relative score error over {nk} keys: {err:.3e}", flush=True)
     np.testing.assert_allclose(sub, want, rtol=RTOL, atol=1e-6)
+    # the selection over all 98,304 tokens on these scores (top 15% of the
+    # cached keys, gaps and 16-token overflow forced): the GPU's index set
+    # equals the oracle's outside the epsilon band at the k-th score
+    forced = O.dilate(gap, 16)
+    got_sel = S.select(torch.from_numpy(sub).to(DEV), torch.from_numpy(gap).to(DEV), 0.15,
+                       torch.from_numpy(forced).to(DEV)).cpu().numpy()
+    want_sel = O.select(want, gap, 0.15, forced)
+    base = gap | forced
+    k_budget = O.select_budget(nk, int(gap.sum()), int(base.sum()), 0.15)
+    kth = np.sort(want[~base])[::-1][k_budget - 1]
+    eps = float(np.max(np.abs(sub - want)[~base]))
+    band = ~base & (np.abs(want - kth) <= 2 * eps)
+    disagree = np.setxor1d(got_sel, want_sel)
+    print(f"full-context selection: {got_sel.size} selected, band {int(band.sum())}, "
+          f"disagreements {disagree.size}", flush=True)
+    assert got_sel.size == want_sel.size
+    assert np.all(band[disagree])
     # linearity over the query set at the full size
     np.testing.assert_allclose(full, sub + rest, rtol=1e-4, atol=1e-6)
     full64 = full.astype(np.float64)
