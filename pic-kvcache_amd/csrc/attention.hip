@@ -13,8 +13,12 @@
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K rows, B = Q rows,
 //                   both 16-byte loads of 8 consecutive dims; the result
 //                   holds key 4*(lane/16)+i of row lane%16 in register i
-//   online softmax  per row in the log2 domain, the row's 32 keys spread
-//                   over its 4 lane groups (two xor shuffles)
+//   softmax         per row in the log2 domain against a fixed reference:
+//                   the maximum of the row's first block (a logit of the row,
+//                   so no term exceeds 2^(max - m)); no per-logit maximum in
+//                   the later blocks. A row whose sum outgrows it (2^100) is
+//                   recomputed with online maxima (lazily rescaled, the row's
+//                   32 keys of a block spread over its 4 lane groups)
 //   O += P . V      v_mfma_f32_16x16x32_{bf16,f16}: the two halves' S^T
 //                   registers, concatenated, are the A operand (row lane%16,
 //                   keys 4*(lane/16)..+3 and 16+4*(lane/16)..+3: the
@@ -176,7 +180,7 @@ __device__ __forceinline__ void qk_block(const uint16_t* ks, const BlockOffsets<
 // position); lm[t] = this lane's maximum over its logits of row tile t, taken
 // before the second rounding (rounding is monotonic, and the reference
 // maximum only needs to bound the logits within the rescale headroom).
-template <bool F16, int RT, bool MASK>
+template <bool F16, int RT, bool MASK, bool WITH_MAX = true>
 __device__ __forceinline__ void logits_block(f32x4 (&s)[RT][2], int32_t k0, float scale, const int32_t (&rpos)[RT],
                                              float (&lm)[RT], uint32_t grp) {
 #pragma unroll
@@ -194,8 +198,9 @@ __device__ __forceinline__ void logits_block(f32x4 (&s)[RT][2], int32_t k0, floa
           if (k0 + 16 * h + int32_t(4 * grp) + i > rpos[t]) y[h][i] = kNegInf;
       }
     }
-    lm[t] = fmaxf(fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3])),
-                  fmaxf(fmaxf(y[1][0], y[1][1]), fmaxf(y[1][2], y[1][3])));
+    if constexpr (WITH_MAX)
+      lm[t] = fmaxf(fmaxf(fmaxf(y[0][0], y[0][1]), fmaxf(y[0][2], y[0][3])),
+                    fmaxf(fmaxf(y[1][0], y[1][1]), fmaxf(y[1][2], y[1][3])));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       round2<F16>(y[h][0], y[h][1]);
@@ -425,8 +430,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
   constexpr uint32_t kSlot = kKeyBlock * D * 2, kVOffset = kBuffers * kSlot;
   const int64_t kstep = int64_t(kKeyBlock) * a.k_stride * 2, vstep = int64_t(kKeyBlock) * a.v_stride * 2;
   const bool last_whole = nblocks * kKeyBlock <= int32_t(a.nk);
-  const char* kg = reinterpret_cast<const char*>(a.k) + int64_t(min(3, nblocks - 1)) * kstep;
-  const char* vg = reinterpret_cast<const char*>(a.v) + int64_t(min(1, nblocks - 1)) * vstep;
+  const char* const kg0 = reinterpret_cast<const char*>(a.k) + int64_t(min(3, nblocks - 1)) * kstep;
+  const char* const vg0 = reinterpret_cast<const char*>(a.v) + int64_t(min(1, nblocks - 1)) * vstep;
+  const char* kg = kg0;
+  const char* vg = vg0;
   auto stream = [&](int32_t j, const char*& g, int64_t stride_bytes, int64_t stride, const uint32_t (&offs)[kInsts],
                     uint32_t l) __attribute__((always_inline)) {
     const bool inner = j < nblocks - 1;
@@ -450,11 +457,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
   // P of block b - 1; the step leaves S^T of block b + 1 in sn and P of
   // block b in pc (two register sets taken in turn: no copies between
   // steps).
-  auto step = [&](auto kind, auto first, auto phase, int32_t b, f32x4 (&sc)[RT][2], f32x4 (&sn)[RT][2],
-                  typename O::A8 (&pp)[RT], typename O::A8 (&pc)[RT]) __attribute__((always_inline)) {
+  auto step = [&](auto kind, auto first, auto phase, auto fix, int32_t b, f32x4 (&sc)[RT][2],
+                  f32x4 (&sn)[RT][2], typename O::A8 (&pp)[RT], typename O::A8 (&pc)[RT])
+                  __attribute__((always_inline)) {
     constexpr int KIND = decltype(kind)::value;
     constexpr bool FIRST = decltype(first)::value;
     constexpr int PHASE = decltype(phase)::value;
+    constexpr bool FIX = decltype(fix)::value;
     CBK_WAIT_VM_LGKM0(2 * kInsts);  // K(b + 1) and V(b - 1) have landed
     asm volatile("s_barrier" ::: "memory");
     uint32_t kb_addr, vb_addr, kw_addr, vw_addr;
@@ -477,7 +486,15 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
     if constexpr (KIND < 3) {
       const uint16_t* ks = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)kb_addr;
       const uint16_t* vs = (const uint16_t*)(__attribute__((address_space(3))) const uint16_t*)(size_t)vb_addr;
-      if constexpr (KIND < 2) {
+      if constexpr (KIND < 2 && FIX) {
+        qk_block<F16, D, RT>(ks, off, qf, sn);
+        float lm[RT];
+        logits_block<F16, RT, KIND == 1, false>(sc, b * kKeyBlock, a.scale, rpos, lm, grp);
+        probs_block<F16, RT>(sc, nms, pc);
+        if constexpr (!FIRST) pv_block<F16, D, RT>(vs, off, pp, o, ol);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) asm volatile("" : "+v"(pc[t]));
+      } else if constexpr (KIND < 2) {
         qk_block<F16, D, RT>(ks, off, qf, sn);
         float lm[RT];
         logits_block<F16, RT, KIND == 1>(sc, b * kKeyBlock, a.scale, rpos, lm, grp);
@@ -510,8 +527,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
 #pragma unroll
         for (int t = 0; t < RT; ++t) asm volatile("" : "+v"(pc[t]));
       } else if constexpr (!FIRST) {
-        if (pending) rescale_o();
-        pending = false;
+        if constexpr (!FIX) {
+          if (pending) rescale_o();
+          pending = false;
+        }
         pv_block<F16, D, RT>(vs, off, pp, o, ol);
       }
     }
@@ -527,8 +546,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
   using any = std::integral_constant<int, -1>;
   // one step with its buffers chosen at run time, S^T of block b in sa and P
   // of block b - 1 in pa before and after
-  auto single = [&](auto kind, int32_t& b) __attribute__((always_inline)) {
-    step(kind, no(), any(), b++, sa, sb, pa, pb);
+  auto single = [&](auto kind, auto fix, int32_t& b) __attribute__((always_inline)) {
+    step(kind, no(), any(), fix, b++, sa, sb, pa, pb);
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
       sa[t][0] = sb[t][0];
@@ -539,19 +558,22 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
   // steps [b, end) of one kind: six at a time from a multiple of 6 (the
   // three-buffer rings and the two register sets back where they started),
   // single steps at the edges
-  auto run = [&](auto kind, int32_t& b, int32_t end) __attribute__((always_inline)) {
-    while (b < end && b % 6 != 0) single(kind, b);
+  auto run = [&](auto kind, auto fix, int32_t& b, int32_t end) __attribute__((always_inline)) {
+    while (b < end && b % 6 != 0) single(kind, fix, b);
     for (; b + 6 <= end; b += 6) {
-      step(kind, no(), std::integral_constant<int, 0>(), b, sa, sb, pa, pb);
-      step(kind, no(), std::integral_constant<int, 1>(), b + 1, sb, sa, pb, pa);
-      step(kind, no(), std::integral_constant<int, 2>(), b + 2, sa, sb, pa, pb);
-      step(kind, no(), std::integral_constant<int, 3>(), b + 3, sb, sa, pb, pa);
-      step(kind, no(), std::integral_constant<int, 4>(), b + 4, sa, sb, pa, pb);
-      step(kind, no(), std::integral_constant<int, 5>(), b + 5, sb, sa, pb, pa);
+      step(kind, no(), std::integral_constant<int, 0>(), fix, b, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 1>(), fix, b + 1, sb, sa, pb, pa);
+      step(kind, no(), std::integral_constant<int, 2>(), fix, b + 2, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 3>(), fix, b + 3, sb, sa, pb, pa);
+      step(kind, no(), std::integral_constant<int, 4>(), fix, b + 4, sa, sb, pa, pb);
+      step(kind, no(), std::integral_constant<int, 5>(), fix, b + 5, sb, sa, pb, pa);
     }
-    while (b < end) single(kind, b);
+    while (b < end) single(kind, fix, b);
   };
-  if (nblocks > 0) {
+  // one pass over the blocks; the first step always takes the lazy path (it
+  // sets each row's reference from block 0, where every row with a position
+  // sees key 0 at least)
+  auto pass = [&](auto fix) __attribute__((always_inline)) {
     // K of blocks 0-2 and V of block 0 ahead of step 0; then every wave
     // takes steps 0 .. nblocks (the requests and barriers of each)
     request(0, a.k, a.k_stride, koff, kbuf);
@@ -567,7 +589,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
     }
     int32_t b = 0;
     auto first = [&](auto kind) __attribute__((always_inline)) {
-      step(kind, yes(), any(), b++, sa, sb, pa, pb);
+      step(kind, yes(), any(), no(), b++, sa, sb, pa, pb);
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
         sa[t][0] = sb[t][0];
@@ -579,14 +601,54 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
       first(visible());
     else if (b_w > 0)
       first(masked());
-    run(visible(), b, b_m);
-    run(masked(), b, b_w);
+    run(visible(), fix, b, b_m);
+    run(masked(), fix, b, b_w);
     if (b_w > 0)
-      step(last(), no(), any(), b++, sa, sb, pa, pb);
+      step(last(), no(), any(), fix, b++, sa, sb, pa, pb);
     else
-      step(none(), yes(), any(), b++, sa, sb, pa, pb);
-    for (; b <= nblocks; ++b) step(none(), no(), any(), b, sa, sb, pa, pb);
+      step(none(), yes(), any(), fix, b++, sa, sb, pa, pb);
+    for (; b <= nblocks; ++b) step(none(), no(), any(), fix, b, sa, sb, pa, pb);
     CBK_WAIT_VM_LGKM0(0);  // no LDS write in flight past this point
+  };
+  // Fixed reference: after block 0 every row keeps the reference its first
+  // step set (a logit of the row, so p <= 2^(max - m)) -- no per-logit
+  // maximum, no threshold ballot. A row whose terms outgrew it (its sum past
+  // 2^100: a logit more than ~69 above the first block's maximum) or whose
+  // output is not finite is recomputed, workgroup-wide, with the lazy
+  // rescaling.
+  __shared__ uint32_t s_redo;
+  if (nblocks > 0) {
+    pass(yes());
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bad |= !(ol[t][i] < 0x1p100f);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) bad |= !(fabsf(o[t][c][i]) < 3.0e38f);
+      }
+    }
+    if (threadIdx.x == 0) s_redo = 0;
+    __syncthreads();
+    if (bad) s_redo = 1;
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(s_redo)) {  // uniform: the pass's loops stay scalar
+      pending = false;
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        m[t] = kNegInf;
+        nms[t] = 0.f;
+        thr[t] = kNegInf;
+        alpha[t] = 1.f;
+        ol[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) o[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      kg = kg0;
+      vg = vg0;
+      pass(no());
+    }
   }
   __syncthreads();  // every wave is done with the K buffers the output staging reuses
 

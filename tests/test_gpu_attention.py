@@ -195,13 +195,18 @@ def test_blend_attention_partial_key_blocks(nq, nk, d):
 
 
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 128), (torch.bfloat16, 64)])
-def test_blend_attention_rising_row_maxima(dtype, d):
+@pytest.mark.parametrize("slope", [4.0, 2.0])
+def test_blend_attention_rising_row_maxima(dtype, d, slope):
     """Logits that rise along the keys: the running maximum is raised block
     after block (every block over the first 320 keys, every few blocks over
     the next 512), then stays; half of the heads see the logits falling
     instead (a maximum in the first block, never raised). Exact dots: q is
     +-1/8 in every dim, key j is t_j / 8 in every dim, so q.k_j = +-d t_j / 64
-    (scale 256 / d: logits +-4 t_j at both head sizes)."""
+    (scale 64 slope / d: logits +-slope t_j at both head sizes). At slope 4 the
+    rising rows climb 112 above their first block (161 in log2 units): their
+    terms overflow the first block's reference and the kernel recomputes them
+    with the lazy rescaling; at slope 2 they climb 81 log2 units and stay on
+    the fixed reference, with terms up to 2^81."""
     nq, nk, hq, hkv = 200, 1200, 8, 2
     g = torch.Generator().manual_seed(77)
     j = torch.arange(nk)
@@ -212,10 +217,10 @@ def test_blend_attention_rising_row_maxima(dtype, d):
     q = (sign[None, :, None] / 8).expand(nq, hq, d).to(dtype)
     v = torch.randn(nk, hkv, d, generator=g).to(dtype)
     pos = torch.randperm(nk, generator=g)[:nq].sort().values
-    scale = 256.0 / d  # the same logits at both head sizes
+    scale = 64.0 * slope / d  # the same logits at both head sizes
     got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos, scale)
     rounding = "bf16" if dtype == torch.bfloat16 else "f16"
-    _check(got, _oracle(q, k, v, pos, scale, rounding), f"rising maxima {dtype} d={d}")
+    _check(got, _oracle(q, k, v, pos, scale, rounding), f"rising maxima {dtype} d={d} slope={slope}")
 
 
 @pytest.mark.parametrize("seed", range(8))
