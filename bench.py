@@ -437,10 +437,8 @@ def sparse_q(torch, S, synthetic, dev):
     flops_pass = 2.0 * d * hq * float((pos + 1).sum())
     scale = d ** -0.5
     fn = lambda: S.sparse_q_full_scores(query, key, rows, absolute, scale, out_index=absolute)  # noqa: E731
-    # steady state: after a second of other kernels over the same tensors and
-    # 8 calls (the first rounds after a cold start ran up to 9% slower), the
-    # mean of 5 rounds of 3 calls, the fastest round beside it
-    _settle(torch, (query, key), 1.0)
+    # steady state: after 8 calls (the first rounds after only two ran up to
+    # 9% slower), the mean of 5 rounds of 3 calls, the fastest round beside it
     for _ in range(8):
         fn()
     rounds = [event_time_ms(torch, fn, 3) for _ in range(5)]
@@ -497,9 +495,8 @@ def blend_attention_bench(torch, dev):
     d, hq = q.shape[2], q.shape[1]
     flops = 4.0 * d * hq * float((pos_np + 1).sum())
     fn = lambda: blend_attention(q, k, v, pos, d ** -0.5)  # noqa: E731
-    # steady state: after a second of other kernels over the same tensors and
-    # 8 calls, the mean of 5 rounds of 3 calls, the fastest round beside it
-    _settle(torch, (q, k, v), 1.0)
+    # steady state: after 8 calls, the mean of 5 rounds of 3 calls, the
+    # fastest round beside it
     for _ in range(8):
         fn()
     rounds = [event_time_ms(torch, fn, 3) for _ in range(5)]
@@ -918,18 +915,14 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
     key = (torch.randn((nk, hkv, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
     rows = torch.from_numpy(np.flatnonzero(synthetic.sparse_q_layout(nk, 4096, seed=0))).to(dev)
     absolute = torch.arange(nk, device=dev)
-    # steady state: the Sparse-Q and attention calls follow a few seconds of
-    # other kernels over the same tensors (page tables and clocks settled)
-    _settle(torch, (query, key))
     # 8 warm-up calls, then the steady-state calls (the bench line times the
-    # same sequence: settle, 8 calls, then its timed rounds)
+    # same sequence: 8 calls, then its timed rounds)
     for _ in range(8 + max(5, args.steps // 2)):
         S.sparse_q_full_scores(query, key, rows, absolute, d ** -0.5, out_index=absolute)
     del query, key
     from cacheblend_vllm.attention import blend_attention
 
     aq, ak, av, apos, _ = _attention_inputs(torch, dev)
-    _settle(torch, (aq, ak, av))
     for _ in range(8 + max(5, args.steps // 2)):
         blend_attention(aq, ak, av, apos, 128 ** -0.5)
     del aq, ak, av
@@ -939,17 +932,6 @@ def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args,
         "gathers and scatters, C3 commits, store gather into host chunks, blend assembly from "
         "host chunks), sparse_q, attention")
     return 0
-
-
-def _settle(torch, tensors, seconds: float = 2.0) -> None:
-    """Reductions over ``tensors`` for about ``seconds`` (torch's own kernels):
-    their pages are mapped and the clocks are at their working level before
-    the kernels under study run."""
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for t in tensors:
-            t.view(-1)[::7].float().sum()
-        torch.cuda.synchronize()
 
 
 def _profile_commit(torch, synthetic, args, dev):
