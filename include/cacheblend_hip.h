@@ -231,7 +231,7 @@ size_t cbk_select_workspace_bytes(int64_t n);
  * (ascend.py:662-671) when radius > 0. Masks are uint8 (0/1).
  *
  * A count of -1 means the one-launch select gave up and wrote no index: it
- * runs every 2048-token tile in its own workgroup with grid barriers between
+ * runs every 4096-token tile in its own workgroup with grid barriers between
  * phases, launched only when the occupancy query says all the workgroups fit
  * on the device at once; workgroups of kernels on other streams can still
  * hold the CUs, and a barrier that waits about 2^22 polls for the missing

@@ -256,26 +256,29 @@ __device__ __forceinline__ bool last_block(uint32_t* ticket, uint32_t nblocks, u
 }
 
 // Among bins scanned from the highest down, find the one holding the k-th
-// largest key: cum(above) < k <= cum(above) + hist[bin].
-template <int NBINS>
+// largest key: cum(above) < k <= cum(above) + hist[bin]. NT threads, PER
+// bins each; threads past the last bin (NT > NBINS) read nothing.
+template <int NBINS, int NT = kSelThreads>
 __device__ void find_bin_desc(const uint32_t* hist, uint32_t k, uint32_t* lds_scan,
                               uint32_t* out_bin, uint32_t* out_krem, uint32_t* out_count = nullptr) {
-  constexpr int PER = NBINS / kSelThreads;
+  constexpr int PER = (NBINS + NT - 1) / NT;
+  static_assert(NBINS % PER == 0, "bins split evenly over the threads that hold any");
   uint32_t c[PER];
   uint32_t s = 0;
+  const uint32_t j0 = threadIdx.x * PER;  // this thread's bins: NBINS - 1 - (j0 .. j0 + PER - 1)
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
-    c[p] = ld_acq(&hist[NBINS - 1 - threadIdx.x * PER - p]);
+    c[p] = j0 < NBINS ? ld_acq(&hist[NBINS - 1 - (j0 + p)]) : 0u;
     s += c[p];
   }
   uint32_t total;
-  const uint32_t above = block_exclusive_scan<kSelThreads>(s, lds_scan, &total);
-  if (above < k && k <= above + s) {
+  const uint32_t above = block_exclusive_scan<NT>(s, lds_scan, &total);
+  if (j0 < NBINS && above < k && k <= above + s) {
     uint32_t run = above;
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       if (run < k && k <= run + c[p]) {
-        *out_bin = NBINS - 1 - threadIdx.x * PER - p;
+        *out_bin = NBINS - 1 - (j0 + p);
         *out_krem = k - run;
         if (out_count) *out_count = c[p];
       }
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_write_kernel(const SelArgs a)
 // ---------------------------------------------------------------------
 // One-launch selection (cooperative launch, every block co-resident).
 //
-// Block b owns tile b (kSelThreads * ITEMS tokens, ITEMS consecutive tokens
+// Block b owns tile b (NT * ITEMS tokens, ITEMS consecutive tokens
 // per thread, kept in registers across the grid barriers):
 //   P1  base flags (gap | forced | dilated gap), order keys, the tile's
 //       12-bit first-digit histogram merged into H1; gap / base counts.
@@ -627,21 +630,12 @@ __device__ __forceinline__ uint32_t ld_rlx(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sum over blocks' published values v[0 .. count) (block-wide).
-__device__ uint32_t block_sum_published(const uint32_t* v, uint32_t count, uint32_t* scan) {
-  uint32_t local = 0;
-  for (uint32_t t = threadIdx.x; t < count; t += kSelThreads) local += ld_rlx(&v[t]);
-  uint32_t total;
-  block_exclusive_scan<kSelThreads>(local, scan, &total);
-  return total;
-}
-
 // LDS histogram `h` of NBINS bins: the bin holding the k-th largest
 // (descending) or k-th smallest (ascending) element, and k's rank inside it.
-template <int NBINS, bool DESC>
+template <int NT, int NBINS, bool DESC>
 __device__ void lds_find_bin(const uint32_t* h, uint32_t k, uint32_t* scan, uint32_t* out_bin,
                              uint32_t* out_krem) {
-  constexpr int PER = (NBINS + kSelThreads - 1) / kSelThreads;
+  constexpr int PER = (NBINS + NT - 1) / NT;
   uint32_t c[PER];
   uint32_t s = 0;
 #pragma unroll
@@ -652,7 +646,7 @@ __device__ void lds_find_bin(const uint32_t* h, uint32_t k, uint32_t* scan, uint
     s += c[p];
   }
   uint32_t total;
-  const uint32_t before = block_exclusive_scan<kSelThreads>(s, scan, &total);
+  const uint32_t before = block_exclusive_scan<NT>(s, scan, &total);
   if (before < k && k <= before + s) {
     uint32_t run = before;
 #pragma unroll
@@ -672,6 +666,7 @@ __device__ void lds_find_bin(const uint32_t* h, uint32_t k, uint32_t* scan, uint
 // `prefix`, the key of the k-th largest: radix passes of up to 10 bits.
 // Returns T; *need = k's rank among the candidates equal to T, *ties = their
 // count.
+template <int NT>
 __device__ uint32_t cand_kth_key(const uint32_t* ck, uint32_t cnt, uint32_t prefix, int bits, uint32_t k,
                                  uint32_t* h, uint32_t* scan, uint32_t* sv, uint32_t* need,
                                  uint32_t* ties) {
@@ -681,16 +676,16 @@ __device__ uint32_t cand_kth_key(const uint32_t* ck, uint32_t cnt, uint32_t pref
   while (bits > 0) {
     const int b = bits > 10 ? 10 : bits;
     bits -= b;
-    for (uint32_t j = threadIdx.x; j < (1u << b); j += kSelThreads) h[j] = 0u;
+    for (uint32_t j = threadIdx.x; j < (1u << b); j += NT) h[j] = 0u;
     __syncthreads();
-    for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+    for (uint32_t j = threadIdx.x; j < cnt; j += NT) {
       const uint32_t key = ck[j];
       if ((key >> (bits + b)) == pfx) atomicAdd(&h[(key >> bits) & ((1u << b) - 1u)], 1u);
     }
     __syncthreads();
-    if (b == 10) lds_find_bin<1024, true>(h, want, scan, &sv[0], &sv[1]);
-    else if (b == 9) lds_find_bin<512, true>(h, want, scan, &sv[0], &sv[1]);
-    else lds_find_bin<256, true>(h, want, scan, &sv[0], &sv[1]);  // b <= 8 here
+    if (b == 10) lds_find_bin<NT, 1024, true>(h, want, scan, &sv[0], &sv[1]);
+    else if (b == 9) lds_find_bin<NT, 512, true>(h, want, scan, &sv[0], &sv[1]);
+    else lds_find_bin<NT, 256, true>(h, want, scan, &sv[0], &sv[1]);  // b <= 8 here
     const uint32_t bin = sv[0];
     want = sv[1];
     last = h[bin];
@@ -704,6 +699,7 @@ __device__ uint32_t cand_kth_key(const uint32_t* ck, uint32_t cnt, uint32_t pref
 
 // The `need`-th smallest index among LDS candidates whose key equals T
 // (indices < 2^31 in ci's low bits): radix passes of 11, 10 and 10 bits.
+template <int NT>
 __device__ uint32_t cand_kth_tie_index(const uint32_t* ck, const uint32_t* ci, uint32_t cnt, uint32_t T,
                                        uint32_t need, uint32_t* h, uint32_t* scan, uint32_t* sv) {
   uint32_t pfx = 0;
@@ -713,15 +709,15 @@ __device__ uint32_t cand_kth_tie_index(const uint32_t* ck, const uint32_t* ci, u
   for (int pass = 0; pass < 3; ++pass) {
     const int b = widths[pass];
     const int low = 31 - done - b;
-    for (uint32_t j = threadIdx.x; j < (1u << b); j += kSelThreads) h[j] = 0u;
+    for (uint32_t j = threadIdx.x; j < (1u << b); j += NT) h[j] = 0u;
     __syncthreads();
-    for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+    for (uint32_t j = threadIdx.x; j < cnt; j += NT) {
       const uint32_t idx = ci[j] & 0x7FFFFFFFu;
       if (ck[j] == T && (idx >> (low + b)) == pfx) atomicAdd(&h[(idx >> low) & ((1u << b) - 1u)], 1u);
     }
     __syncthreads();
-    if (b == 11) lds_find_bin<2048, false>(h, want, scan, &sv[0], &sv[1]);
-    else lds_find_bin<1024, false>(h, want, scan, &sv[0], &sv[1]);
+    if (b == 11) lds_find_bin<NT, 2048, false>(h, want, scan, &sv[0], &sv[1]);
+    else lds_find_bin<NT, 1024, false>(h, want, scan, &sv[0], &sv[1]);
     pfx = (pfx << b) | sv[0];
     want = sv[1];
     done += b;
@@ -735,9 +731,10 @@ __device__ uint32_t cand_kth_tie_index(const uint32_t* ck, const uint32_t* ci, u
 // scanning from the top bin down; thread t reads bins [4080 - 16t, 4096 -
 // 16t) as four 16-byte loads. Outputs the bin, k's rank inside it and the
 // bin's count; one block barrier.
+template <int NT>
 __device__ void find_bin_desc_4096(const uint32_t* hist, uint32_t k, uint32_t* lds, uint32_t* out_bin,
                                    uint32_t* out_krem, uint32_t* out_count) {
-  constexpr int PER = 4096 / kSelThreads;  // 16
+  constexpr int PER = 4096 / NT;  // 16 at 256 threads, 4 at 1024
   const uint32_t lo = 4096 - PER * (threadIdx.x + 1);
   uint32_t c[PER];
 #pragma unroll
@@ -769,10 +766,10 @@ __device__ void find_bin_desc_4096(const uint32_t* hist, uint32_t k, uint32_t* l
 }
 
 // Block-wide sums of K values per thread (two barriers, no atomics). `lds`
-// holds K * kSelThreads / 64 words.
-template <int K>
+// holds K * NT / 64 words.
+template <int NT, int K>
 __device__ __forceinline__ void block_sums(uint32_t (&v)[K], uint32_t* lds) {
-  constexpr int NW = kSelThreads / 64;
+  constexpr int NW = NT / 64;
   const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
@@ -794,12 +791,12 @@ __device__ __forceinline__ void block_sums(uint32_t (&v)[K], uint32_t* lds) {
 // the 56 gap flags [i0 - 24, i0 + 32) its thread loads.
 constexpr int kRegDilation = 24;
 
-template <int ITEMS>
-__global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs a) {
-  constexpr uint32_t TILE = kSelThreads * ITEMS;
+template <int ITEMS, int NT>
+__global__ __launch_bounds__(NT) void sel_onepass_kernel(const SelArgs a) {
+  constexpr uint32_t TILE = NT * ITEMS;
   extern __shared__ uint32_t smem[];
-  __shared__ uint32_t scan[16];
-  __shared__ uint32_t red[16];
+  __shared__ uint32_t scan[NT / 64 + 16];
+  __shared__ uint32_t red[4 * NT / 64];
   __shared__ uint32_t sv[4];
   __shared__ uint32_t flag;
   uint32_t* ctrl = a.ws + kCtrl;
@@ -870,16 +867,16 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
     }
   }
 #pragma unroll
-  for (uint32_t q = 0; q < 4096 / (4 * kSelThreads); ++q)
-    reinterpret_cast<uint4*>(hist)[threadIdx.x + q * kSelThreads] = make_uint4(0u, 0u, 0u, 0u);
+  for (uint32_t q = 0; q < 4096 / (4 * NT); ++q)
+    reinterpret_cast<uint4*>(hist)[threadIdx.x + q * NT] = make_uint4(0u, 0u, 0u, 0u);
   if (r > 0 && !reg_dil) {
     const uint32_t W = TILE + 2 * r;
-    for (uint32_t w = threadIdx.x; w < W; w += kSelThreads) {
+    for (uint32_t w = threadIdx.x; w < W; w += NT) {
       const int64_t g = int64_t(tile0) - r + w;
       window[w] = (g >= 0 && g < int64_t(a.n) && a.gap[g]) ? 1u : 0u;
     }
     __syncthreads();
-    const uint32_t per = (W + kSelThreads - 1) / kSelThreads;
+    const uint32_t per = (W + NT - 1) / NT;
     const uint32_t beg = threadIdx.x * per;
     const uint32_t end = min(W, beg + per);
     uint32_t local = 0;
@@ -888,7 +885,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       window[w] = local;
     }
     uint32_t total;
-    const uint32_t excl = block_exclusive_scan<kSelThreads>(local, scan, &total);
+    const uint32_t excl = block_exclusive_scan<NT>(local, scan, &total);
     for (uint32_t w = beg; w < end; ++w) window[w] += excl;
   }
   __syncthreads();
@@ -924,13 +921,13 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
     }
   }
   uint32_t counts[2] = {gap_cnt, base_cnt};
-  block_sums(counts, red);
+  block_sums<NT>(counts, red);
   if (threadIdx.x == 0) {
     if (counts[0]) atomicAdd(&ctrl[C_GAP], counts[0]);
     if (counts[1]) atomicAdd(&ctrl[C_BASE], counts[1]);
     a.tile_base[tile] = counts[1];
   }
-  for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads) {
+  for (uint32_t i = threadIdx.x; i < 4096; i += NT) {
     const uint32_t c = hist[i] + (i == (kKeyNegInf >> 20) ? counts[1] : 0u);
     if (c) atomicAdd(&a.ws[kH1 + i], c);
   }
@@ -958,12 +955,12 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
   if (topk == 0) {
     // only base tokens: the earlier tiles' base counts give the offset
     uint32_t before[1] = {0};
-    for (uint32_t t = threadIdx.x; t < tile; t += kSelThreads) before[0] += a.tile_base[t];
-    block_sums(before, red);
+    for (uint32_t t = threadIdx.x; t < tile; t += NT) before[0] += a.tile_base[t];
+    block_sums<NT>(before, red);
     out_off = before[0];
     if (tile == 0 && threadIdx.x == 0) *a.out_count = bases;
   } else {
-    find_bin_desc_4096(a.ws + kH1, uint32_t(topk), scan, &sv[0], &sv[1], &sv[3]);
+    find_bin_desc_4096<NT>(a.ws + kH1, uint32_t(topk), scan, &sv[0], &sv[1], &sv[3]);
     __syncthreads();
     uint32_t prefix = sv[0];
     uint32_t krem = sv[1];
@@ -973,20 +970,20 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
     if (cnt > kCandCap) {
       // second digit: key[19:8] among keys with key[31:20] == prefix
       __syncthreads();
-      for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads) hist[i] = 0u;
+      for (uint32_t i = threadIdx.x; i < 4096; i += NT) hist[i] = 0u;
       __syncthreads();
 #pragma unroll
       for (int e = 0; e < ITEMS; ++e)
         if (((valid_bits >> e) & 1u) && (key[e] >> 20) == prefix) atomicAdd(&hist[(key[e] >> 8) & 0xFFFu], 1u);
       __syncthreads();
-      for (uint32_t i = threadIdx.x; i < 4096; i += kSelThreads)
+      for (uint32_t i = threadIdx.x; i < 4096; i += NT)
         if (hist[i]) atomicAdd(&a.ws[kH2 + i], hist[i]);
       if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
       __syncthreads();
-      find_bin_desc_4096(a.ws + kH2, krem, scan, &sv[0], &sv[1], &sv[3]);
+      find_bin_desc_4096<NT>(a.ws + kH2, krem, scan, &sv[0], &sv[1], &sv[3]);
       __syncthreads();
       prefix = (prefix << 12) | sv[0];
       krem = sv[1];
@@ -995,19 +992,19 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       if (cnt > kCandCap) {
         // last digit: key[7:0] among keys with key[31:8] == prefix
         __syncthreads();
-        for (uint32_t i = threadIdx.x; i < 256; i += kSelThreads) hist[i] = 0u;
+        for (uint32_t i = threadIdx.x; i < 256; i += NT) hist[i] = 0u;
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < ITEMS; ++e)
           if (((valid_bits >> e) & 1u) && (key[e] >> 8) == prefix) atomicAdd(&hist[key[e] & 0xFFu], 1u);
         __syncthreads();
-        for (uint32_t i = threadIdx.x; i < 256; i += kSelThreads)
+        for (uint32_t i = threadIdx.x; i < 256; i += NT)
           if (hist[i]) atomicAdd(&a.ws[kH3 + i], hist[i]);
         if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
           if (threadIdx.x == 0) *a.out_count = -1;
           return;
         }
-        find_bin_desc<256>(a.ws + kH3, krem, scan, &sv[0], &sv[1]);
+        find_bin_desc<256, NT>(a.ws + kH3, krem, scan, &sv[0], &sv[1]);
         __syncthreads();
         prefix = (prefix << 8) | sv[0];
         krem = sv[1];
@@ -1065,11 +1062,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       // candidates written by every block before the barrier: 16-byte
       // loads, all issued before any is stored (capacity-padded, so a
       // partial last vector stays inside the candidate arrays)
-      constexpr uint32_t kVecPerThread = kCandCap / (4 * kSelThreads);
+      constexpr uint32_t kVecPerThread = kCandCap / (4 * NT);
       uint4 vk[kVecPerThread], vi[kVecPerThread];
 #pragma unroll
       for (uint32_t q = 0; q < kVecPerThread; ++q) {
-        const uint32_t j = 4 * (threadIdx.x + q * kSelThreads);
+        const uint32_t j = 4 * (threadIdx.x + q * NT);
         if (j < cnt) {
           vk[q] = *reinterpret_cast<const uint4*>(a.cand_key + j);
           vi[q] = *reinterpret_cast<const uint4*>(a.cand_idx + j);
@@ -1077,14 +1074,14 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       }
       // the tiles' sure counts, loaded with the candidates
       uint32_t sure_before = 0, sure_all = 0;
-      for (uint32_t t = threadIdx.x; t < ntiles; t += kSelThreads) {
+      for (uint32_t t = threadIdx.x; t < ntiles; t += NT) {
         const uint32_t v = a.tile_sure[t];
         sure_all += v;
         sure_before += t < tile ? v : 0u;
       }
 #pragma unroll
       for (uint32_t q = 0; q < kVecPerThread; ++q) {
-        const uint32_t j = 4 * (threadIdx.x + q * kSelThreads);
+        const uint32_t j = 4 * (threadIdx.x + q * NT);
         if (j < cnt) {
           *reinterpret_cast<uint4*>(ck + j) = vk[q];
           *reinterpret_cast<uint4*>(ci + j) = vi[q];
@@ -1098,11 +1095,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
       // of the keys equal to T
       uint32_t pfx = prefix, want = krem, rest = uint32_t(shift), m = cnt;
       if (rest == 20) {
-        for (uint32_t j = threadIdx.x; j < 2048; j += kSelThreads) h[j] = 0u;
+        for (uint32_t j = threadIdx.x; j < 2048; j += NT) h[j] = 0u;
         __syncthreads();
-        for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) atomicAdd(&h[(ck[j] >> 9) & 2047u], 1u);
+        for (uint32_t j = threadIdx.x; j < cnt; j += NT) atomicAdd(&h[(ck[j] >> 9) & 2047u], 1u);
         __syncthreads();
-        lds_find_bin<2048, true>(h, want, scan, &sv[0], &sv[1]);
+        lds_find_bin<NT, 2048, true>(h, want, scan, &sv[0], &sv[1]);
         m = h[sv[0]];
         pfx = (pfx << 11) | sv[0];
         want = sv[1];
@@ -1114,7 +1111,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         uint32_t* list = h;  // the m candidates sharing the prefix
         if (threadIdx.x == 0) sv[2] = 0;
         __syncthreads();
-        for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+        for (uint32_t j = threadIdx.x; j < cnt; j += NT) {
           if ((ck[j] >> rest) == pfx) {
             const uint32_t slot = atomicAdd(&sv[2], 1u);
             list[2 * slot] = ck[j];
@@ -1143,11 +1140,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         cut = sv[1];
       } else {
         uint32_t need, ties;
-        T = cand_kth_key(ck, cnt, pfx, int(rest), want, h, scan, sv, &need, &ties);
-        cut = need >= ties ? 0x7FFFFFFFu : cand_kth_tie_index(ck, ci, cnt, T, need, h, scan, sv);
+        T = cand_kth_key<NT>(ck, cnt, pfx, int(rest), want, h, scan, sv, &need, &ties);
+        cut = need >= ties ? 0x7FFFFFFFu : cand_kth_tie_index<NT>(ck, ci, cnt, T, need, h, scan, sv);
       }
       uint32_t before = 0, taken = 0;
-      for (uint32_t j = threadIdx.x; j < cnt; j += kSelThreads) {
+      for (uint32_t j = threadIdx.x; j < cnt; j += NT) {
         const uint32_t idx = ci[j] & 0x7FFFFFFFu;
         const bool sel = ck[j] > T || (ck[j] == T && idx <= cut);
         if (sel && !(ci[j] >> 31)) {
@@ -1156,7 +1153,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         }
       }
       uint32_t sums[4] = {taken, before, sure_before, sure_all};
-      block_sums(sums, red);
+      block_sums<NT>(sums, red);
       out_off = sums[2] + sums[1];
       if (tile == 0 && threadIdx.x == 0) *a.out_count = int64_t(sums[3]) + sums[0];
 #pragma unroll
@@ -1178,17 +1175,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         sure += (((base_bits >> e) & 1u) || key[e] > T) ? 1u : 0u;
       }
       uint32_t tile_ties, tile_sure;
-      uint32_t rank = block_exclusive_scan<kSelThreads>(ties, scan, &tile_ties);
-      block_exclusive_scan<kSelThreads>(sure, scan, &tile_sure);
+      uint32_t rank = block_exclusive_scan<NT>(ties, scan, &tile_ties);
+      block_exclusive_scan<NT>(sure, scan, &tile_sure);
       if (threadIdx.x == 0) a.tile_ties[tile] = tile_ties;
       if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
       uint32_t tb = 0;
-      for (uint32_t t = threadIdx.x; t < tile; t += kSelThreads) tb += ld_rlx(&a.tile_ties[t]);
+      for (uint32_t t = threadIdx.x; t < tile; t += NT) tb += ld_rlx(&a.tile_ties[t]);
       uint32_t tie_off;
-      block_exclusive_scan<kSelThreads>(tb, scan, &tie_off);
+      block_exclusive_scan<NT>(tb, scan, &tie_off);
       const int64_t left = int64_t(need) - int64_t(tie_off);
       const uint32_t allow = left <= 0 ? 0u : (left < int64_t(tile_ties) ? uint32_t(left) : tile_ties);
       uint32_t count = 0;
@@ -1206,28 +1203,28 @@ __global__ __launch_bounds__(kSelThreads) void sel_onepass_kernel(const SelArgs 
         }
       }
       uint32_t tile_count;
-      block_exclusive_scan<kSelThreads>(count, scan, &tile_count);
+      block_exclusive_scan<NT>(count, scan, &tile_count);
       if (threadIdx.x == 0) a.tile_cnt[tile] = tile_count;
       if (!grid_barrier(ctrl, ntiles, ++bar_round, a, &flag)) {
         if (threadIdx.x == 0) *a.out_count = -1;
         return;
       }
       uint32_t cb = 0, ca = 0;
-      for (uint32_t t = threadIdx.x; t < ntiles; t += kSelThreads) {
+      for (uint32_t t = threadIdx.x; t < ntiles; t += NT) {
         const uint32_t v = ld_rlx(&a.tile_cnt[t]);
         ca += v;
         cb += t < tile ? v : 0u;
       }
       uint32_t sb, sa;
-      block_exclusive_scan<kSelThreads>(cb, scan, &sb);
-      block_exclusive_scan<kSelThreads>(ca, scan, &sa);
+      block_exclusive_scan<NT>(cb, scan, &sb);
+      block_exclusive_scan<NT>(ca, scan, &sa);
       out_off = sb;
       if (tile == 0 && threadIdx.x == 0) *a.out_count = sa;
     }
   }
   // ------------------------------------------------------------- write
   uint32_t total;
-  uint32_t pos = out_off + block_exclusive_scan<kSelThreads>(__popc(write_bits), scan, &total);
+  uint32_t pos = out_off + block_exclusive_scan<NT>(__popc(write_bits), scan, &total);
 #pragma unroll
   for (int e = 0; e < ITEMS; ++e) {
     if (((write_bits >> e) & 1u) && pos < a.n) a.out_idx[pos++] = int64_t(i0 + e);
@@ -1258,11 +1255,17 @@ int check_select(const float* scores, const uint8_t* gap, int64_t n, int64_t rad
 }
 
 constexpr int kNotLaunched = 1;
+// Threads per block of the one-launch select at 8 tokens per thread: 4096-
+// token tiles, 16 blocks at 64K tokens (38.0 us per K-deviation select
+// against 40.0 at 256 threads and 41.0 at 1024, same box): fewer blocks
+// shorten the histogram merge's contended adds and the barriers' arrival
+// chains, while each thread keeps its 8 tokens.
+constexpr int kOnepassThreads = 512;
 
-// Blocks of sel_onepass_kernel<ITEMS> with `lds` dynamic LDS bytes that the
+// Blocks of sel_onepass_kernel<ITEMS, NT> with `lds` dynamic LDS bytes that the
 // device can hold at once, per device (cached: the occupancy query is a
 // runtime call).
-template <int ITEMS>
+template <int ITEMS, int NT>
 int onepass_capacity(size_t lds, int* capacity) {
   static std::mutex mu;
   static int cached_dev[16] = {};
@@ -1279,7 +1282,7 @@ int onepass_capacity(size_t lds, int* capacity) {
       return CBK_OK;
     }
   int per_cu = 0, cus = 0, coop = 0;
-  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sel_onepass_kernel<ITEMS>, kSelThreads, lds);
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sel_onepass_kernel<ITEMS, NT>, NT, lds);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (err == hipSuccess) err = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
   if (err != hipSuccess) return set_error(CBK_ERR_LAUNCH, "occupancy query: %s", hipGetErrorString(err));
@@ -1294,17 +1297,17 @@ int onepass_capacity(size_t lds, int* capacity) {
 }
 
 // kNotLaunched when the tiles do not fit on the device at once.
-template <int ITEMS>
+template <int ITEMS, int NT>
 int launch_onepass(const SelArgs& a, int64_t n, int64_t radius, hipStream_t stream) {
-  constexpr int64_t tile = int64_t(kSelThreads) * ITEMS;
+  constexpr int64_t tile = int64_t(NT) * ITEMS;
   const int64_t grid = (n + tile - 1) / tile;
   const int64_t p1 = 4096 + tile + 2 * radius + 1;
   const int64_t p3 = 2 * int64_t(kCandCap) + 2048;
   const size_t lds = size_t(p1 > p3 ? p1 : p3) * sizeof(uint32_t);
   int capacity = 0;
-  if (int rc = onepass_capacity<ITEMS>(lds, &capacity)) return rc;
+  if (int rc = onepass_capacity<ITEMS, NT>(lds, &capacity)) return rc;
   if (grid > capacity) return kNotLaunched;
-  hipLaunchKernelGGL(sel_onepass_kernel<ITEMS>, dim3(uint32_t(grid)), dim3(kSelThreads), lds, stream, a);
+  hipLaunchKernelGGL((sel_onepass_kernel<ITEMS, NT>), dim3(uint32_t(grid)), dim3(NT), lds, stream, a);
   return launch_status("select (one launch)");
 }
 
@@ -1349,8 +1352,8 @@ int launch_select(const float* scores, const uint8_t* gap, const uint8_t* forced
   if (!header_zeroed) hipLaunchKernelGGL(sel_zero_kernel, dim3(1), dim3(kSelThreads), 0, stream, a.ws);
   // one launch when every tile's block can be resident at once
   if ((flags & CBK_SELECT_MULTI_LAUNCH) == 0) {
-    int rc = launch_onepass<8>(a, n, radius, stream);
-    if (rc == kNotLaunched) rc = launch_onepass<32>(a, n, radius, stream);
+    int rc = launch_onepass<8, kOnepassThreads>(a, n, radius, stream);
+    if (rc == kNotLaunched) rc = launch_onepass<32, kSelThreads>(a, n, radius, stream);
     if (rc != kNotLaunched) return rc;
   }
   const dim3 grid(L.nblocks), block(kSelThreads);
