@@ -41,7 +41,7 @@ def test_reference_known_answers(golden):
     assert got.tolist() == case["expected"]
 
 
-@pytest.mark.parametrize("n", [1, 2, 7, 1023, 1024, 1025, 4097, 65536, 200000])
+@pytest.mark.parametrize("n", [1, 2, 7, 1023, 1024, 1025, 4095, 4096, 4097, 8193, 65536, 200000])
 def test_select_bit_exact_vs_oracle_random(n):
     rng = np.random.default_rng(n)
     for trial in range(3):
@@ -285,7 +285,8 @@ def test_cpu_plumbing_kdev_leg_exact_zero_ties():
 @pytest.mark.parametrize("n, case", [
     (65536, "one_bin"),        # every key shares the first 12-bit digit: second digit narrows
     (65536, "two_values"),     # two distinct keys: the last digit fixes the k-th key, index ties
-    (1_500_000, "normal"),     # 8192-token tiles
+    (1_500_000, "normal"),     # 4096-token tiles, 367 blocks
+    (3_000_000, "normal"),     # past the 4096-token tiles' capacity: 8192-token tiles
     (5_000_000, "normal"),     # more tiles than fit at once: the multi-launch pipeline
 ])
 def test_select_narrowing_paths_and_sizes(n, case):
