@@ -308,7 +308,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(D =
     const bool valid = r < nrows;
     const uint32_t qi = valid ? r / a.group : 0;
     const uint32_t qh = kvh * a.group + (valid ? r % a.group : 0);
-    rpos[t] = valid ? int32_t(a.pos[qi]) : -1;
+    // a position at or past the context's end sees every key (the last
+    // block's rows past nk repeat its last key and must stay masked)
+    rpos[t] = valid ? int32_t(min(a.pos[qi], int64_t(a.nk) - 1)) : -1;
 #pragma unroll
     for (int st = 0; st < D / 32; ++st) {
       u32x4 w = u32x4(0u);

@@ -194,6 +194,21 @@ def test_blend_attention_partial_key_blocks(nq, nk, d):
     _check(got, _oracle(q, k, v, pos, 0.7, "bf16"), f"nq={q.shape[0]} nk={nk} d={d}")
 
 
+@pytest.mark.parametrize("nk,d", [(31, 128), (33, 64), (97, 128)])
+def test_blend_attention_device_positions_past_the_context(nk, d):
+    """Positions on the device are not checked on the host: one at or past
+    the last key sees every key, as the reference's mask (key <= position
+    over the nk keys) has it -- the last block's rows past nk, which repeat
+    its last key in LDS, stay masked."""
+    hq, hkv = 8, 2
+    q, k, v, _ = _case(6, nk, hq, hkv, d, torch.bfloat16, seed=nk + d)
+    pos = torch.tensor([nk - 1, nk, nk + 5, 1 << 20, 0, nk // 2])
+    got = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), 0.7)
+    _check(got, _oracle(q, k, v, pos, 0.7, "bf16"), f"nk={nk} d={d} positions past the context")
+    same = blend_attention(q.to(DEV), k.to(DEV), v.to(DEV), pos.clamp(max=nk - 1).to(DEV), 0.7)
+    assert torch.equal(got, same)
+
+
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 128), (torch.bfloat16, 64)])
 @pytest.mark.parametrize("slope", [4.0, 2.0])
 def test_blend_attention_rising_row_maxima(dtype, d, slope):
