@@ -310,3 +310,47 @@ def test_select_narrowing_paths_and_sizes(n, case):
         got = S.select(torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV), ratio,
                        torch.from_numpy(forced).to(DEV), radius=radius)
         np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def _fuzz_scores(rng, n, kind):
+    if kind == "normal":
+        return rng.standard_normal(n).astype(np.float32)
+    if kind == "lognormal":
+        return rng.lognormal(0.0, 1.5, n).astype(np.float32)
+    if kind == "few_values":  # masses of exact ties
+        return rng.choice(np.array([0.0, 0.5, 1.0, 2.0], np.float32), n)
+    if kind == "narrow":  # one 12-bit bin, a few 24-bit prefixes
+        return (1.0 + rng.integers(0, 64, n) * 2.0 ** -20).astype(np.float32)
+    s = rng.standard_normal(n).astype(np.float32)  # "specials": -inf, NaN, -0.0, +0.0
+    pick = rng.random(n)
+    s[pick < 0.05] = -np.inf
+    s[(pick >= 0.05) & (pick < 0.07)] = np.nan
+    s[(pick >= 0.07) & (pick < 0.10)] = -0.0
+    s[(pick >= 0.10) & (pick < 0.13)] = 0.0
+    return s
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_select_seeded_random_configurations(seed):
+    """Seeded random selections against the oracle, bit for bit: sizes across
+    the tile and launch-capacity edges, score distributions with ties,
+    -inf, NaN and signed zeros, dilation radii on the register path (<= 24)
+    and the LDS prefix path, forced masks, ratios near 0 and 1."""
+    rng = np.random.default_rng(1000 + seed)
+    sizes = [1, 63, 4095, 4096, 4097, 8191, 8193, 65535, 65536, 65537, 131072, 262143]
+    n = int(sizes[seed % len(sizes)] if seed < 24 else rng.integers(1, 300_000))
+    kind = ["normal", "lognormal", "few_values", "narrow", "specials"][seed % 5]
+    scores = _fuzz_scores(rng, n, kind)
+    gap = rng.random(n) < rng.uniform(0.0, 0.5)
+    forced = (rng.random(n) < rng.uniform(0.0, 0.1)) if seed % 3 else None
+    radius = int([0, 1, 16, 24, 25, 300][seed % 6])
+    ratio = float([0.001, 0.15, 0.5, 0.99, 1.0, rng.uniform(0.0, 1.0)][seed % 6])
+    print(f"seed={seed} n={n} kind={kind} radius={radius} ratio={ratio:.4f} forced={forced is not None}",
+          flush=True)
+    fc = forced
+    if radius:
+        fc = O.dilate(gap, radius) | (forced if forced is not None else False)
+    want = O.select(scores, gap, ratio, fc)
+    got = S.select(torch.from_numpy(scores).to(DEV), torch.from_numpy(gap).to(DEV), ratio,
+                   None if forced is None else torch.from_numpy(forced).to(DEV), radius=radius)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
