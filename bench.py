@@ -1202,7 +1202,7 @@ def cpu_baseline(torch, synthetic):
         "kind": "port",
         "sample": f"4 of 36 layers, 8192-token prompt, gather+scatter with the reference's torch ops "
                   f"(advanced indexing / index_put_), median of {runs} runs",
-        "threads_note": "threads = the host share this process is given (OMP_NUM_THREADS on the GPU box, "
+        "threads_note": "threads = the host share this process is given (OMP_NUM_THREADS where set, "
                         "else its CPU affinity)",
         **host,
         "c1_plumbing_us": round(c1_med * 1e6, 1),

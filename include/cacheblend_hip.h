@@ -28,7 +28,7 @@ typedef void* cbk_stream_t; /* hipStream_t */
 enum {
   CBK_OK = 0,
   CBK_ERR_INVALID = -1,     /* bad argument: shape, stride, alignment, range */
-  CBK_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
+  CBK_ERR_UNSUPPORTED = -2, /* valid request this library does not implement */
   CBK_ERR_LAUNCH = -3,      /* HIP launch/runtime failure */
   CBK_ERR_WORKSPACE = -4    /* workspace too small */
 };

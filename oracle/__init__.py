@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
-checker (or the timed CPU baseline). The product package never imports it.
+reference results are compared against (or the timed CPU baseline). The product
+package never imports it.
 """
 
 from .cacheblend_oracle import *  # noqa: F401,F403

@@ -1,6 +1,6 @@
 """CPU restatement of CacheBlend's KV data-movement and selection semantics.
 
-TEST INFRASTRUCTURE ONLY -- this module is the checker, never the product.
+TEST INFRASTRUCTURE ONLY -- the oracle the tests compare against, never the product.
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import it.
 

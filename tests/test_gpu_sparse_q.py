@@ -1,6 +1,6 @@
 """GPU parity: Sparse-Q attention-mass scores and selection.
 
-Scores must match the oracle within 1e-2 relative (
+Scores must match the oracle within 1e-2 relative (the stated tolerance of the path;
 the observed error is printed and is far smaller). Index sets are compared
 outside an epsilon band around the k-th score: keys whose scores differ from
 the boundary by more than the largest observed score difference must agree.
