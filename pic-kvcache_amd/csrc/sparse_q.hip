@@ -847,7 +847,7 @@ __global__ void sq_zero_kernel(float* p, uint64_t n) {
 constexpr int64_t kMaxHeadDim = 128;
 
 // Key ranges a (query tile, kv head) of rowstats may be split into.
-constexpr uint32_t kMaxRowChunks = 4;
+constexpr uint32_t kMaxRowChunks = 8;
 
 struct SqLayout {
   uint32_t nq_pad, ntiles;
@@ -888,9 +888,10 @@ int device_cus(int* cus) {
 
 // Key ranges per (query tile, kv head) in rowstats: tiles differ in work by
 // their positions (causal), and one workgroup per tile left the latest tiles
-// running alone at the end; with ranges, about three workgroups per resident
-// slot are dispatched in decreasing order of work.
-constexpr uint32_t kRowChunkTarget = 3;  // rowstats workgroups per resident slot (about)
+// running alone at the end; with ranges, about six workgroups per resident
+// slot are dispatched in decreasing order of work (C5, same box: 3.525-3.530
+// ms at 6 ranges against 3.557-3.583 at 3, 3.533 at 8, 3.556-3.579 at 12).
+constexpr uint32_t kRowChunkTarget = 6;  // rowstats workgroups per resident slot (about)
 
 uint32_t row_chunks(uint32_t units, int cus, uint32_t per_cu) {
   const uint32_t slots = per_cu * uint32_t(cus);  // rowstats workgroups resident per CU

@@ -250,18 +250,19 @@ def test_sparse_q_small_contexts(n_active, prefix, d, hq):
     assert abs(float(full.sum()) - rows.numel() * hq) < 1e-3 * rows.numel() * hq
 
 
-@pytest.mark.parametrize("big_key", [260, 330, 400])
+@pytest.mark.parametrize("big_key", [330, 256, 1990])
 def test_sparse_q_rows_far_above_their_first_block(big_key):
     """Row statistics are summed against the first key block of each key
-    range (the row pass splits a tile's blocks into up to 4 ranges); rows
-    with a logit more than 127 (log2 units) above that reference overflow the
-    sum and are recomputed with online maxima. Here one key carries logits
-    ~350 log2 units above every other for a third of the queries (at
-    positions 392-431: 7 key blocks in ranges [0,1) [1,3) [3,5) [5,7)) --
-    inside a range (260), in a range's first block (330), in the last block
-    (400) -- and every score must still match the oracle."""
+    range (the row pass splits a tile's blocks into up to 8 equal ranges:
+    here 3 tiles at positions 1992-2031, 32 blocks each, ranges of 4
+    blocks); rows with a logit more than 127 (log2 units) above that
+    reference overflow the sum and are recomputed with online maxima. One key
+    carries logits ~350 log2 units above every other for a third of the
+    queries -- inside a range (330: block 5 of [4, 8)), at a range's first
+    block (256: block 4), in the last block (1990: block 31 of [28, 32)) --
+    and every score must still match the oracle."""
     g = torch.Generator().manual_seed(7)
-    n_active, prefix, hq, hkv, d = 300, 200, 8, 2, 64
+    n_active, prefix, hq, hkv, d = 300, 1800, 8, 2, 64
     nk = prefix + n_active
     q = torch.randn(n_active, hq, d, generator=g) / d ** 0.5
     k = torch.randn(nk, hkv, d, generator=g) / d ** 0.5
