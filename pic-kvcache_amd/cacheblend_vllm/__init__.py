@@ -7,6 +7,7 @@ Keeps the import paths of the reference vLLM connector package
 * ``cacheblend_vllm.selection``  K-deviation, budgeted top-k, Sparse-Q
 * ``cacheblend_vllm.loader``     PagedBlendLoader (layerwise H2D + scatter)
 * ``cacheblend_vllm.store_path`` the connector's Store-stream save pipeline
+* ``cacheblend_vllm.storage``    LocalPinnedCPUStore (the pinned chunk store)
 
 Every kernel lives in ``libcacheblend_hip.so`` (HIP, gfx950); there is no CPU
 fallback.

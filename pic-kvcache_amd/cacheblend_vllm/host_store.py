@@ -176,6 +176,8 @@ class PinnedChunkStore:
             raise ValueError("max_bytes must be positive")
         self.chunk_size = int(chunk_size)
         self.max_bytes = int(max_bytes)
+        # put_layer's host copies are page-locked (when a GPU runtime is there)
+        self.pin_memory = True
         # called with every layer tensor the store drops (e.g. slab slots)
         # and the GPU events of loads that may still read it (see release)
         self._on_release = on_release
@@ -260,15 +262,16 @@ class PinnedChunkStore:
                 self._drop_if_idle(segment_id, entry)
 
     def put_layer(self, segment_id: SegmentId, layer_id: int, kv: torch.Tensor) -> bool | None:
-        """Copy one layer ``[2, chunk, *row]`` (any device) into fresh pinned
-        host memory and publish it (reference storage.py:78-102)."""
+        """Copy one layer ``[2, chunk, *row]`` (any device) into fresh host
+        memory, page-locked unless ``pin_memory`` is off, and publish it
+        (reference storage.py:78-102)."""
         with self._lock:
             entry = self._entries.get(segment_id)
             if entry is None:
                 raise KeyError(segment_id)
             if not 0 <= layer_id < entry.num_layers:
                 raise ValueError(f"layer {layer_id} is outside [0, {entry.num_layers})")
-        host = torch.empty(kv.shape, dtype=kv.dtype, pin_memory=torch.cuda.is_available())
+        host = torch.empty(kv.shape, dtype=kv.dtype, pin_memory=self.pin_memory and torch.cuda.is_available())
         host.copy_(kv.detach())
         return self.put_layer_host(segment_id, layer_id, host)
 
