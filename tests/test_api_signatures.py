@@ -4,7 +4,7 @@ reference's order (extra parameters come after them, with defaults), and
 what the reference exposes as a property stays a property. The expected
 lists restate the reference's signatures (cacheblend_vllm/kv_layout.py,
 ascend.py, connector.py, config.py, types.py, hashing.py, matcher.py,
-storage.py)."""
+storage.py, registry.py, trace.py)."""
 
 import inspect
 
@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from cacheblend_vllm import attention, config, connector, hashing, kv_layout, loader, matcher, rope
-from cacheblend_vllm import selection, storage, types
+from cacheblend_vllm import registry, selection, storage, trace, types
 
 FUNCTIONS = [
     # kv_layout.py:90, 125
@@ -27,6 +27,11 @@ FUNCTIONS = [
     (hashing.content_hash, ["tokens"]),
     (hashing.rolling_hashes, ["tokens", "window"]),
     (hashing.rolling_hash_values, ["tokens", "window"]),
+    # registry.py:13-41
+    (registry.register_model, ["engine_id", "model"]),
+    (registry.get_model, ["engine_id"]),
+    (registry.unregister_model, ["engine_id"]),
+    (registry.clear_for_test, []),
 ]
 
 METHODS = [
@@ -80,6 +85,10 @@ METHODS = [
     (storage.LocalPinnedCPUStore, "release", ["request_id"]),
     (storage.LocalPinnedCPUStore, "get_layer", ["request_id", "segment", "layer_id"]),
     (storage.LocalPinnedCPUStore, "clear", []),
+    # trace.py
+    (trace.PipelineTracer, "__init__", ["component"]),
+    (trace.PipelineTracer, "emit", ["event", "request_id"]),
+    (trace.PipelineTracer, "close", []),
 ]
 
 CLASS_METHODS = [
@@ -100,6 +109,7 @@ PROPERTIES = [
     (types.BlendPlan, "gap_tokens"),
     (storage.LocalPinnedCPUStore, "current_bytes"),
     (storage.LocalPinnedCPUStore, "committed_entries"),
+    (trace.PipelineTracer, "enabled"),
 ]
 
 
