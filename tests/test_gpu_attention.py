@@ -238,7 +238,7 @@ def test_blend_attention_rising_row_maxima(dtype, d, slope):
     _check(got, _oracle(q, k, v, pos, scale, rounding), f"rising maxima {dtype} d={d} slope={slope}")
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(24))
 def test_blend_attention_random_shapes(seed):
     """Seeded random shapes: 1-200 queries at sorted or unsorted positions
     over 1-1500 keys, 1-8 query heads per KV head, head_dim 64 or 128, bf16
