@@ -14,13 +14,15 @@
 //             apply) in the log2 domain, merged across the 16 lanes that
 //             share a row -> (m, l) per (range, head, query)
 //   merge     the ranges' (m, l) of each row, in range order -> m + log2(l)
-//   colsum    one workgroup per (256-key block, kv head): each wave keeps its
-//             64 keys' K fragments in registers and streams the query tiles
-//             (all G heads staged in LDS), accumulating exp2(x - m - log2 l) per
-//             key column in registers -> partial[kv head][key]; every key is
-//             owned by exactly one wave, so the sum order is fixed and the
-//             result is identical run to run (no float atomics)
-//   gather    out[i] = sum over kv heads (fixed order) of partial[.][idx[i]]
+//   colsum    one workgroup per (256-key block, query-unit range, kv head):
+//             each wave keeps its 64 keys' K fragments in registers and
+//             streams the range's query tiles (all G heads staged in LDS),
+//             accumulating exp2(x - m - log2 l) per key column in registers
+//             -> partial[range][kv head][key]; every (key, range) is owned by
+//             exactly one wave, so the sum order is fixed and the result is
+//             identical run to run (no float atomics)
+//   gather    out[i] = sum over ranges and kv heads (fixed order) of
+//             partial[.][.][idx[i]]
 // MFMA operand layout (checked on gfx950): A[i][k] in lane i + 16*(k/8),
 // element k%8; B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4),
 // register i%4; 32x32x16: A[i][k] in lane i + 32*(k/8), B[k][j] in lane
@@ -73,6 +75,7 @@ struct SqArgs {
   float* partial;         // [hkv][nk]
   uint16_t* qdense;       // [ntiles][hkv][groups][16][D]: query rows in colsum's unit order
   uint32_t nq_pad;
+  uint32_t col_splits;    // query-unit ranges per (key block, kv head) in colsum
 };
 
 __device__ __forceinline__ float round_logit(float x, int mode) {
@@ -625,7 +628,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // (a division by a runtime value runs on the VALU: readfirstlane brings
   // the results back to scalar registers)
   const uint32_t g = __builtin_amdgcn_readfirstlane(blockIdx.x % a.hkv);
-  const int32_t kb0 = __builtin_amdgcn_readfirstlane(int32_t(blockIdx.x / a.hkv) * kKeyBlock2);
+  const uint32_t rest = __builtin_amdgcn_readfirstlane(blockIdx.x / a.hkv);
+  const uint32_t split = __builtin_amdgcn_readfirstlane(rest % a.col_splits);
+  const int32_t kb0 = __builtin_amdgcn_readfirstlane(int32_t(rest / a.col_splits) * kKeyBlock2);
   const int32_t kw0 = kb0 + int32_t(wave) * 16 * kColTiles;
   const uint32_t col = lane & 15, rgrp = lane >> 4;
 
@@ -664,7 +669,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       break;
     }
   }
-  const int32_t nunits = (ntiles - tlo) * int32_t(nchunks);
+  // this workgroup's share of the block's units: range `split` of
+  // col_splits equal ranges, in unit order
+  const uint32_t all_units = uint32_t(ntiles - tlo) * nchunks;
+  const uint32_t u_lo = all_units * split / a.col_splits;
+  const int32_t nunits = int32_t(all_units * (split + 1) / a.col_splits - u_lo);
 
   // Per-lane byte offsets of the requests. A unit's Q rows are contiguous in
   // the dense copy; rows of heads past the group (a partial last chunk) read
@@ -709,14 +718,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     }
   };
   if (nunits > 0) {
-    int32_t qt_c = ntiles - 1, qt_r = ntiles - 1;  // unit it, and the unit requested in iteration it
-    uint32_t hc_c = 0, hc_r = 0;
+    // unit it, and the unit requested in iteration it: unit u of the block
+    // is head chunk u % nchunks of tile ntiles - 1 - u / nchunks
+    int32_t qt_c = ntiles - 1 - int32_t(u_lo / nchunks), qt_r = qt_c;
+    uint32_t hc_c = u_lo % nchunks, hc_r = hc_c;
+    const uint32_t u_last = u_lo + uint32_t(nunits) - 1;  // the range's last unit
+    const int32_t qt_last = ntiles - 1 - int32_t(u_last / nchunks);
+    const uint32_t hc_last = u_last % nchunks;
     auto request_next = [&](int32_t i, auto bc) __attribute__((always_inline)) {
       if (i < nunits) {
         request(qt_r, hc_r, bc);
         next(qt_r, hc_r);
       } else {
-        request(tlo, nchunks - 1, bc);
+        request(qt_last, hc_last, bc);
       }
     };
     request_next(0, std::integral_constant<int, 0>());
@@ -765,7 +779,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     const int32_t key = kw0 + c * 16 + int32_t(col);
-    if (rgrp == 0 && key < int32_t(a.nk)) a.partial[int64_t(g) * a.nk + key] = v;
+    if (rgrp == 0 && key < int32_t(a.nk)) a.partial[(int64_t(split) * a.hkv + g) * a.nk + key] = v;
   }
 }
 
@@ -817,14 +831,16 @@ __global__ __launch_bounds__(kThreads) void sq_colsum_f32_kernel(const SqArgs a)
 
 // ---------------------------------------------------------------- gather
 
-// out / full = the sum over kv heads of the partial column sums, in head order.
+// out / full = the sum over query-unit ranges and kv heads of the partial
+// column sums [splits][hkv][nk], in that order.
 __global__ __launch_bounds__(kThreads) void sq_gather_kernel(const float* partial, uint32_t nk, uint32_t hkv,
-                                                             const int64_t* index, uint32_t n,
+                                                             uint32_t splits, const int64_t* index, uint32_t n,
                                                              float* out, float* full) {
   const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t parts = splits * hkv;
   if (full != nullptr && i < nk) {
     float v = 0.f;
-    for (uint32_t g = 0; g < hkv; ++g) v += partial[int64_t(g) * nk + i];
+    for (uint32_t p = 0; p < parts; ++p) v += partial[int64_t(p) * nk + i];
     full[i] = v;
   }
   if (out != nullptr && i < n) {
@@ -832,7 +848,7 @@ __global__ __launch_bounds__(kThreads) void sq_gather_kernel(const float* partia
     float v = __uint_as_float(0x7fc00000u);
     if (k >= 0 && k < int64_t(nk)) {
       v = 0.f;
-      for (uint32_t g = 0; g < hkv; ++g) v += partial[int64_t(g) * nk + k];
+      for (uint32_t p = 0; p < parts; ++p) v += partial[int64_t(p) * nk + k];
     }
     out[i] = v;
   }
@@ -848,6 +864,8 @@ constexpr int64_t kMaxHeadDim = 128;
 
 // Key ranges a (query tile, kv head) of rowstats may be split into.
 constexpr uint32_t kMaxRowChunks = 8;
+// Query-unit ranges a (key block, kv head) of colsum may be split into.
+constexpr uint32_t kMaxColSplits = 4;
 
 struct SqLayout {
   uint32_t nq_pad, ntiles;
@@ -861,7 +879,7 @@ __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   L.stats = 0;
   L.tiles = (L.stats + uint64_t(hq) * L.nq_pad * 8 + 255) & ~uint64_t(255);
   L.partial = (L.tiles + uint64_t(L.ntiles) * kTileWords * 4 + 255) & ~uint64_t(255);
-  L.qdense = (L.partial + uint64_t(hkv) * nk * 4 + 255) & ~uint64_t(255);
+  L.qdense = (L.partial + uint64_t(kMaxColSplits) * hkv * nk * 4 + 255) & ~uint64_t(255);
   // padded by one unit: a partial head chunk's requests read past its group
   L.chunk_stats = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
   L.bytes = (L.chunk_stats + uint64_t(kMaxRowChunks) * hq * L.nq_pad * 8 + 255) & ~uint64_t(255);
@@ -893,6 +911,19 @@ int device_cus(int* cus) {
 // ms at 6 ranges against 3.557-3.583 at 3, 3.533 at 8, 3.556-3.579 at 12).
 constexpr uint32_t kRowChunkTarget = 6;  // rowstats workgroups per resident slot (about)
 
+// Query-unit ranges per (key block, kv head) in colsum: a block's work is
+// the query units that see it (the earliest blocks: all of them), and the
+// dispatch runs in decreasing order of work; with ranges, about four colsum
+// workgroups per resident slot (three per CU): 2 ranges at C5 (3.521 ->
+// 3.445-3.446 ms same box; 3 ranges 3.444-3.446, 4 ranges 3.449).
+constexpr uint32_t kColSplitTarget = 4;
+
+uint32_t col_splits(uint32_t units, int cus) {
+  const uint32_t slots = 3u * uint32_t(cus);
+  const uint32_t k = units ? (kColSplitTarget * slots + units - 1) / units : 1u;
+  return std::max(1u, std::min(kMaxColSplits, k));
+}
+
 uint32_t row_chunks(uint32_t units, int cus, uint32_t per_cu) {
   const uint32_t slots = per_cu * uint32_t(cus);  // rowstats workgroups resident per CU
   const uint32_t k = units ? (kRowChunkTarget * slots + units - 1) / units : 1u;
@@ -911,12 +942,13 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, pair || (a.groups > 8 && KS == 4) ? 2u : 3u);
   // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
   CBK_REQUIRE(tgroups * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
-                  kblocks * a.hkv * kThreads < (uint64_t(1) << 32) &&
+                  kblocks * a.hkv * kMaxColSplits * kThreads < (uint64_t(1) << 32) &&
                   uint64_t(a.hq) * a.nq_pad < (uint64_t(1) << 32),
               "sparse_q: %llu query tiles x %llu key blocks x %u kv heads exceed one launch",
               (unsigned long long)ntiles, (unsigned long long)kblocks, a.hkv);
+  a.col_splits = col_splits(uint32_t(kblocks * a.hkv), cus);
   const dim3 g1(uint32_t(tgroups * a.hkv * a.row_chunks));
-  const dim3 g2(uint32_t(kblocks * a.hkv));
+  const dim3 g2(uint32_t(kblocks * a.hkv * a.col_splits));
   if (a.groups == 4)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 4)
@@ -1012,6 +1044,7 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
   a.qdense = reinterpret_cast<uint16_t*>(ws + L.qdense);
   a.chunk_stats = reinterpret_cast<float2*>(ws + L.chunk_stats);
   a.row_chunks = 1;
+  a.col_splits = 1;
   a.nq_pad = L.nq_pad;
   if (nq == 0) {
     const uint64_t n = uint64_t(hkv) * nk;
@@ -1046,7 +1079,7 @@ int cbk_sparse_q_scores(const void* q_dev, int64_t q_row_stride_elems, const int
   const uint32_t n = uint32_t(std::max<int64_t>(full_scores_dev ? nk : 0, out_scores_dev ? n_out : 0));
   if (n > 0)
     hipLaunchKernelGGL(sq_gather_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s,
-                       a.partial, a.nk, a.hkv, out_index_dev, uint32_t(out_scores_dev ? n_out : 0),
+                       a.partial, a.nk, a.hkv, a.col_splits, out_index_dev, uint32_t(out_scores_dev ? n_out : 0),
                        out_scores_dev, full_scores_dev);
   return launch_status("sparse_q gather");
 }
