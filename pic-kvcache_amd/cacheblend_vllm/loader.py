@@ -40,7 +40,7 @@ from .config import CacheBlendConfig, load_staging_layers
 from .kv_layout import kv_desc, kv_planes
 from .rope import cos_sin_table, rope_style
 from .streams import COPY, LOAD, side_stream
-from .trace import PipelineTracer
+from .trace import PipelineTracer, roctx_phase
 from .types import BlendPlan
 
 SRC_ZERO = -1
@@ -401,6 +401,7 @@ class PagedBlendLoader:
 
     # ----------------------------------------------------------- protocol
 
+    @roctx_phase("cacheblend.prefetch")
     def prefetch(self, layer_id: int, rotary_emb) -> None:
         """Enqueue layer ``layer_id``'s load (reference ascend.py:224-278)."""
         if layer_id in self._buffers or layer_id >= len(self.kv_caches):
@@ -476,6 +477,7 @@ class PagedBlendLoader:
             )
         return self._buffers.pop(layer_id)
 
+    @roctx_phase("cacheblend.commit")
     def commit(self, layer_id: int, contiguous: torch.Tensor) -> None:
         """Scatter ``contiguous[:, apc:]`` into the layer's vLLM pages through
         ``slot_mapping[apc:]`` (ascend.py:385-407); APC pages are untouched."""

@@ -24,6 +24,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _native
+from .trace import roctx_phase
 from .config import CacheBlendConfig
 from .kv_layout import write_rows
 
@@ -417,6 +418,7 @@ class BlendSelector:
         scores, forced, stats = self._sparse_q_scores(query, score_keys, absolute_indices, gap_mask, scale)
         return self._select(scores, gap_mask, layer_id, forced_mask=forced), stats
 
+    @roctx_phase("cacheblend.check_layer")
     def check_layer(
         self,
         q: torch.Tensor,

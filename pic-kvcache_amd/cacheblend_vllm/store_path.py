@@ -49,7 +49,7 @@ import torch
 from . import _native
 from .kv_layout import gather_paged_kv, kv_desc, kv_planes
 from .streams import STORE, STORE_COPY, side_stream
-from .trace import PipelineTracer
+from .trace import PipelineTracer, roctx_phase
 from .types import BlendPlan, SegmentId
 
 
@@ -277,6 +277,7 @@ class StoreStreamWriter:
 
     # ------------------------------------------------------------- save
 
+    @roctx_phase("cacheblend.save_layer")
     def save_layer(self, layer_id: int, kv_layer: Any, requests: list[RequestMetadata]) -> None:
         """The per-request body of save_kv_layer (reference connector.py:308-361)."""
         for request in requests:
@@ -521,6 +522,7 @@ class StoreStreamWriter:
             )
         return committed
 
+    @roctx_phase("cacheblend.wait_for_save")
     def wait_for_save(self) -> None:
         """The save boundary (reference connector.py:504-534): drain the Store
         stream, then every publication enqueued so far; stagings are freed

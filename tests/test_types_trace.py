@@ -109,3 +109,32 @@ def test_trace_appends_across_tracers(monkeypatch, tmp_path):
     (path,) = tmp_path.iterdir()
     assert [json.loads(s)["event"] for s in path.read_text().splitlines()] == \
         ["trace_started", "x", "trace_started", "x"]
+
+
+def test_roctx_ranges_are_opt_in(monkeypatch):
+    """Without CACHEBLEND_ROCTX the phase decorators and roctx_range touch no
+    profiler API; with it, each call sits inside one push/pop pair."""
+    import torch
+
+    from cacheblend_vllm import trace
+
+    calls = []
+    monkeypatch.setattr(torch.cuda.nvtx, "range_push", lambda name: calls.append(("push", name)))
+    monkeypatch.setattr(torch.cuda.nvtx, "range_pop", lambda: calls.append(("pop",)))
+
+    @trace.roctx_phase("phase")
+    def work(x, *, y=1):
+        calls.append(("work", x, y))
+        return x + y
+
+    monkeypatch.setattr(trace, "_roctx_on", False)
+    assert work(2, y=3) == 5
+    with trace.roctx_range("r"):
+        pass
+    assert calls == [("work", 2, 3)]
+    calls.clear()
+    monkeypatch.setattr(trace, "_roctx_on", True)
+    assert work(1) == 2
+    with trace.roctx_range("r"):
+        calls.append(("inside",))
+    assert calls == [("push", "phase"), ("work", 1, 1), ("pop",), ("push", "r"), ("inside",), ("pop",)]
