@@ -514,11 +514,11 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     8192-token prompt (32 chunks of 256) through the Store stream, timed from
     the first save to the end of wait_for_save (publication of every chunk
     into the host store included), in three modes:
-    host_write -- (default) pinned slab slots allocated as consecutive runs,
-                  written by the gather kernel directly over the host link;
-    dma        -- the same slots; gather into a chunk-major device staging,
-                  then (copier thread, Copy stream) one hipMemcpyAsync per
-                  run of slots;
+    host_write -- pinned slab slots allocated as consecutive runs, written by
+                  the gather kernel directly over the host link;
+    dma        -- (the writer's default) the same slots; gather into a
+                  chunk-major device staging, then (copier thread, Copy
+                  stream) one copy command per run of slots;
     reference  -- gather into device staging + one D2H into a freshly pinned
                   per-layer batch (the reference's scheme).
     Also timed with the saves interleaved with bf16 GEMMs on the serving
