@@ -54,6 +54,9 @@ def parse_args():
     p.add_argument("--skip-extras", action="store_true", help="only the headline copy step")
     p.add_argument("--profile", action="store_true",
                    help="run each kernel --steps times and exit (for rocprofv3 runs)")
+    p.add_argument("--profile-store", action="store_true",
+                   help="run the 36-layer store pipeline (dma mode) 4 times and exit "
+                        "(for rocprofv3 timeline runs; CACHEBLEND_ROCTX=1 marks its phases)")
     return p.parse_args()
 
 
@@ -145,6 +148,8 @@ def main() -> int:
 
     if args.profile:
         return profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev)
+    if args.profile_store:
+        return profile_store_run(torch, layers, cache, src_slots)
 
     # correctness guard on the real workload before timing: round trip
     step()
@@ -884,6 +889,49 @@ def blend_load(torch, synthetic, dev, args):
                              "plain_copy_same_bytes_GBps": round(ceiling, 1),
                              "frac_of_same_size_copy": round(gb / ceiling, 4)}
     return out
+
+
+def profile_store_run(torch, layers, cache, src_slots) -> int:
+    """The Qwen3-8B layerwise store of ``store_pipeline`` in its default dma
+    mode, 4 repetitions (the first pins the slab's arenas and warms the
+    pools), each from the first save_layer to the end of wait_for_save; the
+    stored chunks of the last repetition are checked against a gather."""
+    from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
+    from cacheblend_vllm.kv_layout import gather_paged_kv
+    from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
+    from cacheblend_vllm.types import BlendSegment
+
+    L, T = len(layers), src_slots.numel()
+    H, D = cache.row_shape
+    slots_cpu = src_slots.cpu()
+    nbytes = L * 2 * T * H * D * 2
+    slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=128)
+    for rep in range(4):
+        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free)
+        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2, slab=slab)
+        request = RequestMetadata(f"p{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None, True, T)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for l in range(L):
+            writer.save_layer(l, layers[l], [request])
+        writer.wait_for_save()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        log(f"store pipeline rep {rep}: {elapsed * 1e3:.3f} ms, {nbytes / elapsed / 1e9:.2f} GB/s")
+        if rep == 3:
+            segments = [BlendSegment(sid, start) for start, sid in writer._chunk_ids[request.request_id]]
+            store.pin("check", segments)
+            for l in (0, L - 1):
+                want = gather_paged_kv(layers[l], src_slots, cache.block_size).cpu()
+                for seg in segments:
+                    got = store.get_layer("check", seg, l)
+                    if not torch.equal(got, want[:, seg.target_start:seg.target_start + 256]):
+                        log(f"stored chunk at {seg.target_start} of layer {l} differs from the gather")
+                        return 1
+            store.release("check")
+        writer.close()
+        store.clear()
+    return 0
 
 
 def profile_run(torch, S, synthetic, cache, src_slots, dst_slots, staging, args, dev):
