@@ -54,6 +54,24 @@ def test_noalloc_select_matches_workspace_entry_point():
         assert bool(gap[got_idx].sum() == gap.sum())   # every gap token is selected
 
 
+def test_noalloc_select_at_its_maximum_size():
+    """Exactly the largest accepted span (the static scratch's whole layout in
+    use; one head of 8 dims keeps the inputs at 16 MB), then a smaller call
+    on the same scratch: both equal the workspace entry point bit for bit."""
+    lib = _native.load()
+    for n, seed in ((MAX_TOKENS, 5), (4097, 6)):
+        print(f"noalloc kdev select n={n} seed={seed}", flush=True)
+        fresh, cached, gap = synthetic.kdev_inputs(n, 1, 8, torch.bfloat16, DEV, seed=seed)
+        gap_u8 = gap.view(torch.uint8)
+        workspace = torch.empty(lib.cbk_select_workspace_bytes(n), dtype=torch.uint8, device=DEV)
+        want_scores, want_idx, want_k = _call(lib, fresh, cached, gap_u8, 0.15, 16, workspace)
+        got_scores, got_idx, got_k = _call(lib, fresh, cached, gap_u8, 0.15, 16)
+        assert torch.equal(got_scores.view(torch.int32), want_scores.view(torch.int32))
+        assert got_k == want_k > 0
+        assert torch.equal(got_idx, want_idx)
+        assert bool(gap[got_idx].sum() == gap.sum())
+
+
 def test_noalloc_select_rejects_sizes_beyond_its_scratch():
     lib = _native.load()
     tiny = torch.zeros(8, dtype=torch.uint8, device=DEV)
