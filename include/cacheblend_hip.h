@@ -189,7 +189,9 @@ int cbk_stream_destroy(cbk_stream_t stream);
  * connector.py:425-429). Consecutive runs are folded into as few DMA
  * commands as their addresses allow: runs adjacent in dst and in src into
  * one hipMemcpyAsync, runs of one size at constant dst and src pitches
- * into one hipMemcpy2DAsync.
+ * into one hipMemcpy2DAsync. A folded command whose runs lie in different
+ * allocations (addresses that only happen to line up) is rejected by the
+ * runtime before anything is enqueued; its runs are then issued one by one.
  */
 int cbk_memcpy_runs(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int64_t n,
                     cbk_stream_t stream);

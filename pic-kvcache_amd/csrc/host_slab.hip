@@ -249,10 +249,24 @@ int cbk_memcpy_runs(const uint64_t* dst, const uint64_t* src, const uint64_t* by
     const int64_t covered = next_command(dst, src, bytes, n, i, &c);
     void* d = reinterpret_cast<void*>(c.dst);
     const void* from = reinterpret_cast<const void*>(c.src);
-    const hipError_t err = c.rows == 1
-                               ? hipMemcpyAsync(d, from, size_t(c.width), hipMemcpyDefault, s)
-                               : hipMemcpy2DAsync(d, size_t(c.dpitch), from, size_t(c.spitch), size_t(c.width),
-                                                  size_t(c.rows), hipMemcpyDefault, s);
+    hipError_t err = c.rows == 1
+                         ? hipMemcpyAsync(d, from, size_t(c.width), hipMemcpyDefault, s)
+                         : hipMemcpy2DAsync(d, size_t(c.dpitch), from, size_t(c.spitch), size_t(c.width),
+                                            size_t(c.rows), hipMemcpyDefault, s);
+    if (err == hipErrorInvalidValue && covered > 1) {
+      // Folded runs can lie in different allocations whose addresses merely
+      // happen to line up (two pinned tensors, two slab arenas); the runtime
+      // checks a command's whole extent against one allocation and rejects
+      // it before enqueueing anything. Each run lies in one allocation, so
+      // the group goes out run by run.
+      (void)hipGetLastError();
+      err = hipSuccess;
+      for (int64_t j = i; j < i + covered && err == hipSuccess; ++j) {
+        if (bytes[j] == 0) continue;
+        err = hipMemcpyAsync(reinterpret_cast<void*>(dst[j]), reinterpret_cast<const void*>(src[j]),
+                             size_t(bytes[j]), hipMemcpyDefault, s);
+      }
+    }
     if (err != hipSuccess)
       return cbk::set_error(CBK_ERR_LAUNCH, "copy of runs %lld..%lld: %s", (long long)i,
                             (long long)(i + covered - 1), hipGetErrorString(err));

@@ -237,6 +237,67 @@ def test_loader_dma_ring_wraps_bit_exact(ring_slots):
     assert loader._hit_ring.shape[0] == min(ring_slots, L) and not loader._zc_layers
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_loader_random_plans_bit_exact_vs_oracle(seed):
+    """Seeded random blend plans over two layers: block sizes 8-32, head
+    shapes (the 80-dim per-pair path included), chunk sizes 16-64, an APC
+    prefix of 0-3 blocks, 1-5 segments with 0-69-token gaps, an allocation
+    end not aligned to the block size, RoPE relocation (NeoX or interleaved)
+    in bf16 and float32 and bit copies in f16, every transfer mode. Each
+    assembled buffer and the pages after each commit equal the oracle's."""
+    rng = np.random.default_rng(1000 + seed)
+    bs = int(rng.choice([8, 16, 32]))
+    heads, dim = [(1, 64), (2, 128), (4, 128), (8, 64), (3, 80)][int(rng.integers(5))]
+    dtype = [torch.bfloat16, torch.float32, torch.float16][int(rng.integers(3))]
+    chunk = int(rng.choice([16, 32, 64]))
+    moved = dtype != torch.float16 and rng.random() < 0.8
+    neox = bool(rng.integers(2))
+    zero_copy = ["auto", True, False][int(rng.integers(3))]
+    apc = int(rng.integers(0, 3 * bs + 1))
+    segs, pos = [], apc
+    for _ in range(int(rng.integers(1, 6))):
+        pos += int(rng.integers(0, 70))
+        n = chunk * int(rng.integers(1, 5))
+        segs.append((int(rng.integers(0, 600)) if moved else pos, pos, n))
+        pos += n
+    alloc_end = pos + int(rng.integers(0, 2 * bs + 2))
+    nb = (alloc_end + bs - 1) // bs + 8
+    print(f"seed={seed} bs={bs} heads={heads} dim={dim} {dtype} chunk={chunk} moved={moved} neox={neox} "
+          f"zero_copy={zero_copy} apc={apc} segs={segs} alloc_end={alloc_end}", flush=True)
+    layers, store, plan, slots, hosts = _blend_setup(2, nb, bs, heads, dim, apc, segs, alloc_end, dtype,
+                                                     chunk, seed=seed)
+    rope = Rope(dim, 2048, neox)
+    cache = rope.cos_sin_cache.cpu().numpy()
+
+    def reloc(old, new, k_bits):
+        if dtype == torch.bfloat16:
+            k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
+            out = O.relocate_key(cache, old, new, k, dim, neox, bf16=True)
+            return O.f32_to_bf16(out).reshape(k_bits.shape)
+        k = k_bits.reshape(k_bits.shape[0], -1)
+        return O.relocate_key(cache, old, new, k, dim, neox, bf16=False).reshape(k_bits.shape)
+
+    loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk),
+                              zero_copy=zero_copy)
+    loader.prefetch(0, rope)
+    for l in range(2):
+        buf = loader.get(l)
+        loader.prefetch(l + 1, rope)
+        want = O.loader_assemble(
+            _bits(layers[l]), slots.numpy(), bs, apc, alloc_end,
+            [(s, t, _bits(hosts[i, l])) for i, (s, t, _) in enumerate(segs)],
+            relocate=reloc if moved else None,
+        )
+        np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
+        expect_pages = _bits(layers[l]).copy()
+        fresh = torch.randn(buf.shape, dtype=torch.float32).to(dtype).to(DEV)
+        O.loader_commit(_bits(fresh), expect_pages, slots.numpy(), bs, apc, alloc_end)
+        buf.copy_(fresh)
+        loader.commit(l, buf)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_bits(layers[l]), expect_pages, err_msg=f"commit layer {l}")
+
+
 def test_loader_without_relocation_is_a_bit_copy():
     heads, dim, bs, chunk = 2, 64, 16, 32
     segs = [(40, 40, 64), (200, 200, 32)]  # source == target

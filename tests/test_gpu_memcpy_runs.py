@@ -120,6 +120,44 @@ def test_memcpy_runs_on_slab_memory(direction):
         slab.close()
 
 
+@pytest.mark.parametrize("direction", ["h2d", "d2h"])
+def test_memcpy_runs_group_across_two_allocations(direction):
+    """Two equal runs whose host sides are two separate pinned allocations
+    (slab arenas of one slot each) at a pitch that merely lines up, their
+    device sides adjacent: the planner folds them into one 2D command, which
+    the runtime rejects for reaching across allocations; the runs then go out
+    one by one, and every byte arrives."""
+    w = 4096
+    slab = PinnedChunkSlab((w,), torch.uint8, chunks_per_arena=1)
+    try:
+        (first,) = slab.alloc_run(1)
+        (second,) = slab.alloc_run(1)
+        lo, hi = sorted((first, second), key=lambda t: t.data_ptr())
+        if not w <= hi.data_ptr() - lo.data_ptr() <= (1 << 31):
+            pytest.skip("the two arenas are not at a foldable pitch on this box")
+        dev = torch.empty(2 * w, dtype=torch.uint8, device="cuda")
+        rng = np.random.default_rng(3)
+        host_addr = np.array([lo.data_ptr(), hi.data_ptr()], dtype=np.uint64)
+        dev_addr = np.array([dev.data_ptr(), dev.data_ptr() + w], dtype=np.uint64)
+        sizes = np.full(2, w, dtype=np.uint64)
+        if direction == "h2d":
+            for t in (lo, hi):
+                t.copy_(torch.from_numpy(rng.integers(0, 256, w, dtype=np.uint8)))
+            dst, src = dev_addr, host_addr
+        else:
+            dev.copy_(torch.from_numpy(rng.integers(0, 256, 2 * w, dtype=np.uint8)))
+            dst, src = host_addr, dev_addr
+        assert _native.memcpy_commands(dst, src, sizes) == 1
+        stream = torch.cuda.current_stream()
+        _native.memcpy_runs(dst, src, sizes, stream.cuda_stream, "runs across two allocations")
+        torch.cuda.synchronize()
+        assert torch.equal(dev.cpu(), torch.cat((lo, hi)))
+        slab.free(first)
+        slab.free(second)
+    finally:
+        slab.close()
+
+
 def test_memcpy_runs_rejects_bad_tables():
     with pytest.raises(ValueError, match="NULL"):
         _native.memcpy_runs(np.array([0], np.uint64), np.array([64], np.uint64), np.array([8], np.uint64),
