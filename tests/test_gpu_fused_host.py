@@ -75,6 +75,80 @@ def test_slab_runs_are_consecutive_and_fall_back_when_fragmented():
     slab.close()
 
 
+def _raw(t):
+    t = t.detach().cpu()
+    return t.view(torch.int32).numpy() if t.dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_store_random_requests_bit_exact(seed):
+    """Seeded random stores over two layers: block sizes 8-32, head shapes
+    (80-dim rows included), bf16 / f16 / float32, chunk sizes 16-128, both
+    page layouts, every transfer mode (slab by DMA, slab written by the
+    gather, the reference's per-layer pinned batch), slab arenas of 1-5 slots
+    (runs broken at arena ends). Three requests per save: A, then B sharing
+    A's first chunks (same tokens at the same positions: those are stored
+    once, so B's pending chunks are a subset) and its own after them, then C;
+    each request's last partial chunk is not stored. Every stored chunk
+    equals the oracle's gather from the request that stored it."""
+    rng = np.random.default_rng(2000 + seed)
+    L = 2
+    bs = int(rng.choice([8, 16, 32]))
+    H, D = [(1, 64), (2, 128), (4, 128), (8, 128), (3, 80)][int(rng.integers(5))]
+    dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+    CH = int(rng.choice([16, 32, 64, 128]))
+    transfer = ["dma", "host_write", None][int(rng.integers(3))]
+    layout = ["merged_first", "merged_block"][int(rng.integers(2))]
+    per_arena = int(rng.integers(1, 6))
+    workgroups = int(rng.choice([16, 64, 256]))
+    na = CH * int(rng.integers(1, 5)) + int(rng.integers(0, CH))
+    shared = int(rng.integers(0, na // CH + 1))  # full chunks of A that B repeats
+    nb_ = shared * CH + CH * int(rng.integers(0, 4)) + int(rng.integers(0, CH))
+    nc = int(rng.integers(0, 4 * CH))
+    base = 100_000 * (seed + 1)
+    tokens = {"A": list(range(base, base + na)),
+              "B": list(range(base, base + shared * CH)) + list(range(base + 50_000, base + 50_000 + nb_ - shared * CH)),
+              "C": list(range(base + 80_000, base + 80_000 + nc))}
+    blocks = {r: (len(t) + bs - 1) // bs for r, t in tokens.items()}
+    NB = sum(blocks.values()) + 8
+    print(f"seed={seed} bs={bs} H={H} D={D} {dtype} CH={CH} transfer={transfer} layout={layout} "
+          f"per_arena={per_arena} workgroups={workgroups} tokens A={na} B={nb_} (shared {shared}) C={nc}",
+          flush=True)
+    pools = [synthetic.paged_pool(NB, bs, H, D, dtype, DEV, seed=60 + seed + l) for l in range(L)]
+    layers = pools if layout == "merged_first" else [p.transpose(0, 1).contiguous() for p in pools]
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(seed))
+    slots, b0 = {}, 0
+    for r in ("A", "B", "C"):
+        slots[r] = synthetic.block_slots(perm[b0:b0 + blocks[r]], bs, len(tokens[r]))
+        b0 += blocks[r]
+    slab = None if transfer is None else PinnedChunkSlab((2, CH, H, D), dtype, chunks_per_arena=per_arena)
+    store = PinnedChunkStore(CH, 1 << 34, on_release=None if slab is None else slab.free)
+    writer = StoreStreamWriter(store, bs, CH, L, "m", slab=slab, max_workgroups=workgroups,
+                               slab_transfer=transfer or "dma")
+    requests = [RequestMetadata(r, tokens[r], slots[r], None, True, len(tokens[r])) for r in ("A", "B", "C")]
+    for l in range(L):
+        writer.save_layer(l, layers[l], requests)
+    writer.wait_for_save()
+    want = {}  # segment id -> (request, start) of the request that stored it
+    for r in ("A", "B", "C"):
+        starts = [s for s, _ in writer._chunk_ids.get(r, [])]
+        assert starts == list(range(0, len(tokens[r]) // CH * CH, CH)), r
+        for start, sid in writer._chunk_ids.get(r, []):
+            want.setdefault(sid, (r, start))
+    assert len(want) == na // CH + nb_ // CH - shared + nc // CH
+    for sid, (r, start) in want.items():
+        assert store.is_committed(sid)
+        for l in range(L):
+            expect = O.gather_paged_kv(_raw(pools[l]), slots[r][start:start + CH].numpy(), bs)
+            np.testing.assert_array_equal(_raw(store._entries[sid].layers[l]), expect,
+                                          err_msg=f"request {r} chunk {start} layer {l}")
+    store.clear()
+    writer.close()
+    if slab is not None:
+        assert slab.stats()["live"] == 0
+        slab.close()
+
+
 @pytest.mark.parametrize("transfer", ["dma", "host_write"])
 @pytest.mark.parametrize("layout", ["merged_first", "merged_block"])
 def test_fused_store_writes_chunks_bit_exact(layout, transfer):
