@@ -124,6 +124,72 @@ def test_check_layer_sparse_q_overwrites_and_selects(strategy, tmp_path, monkeyp
             assert done[key] == res.sparse_q_stats[key], key
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_check_layer_random_configurations(seed):
+    """Seeded random check layers: 1-8 query heads per KV head over 1-4 KV
+    heads, head_dim 64 or 128, 1-2000 active tokens at sorted random
+    positions of a larger context, gap layouts (none: the tail fallback),
+    ratios 0.05-0.6, block sizes 8 / 16 / 32, overflow radii of 0-2 blocks,
+    every strategy. K-deviation sets equal the oracle's; Sparse-Q sets
+    agree outside the epsilon band of the k-th score; the Sparse-Q strategy
+    writes the fresh K rows into the cache (compare leaves it alone)."""
+    rng = np.random.default_rng(3000 + seed)
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 4, 8]))
+    d = int(rng.choice([64, 128]))
+    n = int(rng.integers(1, 2001))
+    nk = n + int(rng.integers(0, 1500))
+    absolute = np.sort(rng.choice(nk, n, replace=False))
+    if rng.random() < 0.25:
+        gap = np.zeros(n, dtype=bool)
+    else:
+        gap = synthetic.gap_layout(n, seed, hit_chunk=int(rng.choice([16, 64])), max_hit_chunks=4, max_gap=40)
+    strategy = ["kv_deviation", "sparse_q", "compare"][int(rng.integers(3))]
+    ratio = float(rng.uniform(0.05, 0.6))
+    bs = int(rng.choice([8, 16, 32]))
+    overflow = int(rng.integers(0, 3))
+    tail = int(rng.integers(1, 100))
+    scale = d ** -0.5
+    print(f"seed={seed} hq={hq} hkv={hkv} d={d} n={n} nk={nk} gaps={int(gap.sum())} {strategy} "
+          f"ratio={ratio:.3f} bs={bs} overflow={overflow} tail={tail}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    old = (torch.randn(nk, hkv * d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    abs_t = torch.from_numpy(absolute)
+    noise = 0.02 * torch.exp(torch.randn(n, 1, generator=g)) * torch.randn(n, hkv * d, generator=g)
+    k = (old[abs_t].float() + noise / d ** 0.5).to(torch.bfloat16)
+    q = (torch.randn(n, hq * d, generator=g) / d ** 0.5).to(torch.bfloat16)
+    config = CacheBlendConfig.from_extra_config({
+        "check_layers": [1], "recompute_ratios": [ratio], "overflow_blocks": overflow,
+        "tail_query_tokens": tail,
+        "selection_strategy": "kv_deviation" if strategy == "kv_deviation" else "sparse_q"})
+    old_dev = old.to(DEV)
+    res = BlendSelector(config, bs).check_layer(
+        q.to(DEV), k.to(DEV), old_dev, abs_t.to(DEV), torch.from_numpy(gap).to(DEV), 1, scale, hq, hkv, d,
+        strategy=strategy)
+    if strategy in ("kv_deviation", "compare"):
+        want = O.select(O.kdev_scores(k.float().numpy(), old.float().numpy()[absolute]), gap, ratio)
+        np.testing.assert_array_equal(res.deviation_selected.cpu().numpy(), want)
+    if strategy == "kv_deviation":
+        return
+    score_keys = old.clone()
+    score_keys[abs_t] = k
+    np.testing.assert_array_equal(_bits(old_dev), _bits(score_keys if strategy == "sparse_q" else old))
+    scores, forced, stats = O.sparse_q_scores(
+        q.float().numpy().reshape(n, hq, d), score_keys.float().numpy().reshape(nk, hkv, d), absolute, gap,
+        scale, block_size=bs, overflow_blocks=overflow, tail_query_tokens=tail, round_logits_bf16=True)
+    for key in ("sparse_query_tokens", "tail_fallback", "gap_tokens"):
+        assert res.sparse_q_stats[key] == stats[key]
+    got = set(res.sparse_q_selected.cpu().tolist())
+    want = set(O.select(scores, gap, ratio, forced).tolist())
+    base = gap | forced
+    disagree = np.array(sorted(got ^ want), dtype=np.int64)
+    if disagree.size:
+        kb = O.select_budget(n, int(gap.sum()), int(base.sum()), ratio)
+        kth = np.sort(scores[~base])[::-1][kb - 1]
+        band = np.abs(scores - kth) <= 1e-2 * abs(kth)
+        assert np.all(band[disagree]), disagree[:10]
+
+
 def test_k_only_gather_through_row_table():
     import ctypes
 
