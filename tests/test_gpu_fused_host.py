@@ -9,6 +9,7 @@ import oracle as O
 from cacheblend_vllm import _native, synthetic
 from cacheblend_vllm.config import CacheBlendConfig
 from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
+from cacheblend_vllm.kv_layout import scatter_chunks
 from cacheblend_vllm.loader import PagedBlendLoader
 from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
 from cacheblend_vllm.types import BlendPlan, BlendSegment
@@ -90,7 +91,9 @@ def test_store_random_requests_bit_exact(seed):
     A's first chunks (same tokens at the same positions: those are stored
     once, so B's pending chunks are a subset) and its own after them, then C;
     each request's last partial chunk is not stored. Every stored chunk
-    equals the oracle's gather from the request that stored it."""
+    equals the oracle's gather from the request that stored it, and A's
+    chunks, reloaded in place from the store into fresh random blocks,
+    equal the oracle's scatter."""
     rng = np.random.default_rng(2000 + seed)
     L = 2
     bs = int(rng.choice([8, 16, 32]))
@@ -142,6 +145,19 @@ def test_store_random_requests_bit_exact(seed):
             expect = O.gather_paged_kv(_raw(pools[l]), slots[r][start:start + CH].numpy(), bs)
             np.testing.assert_array_equal(_raw(store._entries[sid].layers[l]), expect,
                                           err_msg=f"request {r} chunk {start} layer {l}")
+    # reload: A's stored chunks, read in place from the store, into fresh
+    # random blocks of another pool
+    a_ids = [sid for _, sid in writer._chunk_ids.get("A", [])]
+    if a_ids:
+        chunks = [store._entries[sid].layers[1] for sid in a_ids]
+        fresh = synthetic.paged_pool(NB, bs, H, D, dtype, DEV, seed=90 + seed)
+        new_slots = synthetic.block_slots(torch.randperm(NB, generator=torch.Generator().manual_seed(seed + 7))
+                                          [: (len(a_ids) * CH + bs - 1) // bs], bs, len(a_ids) * CH)
+        expect_pool = _raw(fresh).copy()
+        O.scatter_paged_kv(np.concatenate([_raw(c) for c in chunks], axis=1), expect_pool, new_slots.numpy(), bs)
+        scatter_chunks(chunks, fresh, new_slots.to(DEV), bs)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_raw(fresh), expect_pool, err_msg="reload of A's chunks")
     store.clear()
     writer.close()
     if slab is not None:
