@@ -152,6 +152,78 @@ def test_connector_drop_in_save_then_blend_load(monkeypatch, tmp_path):
         assert name in events, name
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_connector_random_reuse(seed):
+    """Seeded random reuse through the connector: two saved prompts of 2-4
+    chunks, then a prompt built from randomly chosen stored chunks (either
+    prompt, any order, adjacent or separated by fresh filler) behind a random
+    APC prefix. The store's matcher finds exactly the placed chunks, and the
+    pages after the blend load equal the oracle's assembly (relocated K) and
+    commit."""
+    rng = np.random.default_rng(4000 + seed)
+    registry.clear_for_test()
+    rope = Rope(D, 4096)
+    executor = CommitExecutor(rope)
+    registry.register_model(f"random-{seed}", executor)
+    conn = CacheBlendConnectorV1(_vllm_config(f"random-{seed}"), KVConnectorRole.WORKER)
+    kv = _layers(30 + seed)
+    conn.register_kv_caches(kv)
+    ordered = [kv[f"model.layers.{i}.self_attn.attn"] for i in range(L)]
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(seed))
+    saved, b0 = {}, 0
+    for r, base in (("a", 1_000_000), ("b", 2_000_000)):
+        n = CH * int(rng.integers(2, 5))
+        tokens = [base + int(t) for t in rng.permutation(n)]
+        slots = synthetic.block_slots(perm[b0:b0 + n // BS], BS, n)
+        b0 += n // BS
+        _save(conn, kv, RequestMetadata(r, tokens, slots, None, True, n))
+        saved[r] = (tokens, slots)
+    apc = int(rng.integers(0, 33))
+    prompt = [3_000_000 + i for i in range(apc)]
+    placed = []  # (request, source_start, target_start)
+    fresh = 4_000_000
+    while len(prompt) < 300:
+        if rng.random() < 0.4:
+            gap = int(rng.integers(1, 41))
+            prompt += list(range(fresh, fresh + gap))
+            fresh += gap
+        r = "ab"[int(rng.integers(2))]
+        src = CH * int(rng.integers(len(saved[r][0]) // CH))
+        placed.append((r, src, len(prompt)))
+        prompt += saved[r][0][src:src + CH]
+    prompt += list(range(fresh, fresh + int(rng.integers(0, 20))))
+    print(f"seed={seed} apc={apc} prompt={len(prompt)} placed={placed}", flush=True)
+    segments = conn._store.match(conn.model_scope, prompt, apc)
+    assert [(s.source_start, s.target_start) for s in segments] == [(s, t) for _, s, t in placed]
+    assert conn._store.pin("new", segments) == segments
+    plan = BlendPlan(apc, len(prompt), CH * len(placed), segments)
+    new_slots = synthetic.block_slots(perm[b0:b0 + (len(prompt) + BS - 1) // BS], BS, len(prompt))
+    before = [_bits(t) for t in ordered]
+    conn.bind_connector_metadata(CacheBlendConnectorMetadata(
+        [RequestMetadata("new", prompt, new_slots, plan, False, 0)]))
+    conn.start_load_kv(SimpleNamespace())
+    for name in kv:
+        conn.wait_for_layer_load(name)
+    torch.cuda.synchronize()
+    cache = rope.cos_sin_cache.cpu().numpy()
+
+    def reloc(old, new, k_bits):
+        k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
+        return O.f32_to_bf16(O.relocate_key(cache, old, new, k, D, True, bf16=True)).reshape(k_bits.shape)
+
+    for layer in range(L):
+        # the stored chunks hold the pages as they were when saved (loads
+        # write only the new prompt's blocks)
+        hosts = [(s, t, O.gather_paged_kv(before[layer], saved[r][1][s:s + CH].numpy(), BS))
+                 for r, s, t in placed]
+        buf = O.loader_assemble(before[layer], new_slots.numpy(), BS, apc, len(prompt), hosts, relocate=reloc)
+        want = before[layer].copy()
+        O.loader_commit(buf, want, new_slots.numpy(), BS, apc, len(prompt))
+        np.testing.assert_array_equal(_bits(ordered[layer]), want, err_msg=f"layer {layer}")
+    conn.close()
+    registry.clear_for_test()
+
+
 def _sleep_cycles_per_ms():
     torch.cuda._sleep(1000)
     torch.cuda.synchronize()
