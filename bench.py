@@ -526,6 +526,9 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
                   stream) one copy command per run of slots;
     reference  -- gather into device staging + one D2H into a freshly pinned
                   per-layer batch (the reference's scheme).
+    One store and writer per mode serve every repetition, as the connector
+    keeps its writer for the life of the process (the first repetition
+    starts the writer's copier and publisher threads and is reported apart).
     Also timed with the saves interleaved with bf16 GEMMs on the serving
     stream (about 1.5x the per-layer transfer time per layer), as a prefill
     would interleave them. Then the reload: the stored chunks scattered back
@@ -545,12 +548,16 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
     c = torch.empty_like(a)
     rep_id = [0]
 
+    writers = {}  # one store and writer per mode for the whole run, as a connector keeps them
+
     def once(mode, gemms=0):
         use_slab = mode != "reference"
-        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if use_slab else None)
-        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2,
-                                   slab=slab if use_slab else None,
-                                   slab_transfer=mode if use_slab else "dma")
+        if mode not in writers:
+            store = PinnedChunkStore(256, 1 << 40, on_release=slab.free if use_slab else None)
+            writers[mode] = (store, StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2,
+                                                      slab=slab if use_slab else None,
+                                                      slab_transfer=mode if use_slab else "dma"))
+        store, writer = writers[mode]
         r = rep_id[0]
         rep_id[0] += 1
         request = RequestMetadata(f"{mode}{r}", list(range(r * T, r * T + T)), slots_cpu, None, True, T)
@@ -564,7 +571,6 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         committed = sum(store.is_committed(sid) for _, sid in writer._chunk_ids[request.request_id])
-        writer.close()
         store.clear()
         return elapsed, committed
 
@@ -604,6 +610,8 @@ def store_pipeline(torch, layers, cache, src_slots, args, reload_slots):
         result["with_gemm_compute"][mode] = {
             "total_ms": round(total * 1e3, 3),
             "store_hidden_frac": round(1.0 - max(0.0, total - compute_s) / alone, 4)}
+    for _, writer in writers.values():
+        writer.close()
     # reload: the stored chunks (pinned slab slots) scattered back over the
     # host link into fresh random blocks, one scatter_chunks launch per layer
     from cacheblend_vllm.kv_layout import scatter_chunks
@@ -893,9 +901,10 @@ def blend_load(torch, synthetic, dev, args):
 
 def profile_store_run(torch, layers, cache, src_slots) -> int:
     """The Qwen3-8B layerwise store of ``store_pipeline`` in its default dma
-    mode, 4 repetitions (the first pins the slab's arenas and warms the
-    pools), each from the first save_layer to the end of wait_for_save; the
-    stored chunks of the last repetition are checked against a gather."""
+    mode, 4 repetitions on one writer (the first pins the slab's arenas and
+    starts the writer's threads), each from the first save_layer to the end
+    of wait_for_save; the stored chunks of the last repetition are checked
+    against a gather."""
     from cacheblend_vllm.host_store import PinnedChunkSlab, PinnedChunkStore
     from cacheblend_vllm.kv_layout import gather_paged_kv
     from cacheblend_vllm.store_path import RequestMetadata, StoreStreamWriter
@@ -906,9 +915,9 @@ def profile_store_run(torch, layers, cache, src_slots) -> int:
     slots_cpu = src_slots.cpu()
     nbytes = L * 2 * T * H * D * 2
     slab = PinnedChunkSlab((2, 256, H, D), torch.bfloat16, chunks_per_arena=128)
+    store = PinnedChunkStore(256, 1 << 40, on_release=slab.free)
+    writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2, slab=slab)
     for rep in range(4):
-        store = PinnedChunkStore(256, 1 << 40, on_release=slab.free)
-        writer = StoreStreamWriter(store, cache.block_size, 256, L, "bench", store_workers=2, slab=slab)
         request = RequestMetadata(f"p{rep}", list(range(rep * T, rep * T + T)), slots_cpu, None, True, T)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -929,8 +938,8 @@ def profile_store_run(torch, layers, cache, src_slots) -> int:
                         log(f"stored chunk at {seg.target_start} of layer {l} differs from the gather")
                         return 1
             store.release("check")
-        writer.close()
         store.clear()
+    writer.close()
     return 0
 
 
