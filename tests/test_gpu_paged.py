@@ -166,6 +166,30 @@ def test_multi_layer_gather_scatter_round_trip():
     assert torch.equal(src.view(torch.int16), got.view(torch.int16))
 
 
+@pytest.mark.parametrize("num_layers", [64, 65, 130])
+def test_multi_layer_copies_across_launches(num_layers):
+    """At most 64 layers go in one launch: 64 is one, 65 two, 130 three (the
+    last one of 2 layers). Every layer of the gather equals the oracle's, and
+    the scatter writes every layer's pages."""
+    layers = [synthetic.paged_pool(24, 16, 1, 64, torch.bfloat16, DEV, seed=100 + s) for s in range(num_layers)]
+    perm = torch.randperm(24, generator=torch.Generator().manual_seed(num_layers))
+    slots = synthetic.block_slots(perm[:8], 16, 120)
+    got = KL.gather_paged_kv_layers(layers, slots.to(DEV), 16)
+    assert got.shape == (num_layers, 2, 120, 1, 64)
+    for i, layer in enumerate(layers):
+        np.testing.assert_array_equal(_np(got[i]), O.gather_paged_kv(_np(layer), slots.numpy(), 16),
+                                      err_msg=f"layer {i}")
+    fresh = torch.randn(got.shape, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(DEV)
+    new_slots = synthetic.block_slots(perm[8:16], 16, 120)
+    want = [_np(layer).copy() for layer in layers]
+    for i in range(num_layers):
+        O.scatter_paged_kv(_np(fresh[i]), want[i], new_slots.numpy(), 16)
+    KL.scatter_paged_kv_layers(fresh, layers, new_slots.to(DEV), 16)
+    torch.cuda.synchronize()
+    for i, layer in enumerate(layers):
+        np.testing.assert_array_equal(_np(layer), want[i], err_msg=f"scatter layer {i}")
+
+
 def test_store_workload_round_trip_full_size():
     """Qwen3-8B store shape per layer: 4096-block pool, 8 KV heads x 128,
     an 8192-token prompt in random blocks, gathered and scattered back into
