@@ -166,6 +166,42 @@ def test_store_random_requests_bit_exact(seed):
 
 
 @pytest.mark.parametrize("transfer", ["dma", "host_write"])
+def test_store_and_reload_more_chunks_than_one_launch(transfer):
+    """A launch carries at most 64 chunk addresses: a 2080-token request in
+    16-token chunks is 130 chunks, three launches each way. Every stored
+    chunk equals the oracle's gather, and the reload of all 130 chunks in
+    place into fresh blocks equals the oracle's scatter."""
+    NB, BS, H, D, CH, T = 160, 16, 2, 64, 16, 2080
+    pool = synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=77)
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(77))
+    slots = synthetic.block_slots(perm[:T // BS], BS, T)
+    slab = PinnedChunkSlab((2, CH, H, D), torch.bfloat16, chunks_per_arena=48)
+    store = PinnedChunkStore(CH, 1 << 34, on_release=slab.free)
+    writer = StoreStreamWriter(store, BS, CH, 1, "m", slab=slab, slab_transfer=transfer)
+    writer.save_layer(0, pool, [RequestMetadata("big", list(range(T)), slots, None, True, T)])
+    writer.wait_for_save()
+    ids = writer._chunk_ids["big"]
+    assert len(ids) == T // CH == 130
+    chunks = []
+    for start, sid in ids:
+        got = store._entries[sid].layers[0]
+        np.testing.assert_array_equal(_bits(got), O.gather_paged_kv(_bits(pool), slots[start:start + CH].numpy(), BS),
+                                      err_msg=f"chunk {start}")
+        chunks.append(got)
+    fresh = synthetic.paged_pool(NB, BS, H, D, torch.bfloat16, DEV, seed=78)
+    new_slots = synthetic.block_slots(torch.randperm(NB, generator=torch.Generator().manual_seed(78))[:T // BS],
+                                      BS, T)
+    expect = _bits(fresh).copy()
+    O.scatter_paged_kv(np.concatenate([_bits(c) for c in chunks], axis=1), expect, new_slots.numpy(), BS)
+    scatter_chunks(chunks, fresh, new_slots.to(DEV), BS)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(fresh), expect)
+    store.clear()
+    writer.close()
+    slab.close()
+
+
+@pytest.mark.parametrize("transfer", ["dma", "host_write"])
 @pytest.mark.parametrize("layout", ["merged_first", "merged_block"])
 def test_fused_store_writes_chunks_bit_exact(layout, transfer):
     L, NB, BS, H, D, CH, T = 3, 128, 16, 8, 128, 256, 1000
