@@ -243,14 +243,17 @@ def test_loader_random_plans_bit_exact_vs_oracle(seed):
     shapes (the 80-dim per-pair path included), chunk sizes 16-64, an APC
     prefix of 0-3 blocks, 1-5 segments with 0-69-token gaps, an allocation
     end not aligned to the block size, RoPE relocation (NeoX or interleaved)
-    in bf16 and float32 and bit copies in f16, every transfer mode. Each
-    assembled buffer and the pages after each commit equal the oracle's."""
+    in bf16, float32 and f16, every transfer mode. Each assembled buffer and
+    the pages after each commit equal the oracle's bit for bit, except the
+    relocated f16 K rows: the oracle rounds once, at the end, where the
+    kernel rounds every elementwise step to f16 as torch does, so those rows
+    agree within 2e-3."""
     rng = np.random.default_rng(1000 + seed)
     bs = int(rng.choice([8, 16, 32]))
     heads, dim = [(1, 64), (2, 128), (4, 128), (8, 64), (3, 80)][int(rng.integers(5))]
     dtype = [torch.bfloat16, torch.float32, torch.float16][int(rng.integers(3))]
     chunk = int(rng.choice([16, 32, 64]))
-    moved = dtype != torch.float16 and rng.random() < 0.8
+    moved = rng.random() < 0.8
     neox = bool(rng.integers(2))
     zero_copy = ["auto", True, False][int(rng.integers(3))]
     apc = int(rng.integers(0, 3 * bs + 1))
@@ -274,9 +277,17 @@ def test_loader_random_plans_bit_exact_vs_oracle(seed):
             k = O.bf16_to_f32(k_bits).reshape(k_bits.shape[0], -1)
             out = O.relocate_key(cache, old, new, k, dim, neox, bf16=True)
             return O.f32_to_bf16(out).reshape(k_bits.shape)
+        if dtype == torch.float16:
+            k = k_bits.view(np.float16).astype(np.float32).reshape(k_bits.shape[0], -1)
+            out = O.relocate_key(cache16, old, new, k, dim, neox, bf16=False)
+            return out.astype(np.float16).view(np.uint16).reshape(k_bits.shape)
         k = k_bits.reshape(k_bits.shape[0], -1)
         return O.relocate_key(cache, old, new, k, dim, neox, bf16=False).reshape(k_bits.shape)
 
+    cache16 = cache.astype(np.float16).astype(np.float32)
+    relocated = np.zeros(alloc_end, dtype=bool)  # K rows whose positions move
+    for s, t, n in segs:
+        relocated[t:t + n] |= s != t
     loader = PagedBlendLoader(layers, store, "req", plan, slots, bs, _cfg(chunk_size=chunk),
                               zero_copy=zero_copy)
     loader.prefetch(0, rope)
@@ -288,7 +299,15 @@ def test_loader_random_plans_bit_exact_vs_oracle(seed):
             [(s, t, _bits(hosts[i, l])) for i, (s, t, _) in enumerate(segs)],
             relocate=reloc if moved else None,
         )
-        np.testing.assert_array_equal(_bits(buf), want, err_msg=f"layer {l}")
+        got = _bits(buf)
+        if dtype == torch.float16 and moved:
+            np.testing.assert_array_equal(got[1], want[1], err_msg=f"V layer {l}")
+            np.testing.assert_array_equal(got[0][~relocated], want[0][~relocated], err_msg=f"K layer {l}")
+            np.testing.assert_allclose(got[0][relocated].view(np.float16).astype(np.float32),
+                                       want[0][relocated].view(np.float16).astype(np.float32),
+                                       rtol=2e-3, atol=2e-3, err_msg=f"relocated K layer {l}")
+        else:
+            np.testing.assert_array_equal(got, want, err_msg=f"layer {l}")
         expect_pages = _bits(layers[l]).copy()
         fresh = torch.randn(buf.shape, dtype=torch.float32).to(dtype).to(DEV)
         O.loader_commit(_bits(fresh), expect_pages, slots.numpy(), bs, apc, alloc_end)
