@@ -7,8 +7,9 @@
 //
 // Two passes over Q.K^T on MFMA (v_mfma_f32_16x16x32_{bf16,f16}; the row
 // pass of 16-head groups on v_mfma_f32_32x32x16_{bf16,f16}):
-//   rowstats  one workgroup per (16-query tile, key range, kv head): the G
-//             query heads of the group x 16 queries against the range's
+//   rowstats  one workgroup per (1, 2 or 4 adjacent 16-query tiles, key
+//             range, kv head): the G query heads of the group x 16 queries
+//             of each tile against the range's
 //             64-key blocks staged in LDS, sums of exp against the range's
 //             first-block maximum (online max / sum where that does not
 //             apply) in the log2 domain, merged across the 16 lanes that
@@ -289,20 +290,29 @@ __device__ __forceinline__ void rowstats_block_wide(const SqArgs& a, const uint1
 // units do in colsum (see there for the wait and barrier scheme).
 // FULL: the group is exactly (4 / TPW) * MAXT heads, so every wave has MAXT
 // row tiles (a compile-time count: no branch between the tiles of a block).
-// TPW: query tiles per workgroup. With 2, two waves serve each of two
-// adjacent tiles (sorted queries: nearby positions) with twice the head slots,
-// so each K fragment read from LDS serves 64 rows (two waves per SIMD).
-// Two waves per SIMD for paired tiles (238 registers at head_dim 128) and
-// for four head slots per wave at head_dim 128 (236 registers; three waves
-// per SIMD spilled 224 bytes per lane); three waves per SIMD otherwise (two
+// TPW: query tiles per workgroup (adjacent tiles of sorted queries: nearby
+// positions), 4 / TPW waves per tile. With 2, two waves serve each of two
+// tiles with twice the head slots, so each K fragment read from LDS serves
+// 64 rows at 8 heads per KV head; with 4, each wave takes a whole tile's
+// group (up to 4 heads), so a K block staged in LDS serves four tiles and
+// no wave idles when the group is smaller than 4.
+// Two waves per SIMD for paired tiles (238 registers at head_dim 128), for
+// four head slots per wave at head_dim 128 (236 registers; three waves per
+// SIMD spilled 224 bytes per lane), and for four tiles per workgroup at
+// head_dim 128 or with 3-4 head slots (three waves per SIMD spill 87 bytes
+// per lane at 3 slots; at head_dim 64 with 1-2 slots three waves measured
+// 3% faster at one head per KV head); three waves per SIMD otherwise (two
 // head slots at head_dim 128 spill 96 bytes per lane there, yet two waves
 // per SIMD measured slower: 2.21-2.23 vs 1.99-2.00 ms at 5 heads per KV
-// head, 1.35 vs 1.30 ms at 6, on 32K-key layers).
-constexpr bool rs_two_waves(int tpw, int maxt, int ksteps) {
-  return tpw == 2 || (ksteps == 4 && maxt == 4);
+// head, 1.35 vs 1.30 ms at 6, on 32K-key layers, with one tile per
+// workgroup).
+constexpr int rs_waves(int tpw, int maxt, int ksteps) {
+  if (tpw == 2) return 2;
+  if (tpw == 4) return (ksteps == 4 || maxt >= 3) ? 2 : 3;
+  return (ksteps == 4 && maxt == 4) ? 2 : 3;
 }
 template <typename V, int KSTEPS, int MAXT, int RMODE, bool FULL, int TPW = 1>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(rs_two_waves(TPW, MAXT, KSTEPS) ? 2 : 3, rs_two_waves(TPW, MAXT, KSTEPS) ? 2 : 3)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(rs_waves(TPW, MAXT, KSTEPS), rs_waves(TPW, MAXT, KSTEPS))))
 void sq_rowstats_kernel(const SqArgs a) {
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per key row
@@ -935,11 +945,18 @@ template <typename V, int RMODE, int KS>
 int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   const uint64_t ntiles = (a.nq + kQTile - 1) / kQTile;
   const uint64_t kblocks = (a.nk + kKeyBlock2 - 1) / kKeyBlock2;
-  // 8 heads per KV head: two tiles per workgroup, four head slots per wave
-  // (two workgroups per CU); otherwise one tile (three per CU)
-  const bool pair = a.groups == 8;
-  const uint64_t tgroups = pair ? (ntiles + 1) / 2 : ntiles;
-  a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, pair || (a.groups > 8 && KS == 4) ? 2u : 3u);
+  // Query tiles per row-pass workgroup by heads per KV head: up to 4, four
+  // tiles, one wave per tile with the whole group; 5-8, two tiles, two waves
+  // per tile with up to four head slots each; more, one tile (its 16 heads
+  // on 32x32 MFMAs). Measured on 98,304-key layers of 4,096 sparse queries
+  // (C5 positions, ms at head_dim 128 against one tile per workgroup, which
+  // left waves without a head below 4): 1 head 13.83 -> 8.17, 2 heads 7.34 ->
+  // 5.03, 3 heads 3.57 -> 2.96, 4 heads 4.19 -> 3.53, 5 heads 5.87 -> 5.34,
+  // 6 heads 6.58 -> 5.71, 7 heads 3.49 -> 3.23 (28 query heads over 4).
+  const uint32_t tpw = a.groups <= 4 ? 4u : a.groups <= 8 ? 2u : 1u;
+  const uint64_t tgroups = (ntiles + tpw - 1) / tpw;
+  const int waves = tpw == 4 ? ((KS == 4 || a.groups >= 3) ? 2 : 3) : tpw == 2 ? 2 : (a.groups > 8 && KS == 4) ? 2 : 3;
+  a.row_chunks = row_chunks(uint32_t(tgroups * a.hkv), cus, uint32_t(waves));
   // one-dimensional grids (the kv head fastest): every launch within 2^32 threads
   CBK_REQUIRE(tgroups * a.hkv * a.row_chunks * kThreads < (uint64_t(1) << 32) &&
                   kblocks * a.hkv * kMaxColSplits * kThreads < (uint64_t(1) << 32) &&
@@ -949,14 +966,18 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   a.col_splits = col_splits(uint32_t(kblocks * a.hkv), cus);
   const dim3 g1(uint32_t(tgroups * a.hkv * a.row_chunks));
   const dim3 g2(uint32_t(kblocks * a.hkv * a.col_splits));
-  if (a.groups == 4)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
-  else if (a.groups < 4)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
-  else if (pair)
+  if (a.groups == 1)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 1, RMODE, true, 4>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 2)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, true, 4>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 3)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 3, RMODE, true, 4>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 4)
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true, 4>), g1, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 8)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true, 2>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups < 8)
-    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 2, RMODE, false>), g1, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, false, 2>), g1, dim3(kThreads), 0, stream, a);
   else if (a.groups == 16)
     hipLaunchKernelGGL((sq_rowstats_kernel<V, KS, 4, RMODE, true>), g1, dim3(kThreads), 0, stream, a);
   else

@@ -88,6 +88,13 @@ def _inputs(n_active, prefix, hq, hkv, d, dtype, seed):
     (torch.bfloat16, 128, 24, 2),
     (torch.bfloat16, 64, 9, 1),
     (torch.float16, 128, 12, 1),
+    # row-pass tile grouping: 1-4 heads per KV head take four tiles per
+    # workgroup (2 and 3 here, 1 and 4 above), 5-7 two tiles with head slots
+    # past the group (5, 7)
+    (torch.bfloat16, 128, 8, 4),
+    (torch.bfloat16, 64, 6, 2),
+    (torch.bfloat16, 128, 20, 4),
+    (torch.float16, 64, 14, 2),
 ])
 def test_sparse_q_scores_vs_oracle(dtype, d, hq, hkv):
     n_active, prefix = 1200 if dtype != torch.float32 else 300, 500
