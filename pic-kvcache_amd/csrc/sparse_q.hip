@@ -72,9 +72,9 @@ struct SqArgs {
   float2* stats;          // [hq][nq_pad] (m2 + log2(l), unused)
   float2* chunk_stats;    // [row_chunks][hq][nq_pad] (m2, l) of each key range, row_chunks > 1
   uint32_t row_chunks;    // key ranges per (query tile, kv head) in rowstats
-  int32_t* tiles;         // [ntiles][32]: the 16 query positions (-1 past nq), min, max, unused
+  int32_t* tiles;         // [nq_pad / 16][32]: the 16 query positions (-1 past nq), min, max, unused
   float* partial;         // [hkv][nk]
-  uint16_t* qdense;       // [ntiles][hkv][groups][16][D]: query rows in colsum's unit order
+  uint16_t* qdense;       // [hkv][nq_pad / 16][groups][16][D]: query rows in colsum's unit order
   uint32_t nq_pad;
   uint32_t col_splits;    // query-unit ranges per (key block, kv head) in colsum
 };
@@ -327,6 +327,10 @@ void sq_rowstats_kernel(const SqArgs a) {
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t ntiles = (a.nq + kQTile - 1) / kQTile;
   const uint32_t ngroups = (ntiles + TPW - 1) / TPW;  // workgroups' tile groups
+  // tiles the column pass reads (its units of 2 or 4 tiles at 1-2 heads per
+  // KV head end on a multiple of 4 tiles): their records and dense query
+  // rows are written too, empty past the queries
+  const uint32_t ntiles_pad = a.nq_pad / kQTile;
   // workgroup -> (tile, key range, kv head), the kv head fastest and the
   // latest tiles (most keys) first, so that workgroups are dispatched in
   // decreasing order of work across all heads
@@ -353,7 +357,7 @@ void sq_rowstats_kernel(const SqArgs a) {
       }
       lo = min(lo, tlo);
       hi = max(hi, thi);
-      if (g == 0 && chunk == 0 && qt_first + u < ntiles) {
+      if (g == 0 && chunk == 0 && qt_first + u < ntiles_pad) {
         a.tiles[kTileWords * (qt_first + u) + kQTile] = tlo;
         a.tiles[kTileWords * (qt_first + u) + kQTile + 1] = thi;
       }
@@ -400,13 +404,13 @@ void sq_rowstats_kernel(const SqArgs a) {
     for (int s = 0; s < NS; ++s)
       afrag[t][s] = row ? *reinterpret_cast<const V*>(row + (kStepDims * s + d0) * 2) : V(0);
     // the dense copy colsum streams (zeros past nq)
-    if (slot < nslots && chunk == 0 && tile_ok) {
-      uint16_t* dst = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + wv + WT * slot) * (kQTile * D) + col * D;
+    if (slot < nslots && chunk == 0 && qt < ntiles_pad) {
+      uint16_t* dst = a.qdense + ((int64_t(g) * ntiles_pad + qt) * a.groups + wv + WT * slot) * (kQTile * D) + col * D;
 #pragma unroll
       for (int s = 0; s < NS; ++s) *reinterpret_cast<V*>(dst + kStepDims * s + d0) = afrag[t][s];
     }
   }
-  if (g == 0 && chunk == 0 && threadIdx.x < kQTile * TPW && qt_first + threadIdx.x / kQTile < ntiles)
+  if (g == 0 && chunk == 0 && threadIdx.x < kQTile * TPW && qt_first + threadIdx.x / kQTile < ntiles_pad)
     a.tiles[kTileWords * (qt_first + threadIdx.x / kQTile) + threadIdx.x % kQTile] = s_pos[threadIdx.x];
   // nothing of the compiler's own in flight once the requests start
   CBK_WAIT_VM_LGKM0(0);
@@ -580,11 +584,15 @@ __device__ __forceinline__ void colsum_mfma(const uint16_t* qlds, uint32_t hl, c
 // Software-pipelined over the unit's 4 head slots: the MFMAs of head hl + 1
 // are issued before the VALU work of head hl, which they do not depend on.
 // Slots past the group (nh < 4) compute on rows that are never used. FULL
-// (every chunk holds 4 heads, the group is a multiple of 4): no branch
-// inside the unit, which the compiler then schedules as one block.
-template <typename V, int KSTEPS, int RMODE, bool MASK, bool FULL>
+// (every chunk holds 4 heads, the group is a multiple of 4, or the unit
+// spans T = 2 or 4 tiles of 4 / T heads each): no branch inside the unit,
+// which the compiler then schedules as one block. Slot hl's rows are those
+// of the unit's tile hl / (4 / T), whose record is trec[kTileWords * (hl /
+// (4 / T))] in LDS (MASK: its positions are read there, slot by slot, which
+// keeps them out of the registers of the unmasked units).
+template <typename V, int KSTEPS, int RMODE, bool MASK, bool FULL, int T>
 __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
-                                            uint32_t nh, int32_t kw0, const int32_t (&rpos)[4],
+                                            uint32_t nh, int32_t kw0, const int32_t* trec,
                                             const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
                                             uint32_t col, uint32_t rgrp) {
   f32x4 acc[2][kColTiles];
@@ -596,6 +604,11 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
       float mrow[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
+      int32_t rpos[4] = {0, 0, 0, 0};
+      if constexpr (MASK) {
+        const int4 rp = *reinterpret_cast<const int4*>(trec + kTileWords * (hl / (kHeadChunk / T)) + 4 * rgrp);
+        rpos[0] = rp.x; rpos[1] = rp.y; rpos[2] = rp.z; rpos[3] = rp.w;
+      }
 #pragma unroll
       for (int c = 0; c < kColTiles; ++c) {
         const f32x4 v = acc[hl & 1][c];
@@ -620,10 +633,14 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
   }
 }
 
-// three waves per SIMD: the LDS holds three workgroups' buffers
-template <typename V, int KSTEPS, int RMODE, bool FULL>
+// Three waves per SIMD: the LDS holds three workgroups' buffers. T: query
+// tiles per unit -- 1 (the unit is a tile's chunk of up to 4 heads), or 4 /
+// G at G = 1 or 2 heads per KV head (the unit is a group of T tiles, all of
+// their heads), so that no head slot computes on unused rows.
+template <typename V, int KSTEPS, int RMODE, bool FULL, int T = 1>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_colsum_kernel(
     const SqArgs a) {
+  static_assert(T == 1 || (FULL && (T == 2 || T == 4)), "units of several tiles hold whole groups");
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per row
   constexpr uint32_t kInsts = P / 4;              // Q requests per wave per unit (1 KiB each)
@@ -631,7 +648,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   constexpr int kQElems = kHeadChunk * kQTile * D;
   __shared__ __attribute__((aligned(16))) uint16_t qbuf[kQBuffers][kQElems];
   __shared__ __attribute__((aligned(16))) float2 sbuf[kQBuffers][128];  // 64 used, lanes 32-63 repeat
-  __shared__ __attribute__((aligned(16))) int32_t tbuf[kQBuffers][64];  // tile record, repeated
+  // tile records (T == 1: repeated; T == 4: two requests)
+  __shared__ __attribute__((aligned(16))) int32_t tbuf[kQBuffers][T == 4 ? 128 : 64];
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // workgroup -> (key block, kv head), the kv head fastest: the earliest key
   // blocks (seen by the most queries) of every head are dispatched first
@@ -669,7 +687,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // block sees them, so the workgroups resident together stream the same
   // units at about the same time and find them in L2.
   const int32_t ntiles = int32_t((a.nq + kQTile - 1) / kQTile);
-  const uint32_t nchunks = (a.groups + kHeadChunk - 1) / kHeadChunk;
+  const int32_t ntiles_pad = int32_t(a.nq_pad / kQTile);
+  const int32_t nunit_tiles = (ntiles + T - 1) / T;  // tiles, or groups of T tiles
+  const uint32_t nchunks = T == 1 ? (a.groups + kHeadChunk - 1) / kHeadChunk : 1u;
   int32_t tlo = ntiles;
   for (int32_t t0 = 0; t0 < ntiles; t0 += 64) {
     const int32_t u = t0 + int32_t(lane);
@@ -681,7 +701,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   }
   // this workgroup's share of the block's units: range `split` of
   // col_splits equal ranges, in unit order
-  const uint32_t all_units = uint32_t(ntiles - tlo) * nchunks;
+  const uint32_t all_units = tlo < ntiles ? uint32_t(nunit_tiles - tlo / T) * nchunks : 0u;
   const uint32_t u_lo = all_units * split / a.col_splits;
   const int32_t nunits = int32_t(all_units * (split + 1) / a.col_splits - u_lo);
 
@@ -694,21 +714,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     const uint32_t row = (wave * kInsts + j) * kRowsPerInst + lane / P;
     qoff[j] = (row * D + ((lane % P) ^ lds_swizzle<D>(row)) * 8) * 2;
   }
-  const uint32_t toff = (lane % kTileWords) * 4;
-  // wave 0's statistics request: 8 lanes (128 bytes) per head of the chunk;
-  // with every chunk whole (FULL) the lanes' offsets are the same each unit
-  const uint32_t soff_full = (((lane / 8) % kHeadChunk) * a.nq_pad + (lane % 8) * 2) * 8;
-  // Issues the unit of tile qt, head chunk hc (a request past the last unit
-  // repeats it, so every iteration issues the same number of requests) into
-  // buffer B: the Q rows, and on wave 0 the row statistics and the tile record.
+  const uint32_t toff = (T == 1 ? lane % kTileWords : lane) * 4;
+  // wave 0's statistics request: 8 lanes (128 bytes) per head slot of the
+  // unit (slot s: head s % (4 / T) of the unit's tile s / (4 / T)); with
+  // every unit whole (FULL) the lanes' offsets are the same each unit
+  constexpr uint32_t kSlotHeads = kHeadChunk / T;
+  const uint32_t slot0 = (lane / 8) % kHeadChunk;
+  const uint32_t soff_full =
+      ((slot0 % kSlotHeads) * a.nq_pad + (slot0 / kSlotHeads) * kQTile + (lane % 8) * 2) * 8;
+  // Issues the unit of tile (or tile group) qt, head chunk hc (a request past
+  // the last unit repeats it, so every iteration issues the same number of
+  // requests) into buffer B: the Q rows, and on wave 0 the row statistics
+  // and the tile records. A unit's Q rows are contiguous in the dense copy.
   auto request = [&](int32_t qt, uint32_t hc, auto bc) __attribute__((always_inline)) {
     constexpr int B = decltype(bc)::value;
-    const uint16_t* unit = a.qdense + ((int64_t(qt) * a.hkv + g) * a.groups + hc * kHeadChunk) * (kQTile * D);
+    const int32_t t0 = qt * T;  // the unit's first tile
+    const uint16_t* unit =
+        a.qdense + ((int64_t(g) * ntiles_pad + t0) * a.groups + hc * kHeadChunk) * (kQTile * D);
     const uint32_t lq = lds_address(qbuf[B]);
 #pragma unroll
     for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(unit, qoff[j], lq + (wave * kInsts + j) * 1024);
     if (wave == 0) {
-      const float2* st = a.stats + int64_t(g * a.groups + hc * kHeadChunk) * a.nq_pad + qt * kQTile;
+      const float2* st = a.stats + int64_t(g * a.groups + hc * kHeadChunk) * a.nq_pad + t0 * kQTile;
       uint32_t soff = soff_full;
       if constexpr (!FULL) {
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
@@ -716,11 +743,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         soff = (hl * a.nq_pad + (lane % 8) * 2) * 8;
       }
       lds_dma16(st, soff, lds_address(sbuf[B]));
-      lds_dma4(a.tiles + kTileWords * qt, toff, lds_address(tbuf[B]));
+      lds_dma4(a.tiles + kTileWords * t0, toff, lds_address(tbuf[B]));
+      if constexpr (T == 4) lds_dma4(a.tiles + kTileWords * (t0 + 2), toff, lds_address(tbuf[B]) + 256);
     }
   };
   // units in order: the head chunks of tile ntiles - 1, then of the tile
-  // below, down to tile tlo (stepped without divisions)
+  // below, down to tile tlo (stepped without divisions); with T > 1 the
+  // groups of T tiles from the last down to tlo's
   auto next = [&](int32_t& qt, uint32_t& hc) __attribute__((always_inline)) {
     if (++hc == nchunks) {
       hc = 0;
@@ -729,11 +758,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   };
   if (nunits > 0) {
     // unit it, and the unit requested in iteration it: unit u of the block
-    // is head chunk u % nchunks of tile ntiles - 1 - u / nchunks
-    int32_t qt_c = ntiles - 1 - int32_t(u_lo / nchunks), qt_r = qt_c;
+    // is head chunk u % nchunks of tile (group) nunit_tiles - 1 - u / nchunks
+    int32_t qt_c = nunit_tiles - 1 - int32_t(u_lo / nchunks), qt_r = qt_c;
     uint32_t hc_c = u_lo % nchunks, hc_r = hc_c;
     const uint32_t u_last = u_lo + uint32_t(nunits) - 1;  // the range's last unit
-    const int32_t qt_last = ntiles - 1 - int32_t(u_last / nchunks);
+    const int32_t qt_last = nunit_tiles - 1 - int32_t(u_last / nchunks);
     const uint32_t hc_last = u_last % nchunks;
     auto request_next = [&](int32_t i, auto bc) __attribute__((always_inline)) {
       if (i < nunits) {
@@ -750,8 +779,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     auto iteration = [&](int32_t it, auto bc) __attribute__((always_inline)) {
       constexpr int B = decltype(bc)::value;
       // unit it has landed once at most the newest unit's requests are pending
+      // (wave 0 also requests the statistics and one or two tile-record pieces)
       if (wave == 0)
-        CBK_WAIT_VM_LGKM0(kInsts + 2);
+        CBK_WAIT_VM_LGKM0(kInsts + (T == 4 ? 3 : 2));
       else
         CBK_WAIT_VM_LGKM0(kInsts);
       asm volatile("s_barrier" ::: "memory");
@@ -759,17 +789,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       const int32_t qt = qt_c;
       const uint32_t hc = hc_c;
       next(qt_c, hc_c);
-      const int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile]);  // uniform: scalar
-      const int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile + 1]);
-      if (tmax >= kw0) {
-        int32_t rpos[4];
+      // the unit's tiles' earliest and latest positions (uniform: scalar)
+      int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile]);
+      int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile + 1]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rpos[i] = tbuf[B][4 * rgrp + i];
+      for (int t = 1; t < T; ++t) {
+        tmin = min(tmin, __builtin_amdgcn_readfirstlane(tbuf[B][kTileWords * t + kQTile]));
+        tmax = max(tmax, __builtin_amdgcn_readfirstlane(tbuf[B][kTileWords * t + kQTile + 1]));
+      }
+      if (tmax >= kw0) {
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
-        if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt) * kQTile + kQTile > a.nq)
-          colsum_unit<V, KSTEPS, RMODE, true, FULL>(a, qbuf[B], sbuf[B], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+        // masked: some key of the wave past some query, or rows past nq in the unit
+        if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt * T + T) * kQTile > a.nq)
+          colsum_unit<V, KSTEPS, RMODE, true, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], bfrag, acc_col, col,
+                                                       rgrp);
         else
-          colsum_unit<V, KSTEPS, RMODE, false, FULL>(a, qbuf[B], sbuf[B], nh, kw0, rpos, bfrag, acc_col, col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, false, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], bfrag, acc_col,
+                                                        col, rgrp);
       }
     };
     int32_t it = 0;
@@ -885,10 +921,12 @@ struct SqLayout {
 __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   SqLayout L;
   L.ntiles = uint32_t((nq + kQTile - 1) / kQTile);
-  L.nq_pad = L.ntiles * kQTile;
+  // a multiple of 4 tiles: the column pass's units of 4 tiles (one head per
+  // KV head) read whole groups of tile records, statistics and query rows
+  L.nq_pad = (L.ntiles + 3) / 4 * 4 * kQTile;
   L.stats = 0;
   L.tiles = (L.stats + uint64_t(hq) * L.nq_pad * 8 + 255) & ~uint64_t(255);
-  L.partial = (L.tiles + uint64_t(L.ntiles) * kTileWords * 4 + 255) & ~uint64_t(255);
+  L.partial = (L.tiles + uint64_t(L.nq_pad / kQTile) * kTileWords * 4 + 255) & ~uint64_t(255);
   L.qdense = (L.partial + uint64_t(kMaxColSplits) * hkv * nk * 4 + 255) & ~uint64_t(255);
   // padded by one unit: a partial head chunk's requests read past its group
   L.chunk_stats = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
@@ -985,7 +1023,11 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   if (a.row_chunks > 1)
     hipLaunchKernelGGL(sq_merge_kernel, dim3((a.hq * a.nq_pad + kThreads - 1) / kThreads), dim3(kThreads), 0,
                        stream, a);
-  if (a.groups % kHeadChunk == 0)
+  if (a.groups == 1)
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 4>), g2, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 2)
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 2>), g2, dim3(kThreads), 0, stream, a);
+  else if (a.groups % kHeadChunk == 0)
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true>), g2, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, false>), g2, dim3(kThreads), 0, stream, a);

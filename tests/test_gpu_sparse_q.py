@@ -233,7 +233,7 @@ def test_sparse_q_full_layer6_vs_oracle_and_properties():
     assert np.array_equal(scores(all_rows), full)
 
 
-@pytest.mark.parametrize("hq", [8, 16])
+@pytest.mark.parametrize("hq", [2, 4, 8, 16])
 @pytest.mark.parametrize("n_active,prefix,d", [(1, 0, 128), (5, 0, 64), (17, 40, 128), (63, 1, 64),
                                                 (64, 0, 128), (65, 63, 128), (200, 3, 64)])
 def test_sparse_q_small_contexts(n_active, prefix, d, hq):
@@ -241,7 +241,11 @@ def test_sparse_q_small_contexts(n_active, prefix, d, hq):
     the context repeat the last key and are masked), single and partial
     16-query tiles (rows past the queries are zeros, masked in the column
     pass). 16 query heads over 2 KV heads take the row pass that pairs
-    adjacent tiles: 1 and 5 tiles leave the last pair's second tile empty."""
+    adjacent tiles: 1 and 5 tiles leave the last pair's second tile empty;
+    2 to 8 heads take four tiles per row-pass workgroup (1 to 5 tiles: empty
+    tiles in the last group), and 2 or 4 heads (1 or 2 per KV head) also
+    column-pass units of four or two tiles, whose last unit holds empty
+    tiles."""
     hkv = 2
     g = torch.Generator().manual_seed(n_active * 7 + prefix)
     nk = prefix + n_active
