@@ -412,6 +412,16 @@ void sq_rowstats_kernel(const SqArgs a) {
   }
   if (g == 0 && chunk == 0 && threadIdx.x < kQTile * TPW && qt_first + threadIdx.x / kQTile < ntiles_pad)
     a.tiles[kTileWords * (qt_first + threadIdx.x / kQTile) + threadIdx.x % kQTile] = s_pos[threadIdx.x];
+  // the workgroup of the last tiles also writes the records past them, up
+  // to 4 past the padded count, empty (positions -1, min above any, max -1):
+  // the column pass's units of rows read their tiles' records whole
+  if (blockIdx.x == 0) {
+    const uint32_t t_end = ntiles_pad + 4;
+    for (uint32_t w = ngroups * TPW * kTileWords + threadIdx.x; w < t_end * kTileWords; w += kThreads) {
+      const uint32_t k = w % kTileWords;
+      a.tiles[w] = k < kQTile ? -1 : k == kQTile ? 0x7fffffff : k == kQTile + 1 ? -1 : 0;
+    }
+  }
   // nothing of the compiler's own in flight once the requests start
   CBK_WAIT_VM_LGKM0(0);
 
@@ -584,15 +594,18 @@ __device__ __forceinline__ void colsum_mfma(const uint16_t* qlds, uint32_t hl, c
 // Software-pipelined over the unit's 4 head slots: the MFMAs of head hl + 1
 // are issued before the VALU work of head hl, which they do not depend on.
 // Slots past the group (nh < 4) compute on rows that are never used. FULL
-// (every chunk holds 4 heads, the group is a multiple of 4, or the unit
-// spans T = 2 or 4 tiles of 4 / T heads each): no branch inside the unit,
-// which the compiler then schedules as one block. Slot hl's rows are those
-// of the unit's tile hl / (4 / T), whose record is trec[kTileWords * (hl /
-// (4 / T))] in LDS (MASK: its positions are read there, slot by slot, which
-// keeps them out of the registers of the unmasked units).
+// (every chunk holds 4 heads, the group is a multiple of 4, or the unit is
+// four consecutive (tile, head) rows, T > 1): no branch inside the unit,
+// which the compiler then schedules as one block. With T > 1 slot hl holds
+// head (h0 + hl) mod G of the unit's tile (h0 + hl) / G (its first tile's
+// heads from h0 on, then the next tile's; rows past the last query tile
+// belong to empty tiles, whose positions are -1); MASK reads a slot's
+// positions from its tile's record in LDS (trec), which keeps them out of
+// the unmasked units' registers.
 template <typename V, int KSTEPS, int RMODE, bool MASK, bool FULL, int T>
 __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qlds, const float2* st,
-                                            uint32_t nh, int32_t kw0, const int32_t* trec,
+                                            uint32_t nh, int32_t kw0, const int32_t* trec, uint32_t grp,
+                                            uint32_t h0,
                                             const V (&bfrag)[kColTiles][KSTEPS], float (&acc_col)[kColTiles],
                                             uint32_t col, uint32_t rgrp) {
   f32x4 acc[2][kColTiles];
@@ -606,7 +619,10 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
       for (int i = 0; i < 4; ++i) mrow[i] = st[hl * kQTile + 4 * rgrp + i].x;
       int32_t rpos[4] = {0, 0, 0, 0};
       if constexpr (MASK) {
-        const int4 rp = *reinterpret_cast<const int4*>(trec + kTileWords * (hl / (kHeadChunk / T)) + 4 * rgrp);
+        uint32_t tix = 0;  // the slot's tile within the unit (uniform)
+#pragma unroll
+        for (int k = 1; k < T; ++k) tix += (h0 + hl >= uint32_t(k) * grp) ? 1u : 0u;
+        const int4 rp = *reinterpret_cast<const int4*>(trec + kTileWords * tix + 4 * rgrp);
         rpos[0] = rp.x; rpos[1] = rp.y; rpos[2] = rp.z; rpos[3] = rp.w;
       }
 #pragma unroll
@@ -633,14 +649,22 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
   }
 }
 
-// Three waves per SIMD: the LDS holds three workgroups' buffers. T: query
-// tiles per unit -- 1 (the unit is a tile's chunk of up to 4 heads), or 4 /
-// G at G = 1 or 2 heads per KV head (the unit is a group of T tiles, all of
-// their heads), so that no head slot computes on unused rows.
-template <typename V, int KSTEPS, int RMODE, bool FULL, int T = 1>
+// Three waves per SIMD: the LDS holds three workgroups' buffers. Units: T ==
+// 1, a tile's chunk of up to 4 of its G heads (G a multiple of 4: every
+// chunk whole); T > 1, four consecutive (tile, head) rows of the KV head's
+// queries (row f is head f mod G of tile f / G), which span at most T tiles
+// (T = 4 at one head per KV head, else 2), so that no head slot computes
+// on rows that are never used when G is not a multiple of 4. G0: G known at
+// compile time (1 or 2: the four rows are whole tiles, so every slot's tile
+// and head are constants; 24-43 fewer spilled registers, 3-8% faster than
+// the run-time mapping there), 0 for any G.
+template <typename V, int KSTEPS, int RMODE, bool FULL, int T = 1, int G0 = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_colsum_kernel(
     const SqArgs a) {
-  static_assert(T == 1 || (FULL && (T == 2 || T == 4)), "units of several tiles hold whole groups");
+  static_assert(T == 1 || (FULL && (T == 2 || T == 4)), "units of rows are whole");
+  static_assert(G0 == 0 || G0 * T == kHeadChunk, "a compile-time group fills the unit's tiles");
+  constexpr bool FLAT = T > 1;
+  const uint32_t G = G0 ? uint32_t(G0) : a.groups;  // heads per KV head
   constexpr int D = 32 * KSTEPS;
   constexpr uint32_t P = D / 8;                   // 16-byte pieces per row
   constexpr uint32_t kInsts = P / 4;              // Q requests per wave per unit (1 KiB each)
@@ -688,8 +712,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   // units at about the same time and find them in L2.
   const int32_t ntiles = int32_t((a.nq + kQTile - 1) / kQTile);
   const int32_t ntiles_pad = int32_t(a.nq_pad / kQTile);
-  const int32_t nunit_tiles = (ntiles + T - 1) / T;  // tiles, or groups of T tiles
-  const uint32_t nchunks = T == 1 ? (a.groups + kHeadChunk - 1) / kHeadChunk : 1u;
+  const uint32_t nflat = uint32_t(ntiles) * G;  // (tile, head) rows of the KV head
+  // unit positions: tiles (each of nchunks units), or units of four rows
+  const int32_t nunit_tiles = FLAT ? int32_t((nflat + 3) / 4) : ntiles;
+  const uint32_t nchunks = FLAT ? 1u : (a.groups + kHeadChunk - 1) / kHeadChunk;
   int32_t tlo = ntiles;
   for (int32_t t0 = 0; t0 < ntiles; t0 += 64) {
     const int32_t u = t0 + int32_t(lane);
@@ -701,7 +727,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   }
   // this workgroup's share of the block's units: range `split` of
   // col_splits equal ranges, in unit order
-  const uint32_t all_units = tlo < ntiles ? uint32_t(nunit_tiles - tlo / T) * nchunks : 0u;
+  // the lowest unit holding a row of tile tlo
+  const int32_t ulo = FLAT ? int32_t(uint32_t(tlo) * G / 4) : tlo;
+  const uint32_t all_units = tlo < ntiles ? uint32_t(nunit_tiles - ulo) * nchunks : 0u;
   const uint32_t u_lo = all_units * split / a.col_splits;
   const int32_t nunits = int32_t(all_units * (split + 1) / a.col_splits - u_lo);
 
@@ -716,28 +744,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   }
   const uint32_t toff = (T == 1 ? lane % kTileWords : lane) * 4;
   // wave 0's statistics request: 8 lanes (128 bytes) per head slot of the
-  // unit (slot s: head s % (4 / T) of the unit's tile s / (4 / T)); with
-  // every unit whole (FULL) the lanes' offsets are the same each unit
-  constexpr uint32_t kSlotHeads = kHeadChunk / T;
+  // unit; with every chunk whole (FULL, T == 1) the lanes' offsets are the
+  // same each unit
   const uint32_t slot0 = (lane / 8) % kHeadChunk;
-  const uint32_t soff_full =
-      ((slot0 % kSlotHeads) * a.nq_pad + (slot0 / kSlotHeads) * kQTile + (lane % 8) * 2) * 8;
-  // Issues the unit of tile (or tile group) qt, head chunk hc (a request past
-  // the last unit repeats it, so every iteration issues the same number of
-  // requests) into buffer B: the Q rows, and on wave 0 the row statistics
-  // and the tile records. A unit's Q rows are contiguous in the dense copy.
+  const uint32_t soff_full = (slot0 * a.nq_pad + (lane % 8) * 2) * 8;
+  // Issues unit qt (a tile's head chunk hc, or the four rows from 4 qt; a
+  // request past the last unit repeats it, so every iteration issues the
+  // same number of requests) into buffer B: the Q rows, and on wave 0 the
+  // row statistics and the tile records. A unit's Q rows are contiguous in
+  // the dense copy.
   auto request = [&](int32_t qt, uint32_t hc, auto bc) __attribute__((always_inline)) {
     constexpr int B = decltype(bc)::value;
-    const int32_t t0 = qt * T;  // the unit's first tile
+    const uint32_t f0 = FLAT ? 4u * uint32_t(qt) : 0u;
+    const int32_t t0 = FLAT ? int32_t(f0 / G) : qt;  // the unit's first tile
     const uint16_t* unit =
-        a.qdense + ((int64_t(g) * ntiles_pad + t0) * a.groups + hc * kHeadChunk) * (kQTile * D);
+        FLAT ? a.qdense + (int64_t(g) * ntiles_pad * G + f0) * (kQTile * D)
+             : a.qdense + ((int64_t(g) * ntiles_pad + t0) * a.groups + hc * kHeadChunk) * (kQTile * D);
     const uint32_t lq = lds_address(qbuf[B]);
 #pragma unroll
     for (uint32_t j = 0; j < kInsts; ++j) lds_dma16(unit, qoff[j], lq + (wave * kInsts + j) * 1024);
     if (wave == 0) {
-      const float2* st = a.stats + int64_t(g * a.groups + hc * kHeadChunk) * a.nq_pad + t0 * kQTile;
+      const float2* st = a.stats + int64_t(g * G + hc * kHeadChunk) * a.nq_pad + t0 * kQTile;
       uint32_t soff = soff_full;
-      if constexpr (!FULL) {
+      if constexpr (FLAT) {
+        // slot s: row f0 + s, head (h0 + s) mod G of tile t0 + (h0 + s) / G
+        const uint32_t hs = f0 - uint32_t(t0) * G + slot0;
+        uint32_t ts = 0;
+#pragma unroll
+        for (int k = 1; k < T; ++k) ts += hs >= uint32_t(k) * G ? 1u : 0u;
+        soff = ((hs - ts * G) * a.nq_pad + ts * kQTile + (lane % 8) * 2) * 8;
+      } else if constexpr (!FULL) {
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
         const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // heads past the chunk repeat its last
         soff = (hl * a.nq_pad + (lane % 8) * 2) * 8;
@@ -749,7 +785,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   };
   // units in order: the head chunks of tile ntiles - 1, then of the tile
   // below, down to tile tlo (stepped without divisions); with T > 1 the
-  // groups of T tiles from the last down to tlo's
+  // units of four rows from the last down to the one holding tlo's first
   auto next = [&](int32_t& qt, uint32_t& hc) __attribute__((always_inline)) {
     if (++hc == nchunks) {
       hc = 0;
@@ -758,7 +794,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   };
   if (nunits > 0) {
     // unit it, and the unit requested in iteration it: unit u of the block
-    // is head chunk u % nchunks of tile (group) nunit_tiles - 1 - u / nchunks
+    // is head chunk u % nchunks of tile nunit_tiles - 1 - u / nchunks (T > 1:
+    // the rows of unit position nunit_tiles - 1 - u)
     int32_t qt_c = nunit_tiles - 1 - int32_t(u_lo / nchunks), qt_r = qt_c;
     uint32_t hc_c = u_lo % nchunks, hc_r = hc_c;
     const uint32_t u_last = u_lo + uint32_t(nunits) - 1;  // the range's last unit
@@ -789,7 +826,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       const int32_t qt = qt_c;
       const uint32_t hc = hc_c;
       next(qt_c, hc_c);
-      // the unit's tiles' earliest and latest positions (uniform: scalar)
+      // the unit's tiles t0 .. t0 + T - 1 (T > 1: all that its rows can
+      // span; a tile it does not reach only widens the test below, and
+      // those past the last query tile have empty records, which the row
+      // pass writes) and their earliest and latest positions (uniform: scalar)
+      const uint32_t f0 = FLAT ? 4u * uint32_t(qt) : 0u;
+      const int32_t t0 = FLAT ? int32_t(f0 / G) : qt;
+      const uint32_t h0 = f0 - uint32_t(t0) * G;  // the first row's head
       int32_t tmin = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile]);
       int32_t tmax = __builtin_amdgcn_readfirstlane(tbuf[B][kQTile + 1]);
 #pragma unroll
@@ -799,13 +842,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       }
       if (tmax >= kw0) {
         const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
-        // masked: some key of the wave past some query, or rows past nq in the unit
-        if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(qt * T + T) * kQTile > a.nq)
-          colsum_unit<V, KSTEPS, RMODE, true, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], bfrag, acc_col, col,
-                                                       rgrp);
+        // masked: some key of the wave past some query, or rows past nq in
+        // the unit's tiles
+        if (kw0 + 16 * kColTiles - 1 > tmin || uint32_t(t0 + T) * kQTile > a.nq)
+          colsum_unit<V, KSTEPS, RMODE, true, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], G, h0, bfrag,
+                                                       acc_col, col, rgrp);
         else
-          colsum_unit<V, KSTEPS, RMODE, false, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], bfrag, acc_col,
-                                                        col, rgrp);
+          colsum_unit<V, KSTEPS, RMODE, false, FULL, T>(a, qbuf[B], sbuf[B], nh, kw0, tbuf[B], G, h0, bfrag,
+                                                        acc_col, col, rgrp);
       }
     };
     int32_t it = 0;
@@ -925,8 +969,11 @@ __host__ SqLayout sq_layout(int64_t nq, int64_t nk, int64_t hq, int64_t hkv) {
   // KV head) read whole groups of tile records, statistics and query rows
   L.nq_pad = (L.ntiles + 3) / 4 * 4 * kQTile;
   L.stats = 0;
-  L.tiles = (L.stats + uint64_t(hq) * L.nq_pad * 8 + 255) & ~uint64_t(255);
-  L.partial = (L.tiles + uint64_t(L.nq_pad / kQTile) * kTileWords * 4 + 255) & ~uint64_t(255);
+  // (plus a tile of rows: the last unit of (tile, head) rows may reach the
+  // rows of the tile past the last query tile, which it masks)
+  L.tiles = (L.stats + (uint64_t(hq) * L.nq_pad + kQTile) * 8 + 255) & ~uint64_t(255);
+  // (plus 4 records: a unit's requests read T records from its first tile)
+  L.partial = (L.tiles + uint64_t(L.nq_pad / kQTile + 4) * kTileWords * 4 + 255) & ~uint64_t(255);
   L.qdense = (L.partial + uint64_t(kMaxColSplits) * hkv * nk * 4 + 255) & ~uint64_t(255);
   // padded by one unit: a partial head chunk's requests read past its group
   L.chunk_stats = (L.qdense + (uint64_t(L.nq_pad) * hq + 4 * kQTile) * kMaxHeadDim * 2 + 255) & ~uint64_t(255);
@@ -1002,6 +1049,11 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
               "sparse_q: %llu query tiles x %llu key blocks x %u kv heads exceed one launch",
               (unsigned long long)ntiles, (unsigned long long)kblocks, a.hkv);
   a.col_splits = col_splits(uint32_t(kblocks * a.hkv), cus);
+  // units of four (tile, head) rows address a KV head's statistics with
+  // per-lane 32-bit byte offsets
+  CBK_REQUIRE(a.groups % kHeadChunk == 0 || uint64_t(a.groups) * a.nq_pad * 8 < (uint64_t(1) << 31),
+              "sparse_q: %u heads per KV head x %u query rows exceed the column pass's offsets", a.groups,
+              a.nq_pad);
   const dim3 g1(uint32_t(tgroups * a.hkv * a.row_chunks));
   const dim3 g2(uint32_t(kblocks * a.hkv * a.col_splits));
   if (a.groups == 1)
@@ -1023,14 +1075,22 @@ int launch_mfma_ks(SqArgs& a, int cus, hipStream_t stream) {
   if (a.row_chunks > 1)
     hipLaunchKernelGGL(sq_merge_kernel, dim3((a.hq * a.nq_pad + kThreads - 1) / kThreads), dim3(kThreads), 0,
                        stream, a);
-  if (a.groups == 1)
-    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 4>), g2, dim3(kThreads), 0, stream, a);
-  else if (a.groups == 2)
-    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 2>), g2, dim3(kThreads), 0, stream, a);
-  else if (a.groups % kHeadChunk == 0)
+  // column-pass units: a tile's chunk of 4 heads when the group is a
+  // multiple of 4, else four consecutive (tile, head) rows (spanning up to 4
+  // tiles at one head per KV head, 2 otherwise); measured on 98,304-key
+  // layers of 4,096 sparse queries at head_dim 128 against chunks whose
+  // slots past the group computed unused rows: 1 head per KV head 8.05 ->
+  // 5.21 ms, 2 heads 4.96 -> 4.16 ms (four rows of two tiles), 3 heads
+  // 2.92 -> 2.78, 5 heads 5.27 -> 4.60, 6 heads 5.70 -> 5.31, 7 heads 3.24 ->
+  // 3.20 ms
+  if (a.groups % kHeadChunk == 0)
     hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true>), g2, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 1)
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 4, 1>), g2, dim3(kThreads), 0, stream, a);
+  else if (a.groups == 2)
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 2, 2>), g2, dim3(kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, false>), g2, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((sq_colsum_kernel<V, KS, RMODE, true, 2>), g2, dim3(kThreads), 0, stream, a);
   return CBK_OK;
 }
 

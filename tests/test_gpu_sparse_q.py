@@ -233,7 +233,7 @@ def test_sparse_q_full_layer6_vs_oracle_and_properties():
     assert np.array_equal(scores(all_rows), full)
 
 
-@pytest.mark.parametrize("hq", [2, 4, 8, 16])
+@pytest.mark.parametrize("hq", [2, 4, 6, 8, 10, 16])
 @pytest.mark.parametrize("n_active,prefix,d", [(1, 0, 128), (5, 0, 64), (17, 40, 128), (63, 1, 64),
                                                 (64, 0, 128), (65, 63, 128), (200, 3, 64)])
 def test_sparse_q_small_contexts(n_active, prefix, d, hq):
@@ -245,7 +245,9 @@ def test_sparse_q_small_contexts(n_active, prefix, d, hq):
     2 to 8 heads take four tiles per row-pass workgroup (1 to 5 tiles: empty
     tiles in the last group), and 2 or 4 heads (1 or 2 per KV head) also
     column-pass units of four or two tiles, whose last unit holds empty
-    tiles."""
+    tiles; 6 and 10 heads (3 and 5 per KV head) take column-pass units of
+    four consecutive (tile, head) rows across tile boundaries, the last of
+    which reaches rows past the last tile."""
     hkv = 2
     g = torch.Generator().manual_seed(n_active * 7 + prefix)
     nk = prefix + n_active
