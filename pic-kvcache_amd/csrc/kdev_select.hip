@@ -40,7 +40,11 @@ template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
 template <> __device__ __forceinline__ float to_f32<_Float16>(_Float16 v) { return float(v); }
 
 // VE elements per load; T is the storage type (uint16_t carries bf16 bits).
-template <typename T, int VE>
+// SUB rows share a wave pass, 64 / SUB lanes each: rows of at most 32 or 16
+// vectors (e.g. 2 KV heads x 128 bf16, a 4-KV-head layer split over two
+// ranks) would otherwise leave half or three quarters of the lanes without
+// a load (2 heads: 63% of 8 TB/s with one row per pass).
+template <typename T, int VE, int SUB>
 __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
     const T* __restrict__ fresh, int64_t fs, const T* __restrict__ cached, int64_t cs,
     int64_t cached_rows_total, const int64_t* __restrict__ rows, int64_t row0, uint32_t n,
@@ -50,9 +54,11 @@ __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
   // counters (the selection kernels run after this launch on the stream)
   if (zero_words != nullptr && blockIdx.x == 0)
     for (uint32_t i = threadIdx.x; i < nzero; i += kKdevThreads) zero_words[i] = 0u;
+  constexpr uint32_t LPR = 64 / SUB;  // lanes per row
   const uint32_t lane = threadIdx.x & 63;
+  const uint32_t sub = lane / LPR, l = lane % LPR;
   const uint32_t wave = blockIdx.x * (kKdevThreads / 64) + (threadIdx.x >> 6);
-  const uint32_t r0 = wave * kRowsPerWave;
+  const uint32_t r0 = wave * kRowsPerWave * SUB;  // rows r0 + SUB i + sub
   if (r0 >= n) return;
 
   const T* fp[kRowsPerWave];
@@ -60,7 +66,7 @@ __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
   bool ok[kRowsPerWave];
 #pragma unroll
   for (int i = 0; i < kRowsPerWave; ++i) {
-    const uint32_t r = r0 + i;
+    const uint32_t r = r0 + SUB * i + sub;
     ok[i] = r < n;
     fp[i] = fresh;
     cp[i] = cached;
@@ -75,7 +81,7 @@ __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
 #pragma unroll
   for (int i = 0; i < kRowsPerWave; ++i) acc[i] = 0.f;
 
-  for (uint32_t j = lane * VE; j < width; j += 64 * VE) {
+  for (uint32_t j = l * VE; j < width; j += LPR * VE) {
     VecT a[kRowsPerWave], b[kRowsPerWave];
     // read once: non-temporal loads (37.45-37.49 -> 37.09-37.39 us per
     // 64K-token select, same box)
@@ -99,8 +105,11 @@ __global__ __launch_bounds__(kKdevThreads) void kdev_kernel(
   }
 #pragma unroll
   for (int i = 0; i < kRowsPerWave; ++i) {
-    const float s = wave_sum(acc[i]);
-    if (lane == 0 && r0 + i < n) scores[r0 + i] = ok[i] ? s : __uint_as_float(0x7fc00000u);
+    float s = acc[i];
+#pragma unroll
+    for (uint32_t off = LPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, int(off), 64);
+    const uint32_t r = r0 + SUB * i + sub;
+    if (l == 0 && r < n) scores[r] = ok[i] ? s : __uint_as_float(0x7fc00000u);
   }
 }
 
@@ -112,19 +121,30 @@ int launch_kdev_t(const void* fresh, int64_t fs, const void* cached, int64_t cs,
   int64_t vals[5] = {fs * eb, cs * eb, width * eb, int64_t(reinterpret_cast<uintptr_t>(fresh)),
                      int64_t(reinterpret_cast<uintptr_t>(cached))};
   const int vec_bytes = common_vec_bytes(vals, 5);
-  const int64_t waves = (n + kRowsPerWave - 1) / kRowsPerWave;
+  const int ve = vec_bytes / int(eb);
+  // rows per wave pass: 4 for rows of at most 16 vectors, 2 for 32, else 1
+  const int64_t row_vecs = (width + ve - 1) / ve;
+  const int sub = row_vecs <= 16 ? 4 : row_vecs <= 32 ? 2 : 1;
+  const int64_t waves = (n + kRowsPerWave * sub - 1) / (kRowsPerWave * sub);
   const dim3 grid(uint32_t((waves + kKdevThreads / 64 - 1) / (kKdevThreads / 64)));
   const T* f = static_cast<const T*>(fresh);
   const T* c = static_cast<const T*>(cached);
-#define CBK_KDEV(VE)                                                                        \
-  hipLaunchKernelGGL((kdev_kernel<T, VE>), grid, dim3(kKdevThreads), 0, stream, f, fs, c, cs, \
+#define CBK_KDEV(VE, SUB)                                                                        \
+  hipLaunchKernelGGL((kdev_kernel<T, VE, SUB>), grid, dim3(kKdevThreads), 0, stream, f, fs, c, cs, \
                      total_rows, rows, row0, uint32_t(n), uint32_t(width), scores, zero_words, nzero)
-  switch (vec_bytes / int(eb)) {
-    case 8: CBK_KDEV(8); break;
-    case 4: CBK_KDEV(4); break;
-    case 2: CBK_KDEV(2); break;
-    default: CBK_KDEV(1); break;
+#define CBK_KDEV_SUB(VE)           \
+  switch (sub) {                   \
+    case 4: CBK_KDEV(VE, 4); break; \
+    case 2: CBK_KDEV(VE, 2); break; \
+    default: CBK_KDEV(VE, 1); break; \
   }
+  switch (ve) {
+    case 8: CBK_KDEV_SUB(8); break;
+    case 4: CBK_KDEV_SUB(4); break;
+    case 2: CBK_KDEV_SUB(2); break;
+    default: CBK_KDEV_SUB(1); break;
+  }
+#undef CBK_KDEV_SUB
 #undef CBK_KDEV
   return launch_status("kdev scores");
 }

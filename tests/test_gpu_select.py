@@ -136,6 +136,22 @@ def test_kdev_scores_vs_oracle(dtype):
     np.testing.assert_allclose(got.cpu().numpy(), O.kdev_scores(f[:1000], c[idx.numpy()]), rtol=SCORE_RTOL)
 
 
+@pytest.mark.parametrize("kv_heads,n", [(1, 1001), (2, 3001), (2, 5), (8, 999)])
+def test_kdev_scores_short_rows_share_a_wave(kv_heads, n):
+    """Rows of 1 or 2 KV heads x 128 bf16 (16 or 32 lanes' loads) take four
+    or two rows per wave pass; odd counts leave the last wave partly empty;
+    8 heads take two passes per row. Against the oracle, with gathered rows."""
+    fresh, cached, _ = synthetic.kdev_inputs(n, kv_heads, 128, torch.bfloat16, DEV, seed=kv_heads + n)
+    f = fresh.float().cpu().numpy()
+    c = cached.float().cpu().numpy()
+    got = S.kdev_scores(fresh, cached)
+    np.testing.assert_allclose(got.cpu().numpy(), O.kdev_scores(f, c), rtol=SCORE_RTOL, atol=0)
+    idx = torch.randperm(n)[: max(1, n // 3)]
+    got = S.kdev_scores(fresh[: idx.numel()], cached, idx.to(DEV))
+    np.testing.assert_allclose(got.cpu().numpy(), O.kdev_scores(f[: idx.numel()], c[idx.numpy()]),
+                               rtol=SCORE_RTOL, atol=0)
+
+
 def test_kdev_odd_width_and_strided_rows():
     torch.manual_seed(5)
     fresh = torch.randn(100, 77, device=DEV).to(torch.bfloat16)
