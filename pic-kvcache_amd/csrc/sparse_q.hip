@@ -593,10 +593,11 @@ __device__ __forceinline__ void colsum_mfma(const uint16_t* qlds, uint32_t hl, c
 
 // Software-pipelined over the unit's 4 head slots: the MFMAs of head hl + 1
 // are issued before the VALU work of head hl, which they do not depend on.
-// Slots past the group (nh < 4) compute on rows that are never used. FULL
-// (every chunk holds 4 heads, the group is a multiple of 4, or the unit is
-// four consecutive (tile, head) rows, T > 1): no branch inside the unit,
-// which the compiler then schedules as one block. With T > 1 slot hl holds
+// FULL (every slot holds rows: chunks of 4 heads when the group is a
+// multiple of 4, or four consecutive (tile, head) rows, T > 1; the kernel
+// is launched with nothing else): no branch inside the unit, which the
+// compiler then schedules as one block (without it, slots hl >= nh would be
+// skipped). With T > 1 slot hl holds
 // head (h0 + hl) mod G of the unit's tile (h0 + hl) / G (its first tile's
 // heads from h0 on, then the next tile's; rows past the last query tile
 // belong to empty tiles, whose positions are -1); MASK reads a slot's
@@ -661,7 +662,9 @@ __device__ __forceinline__ void colsum_unit(const SqArgs& a, const uint16_t* qld
 template <typename V, int KSTEPS, int RMODE, bool FULL, int T = 1, int G0 = 0>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void sq_colsum_kernel(
     const SqArgs a) {
-  static_assert(T == 1 || (FULL && (T == 2 || T == 4)), "units of rows are whole");
+  // every group size is launched with whole units: a multiple of 4 heads in
+  // chunks of 4, any other in units of four rows
+  static_assert(FULL && (T == 1 || T == 2 || T == 4), "units are whole");
   static_assert(G0 == 0 || G0 * T == kHeadChunk, "a compile-time group fills the unit's tiles");
   constexpr bool FLAT = T > 1;
   const uint32_t G = G0 ? uint32_t(G0) : a.groups;  // heads per KV head
@@ -744,8 +747,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   }
   const uint32_t toff = (T == 1 ? lane % kTileWords : lane) * 4;
   // wave 0's statistics request: 8 lanes (128 bytes) per head slot of the
-  // unit; with every chunk whole (FULL, T == 1) the lanes' offsets are the
-  // same each unit
+  // unit; for chunk units (T == 1) the lanes' offsets are the same each unit
   const uint32_t slot0 = (lane / 8) % kHeadChunk;
   const uint32_t soff_full = (slot0 * a.nq_pad + (lane % 8) * 2) * 8;
   // Issues unit qt (a tile's head chunk hc, or the four rows from 4 qt; a
@@ -773,10 +775,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 #pragma unroll
         for (int k = 1; k < T; ++k) ts += hs >= uint32_t(k) * G ? 1u : 0u;
         soff = ((hs - ts * G) * a.nq_pad + ts * kQTile + (lane % 8) * 2) * 8;
-      } else if constexpr (!FULL) {
-        const uint32_t nh = min(uint32_t(kHeadChunk), a.groups - hc * kHeadChunk);
-        const uint32_t hl = min((lane / 8) % kHeadChunk, nh - 1);  // heads past the chunk repeat its last
-        soff = (hl * a.nq_pad + (lane % 8) * 2) * 8;
       }
       lds_dma16(st, soff, lds_address(sbuf[B]));
       lds_dma4(a.tiles + kTileWords * t0, toff, lds_address(tbuf[B]));
