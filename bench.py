@@ -356,6 +356,8 @@ def _headline_scalars(r: dict) -> dict:
     put("sparse_q_ms", "sparse_q", "score_ms")
     put("sparse_q_ms_min", "sparse_q", "score_ms_min")
     put("sparse_q_mfma_frac", "sparse_q", "mfma_frac_of_bf16_peak")
+    put("sparse_q_qwen3_8b_ms", "sparse_q", "other_group_sizes", "qwen3_8b_32q_8kv", "ms")
+    put("sparse_q_qwen3_14b_ms", "sparse_q", "other_group_sizes", "qwen3_14b_40q_8kv", "ms")
     put("attention_ms", "blend_attention", "ms")
     put("attention_ms_min", "blend_attention", "ms_min")
     put("attention_mfma_frac", "blend_attention", "mfma_frac_of_bf16_peak")
@@ -461,6 +463,23 @@ def sparse_q(torch, S, synthetic, dev):
     # the kernel pair computes the logits twice (row statistics, then column
     # sums), reported separately as executed work
     achieved = flops_pass / (ms / 1e3) / 1e12
+    # the same positions at other query-head groupings of Qwen3 layers (a
+    # kernel variant per group size): 4 query heads per KV head (Qwen3-8B,
+    # 32 over 8), 5 (Qwen3-14B, 40 over 8), 2 (Qwen3-1.7B, 16 over 8)
+    del query, key
+    other_groups = {}
+    for name, ghq, ghkv in (("qwen3_8b_32q_8kv", 32, 8), ("qwen3_14b_40q_8kv", 40, 8),
+                            ("qwen3_1p7b_16q_8kv", 16, 8)):
+        gq = (torch.randn((nk, ghq, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+        gk = (torch.randn((nk, ghkv, d), generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+        gfn = lambda: S.sparse_q_full_scores(gq, gk, rows, absolute, scale, out_index=absolute)  # noqa: E731
+        for _ in range(8):
+            gfn()
+        gms = statistics.fmean([event_time_ms(torch, gfn, 3) for _ in range(3)])
+        gflops = 2.0 * d * ghq * float((pos + 1).sum())
+        other_groups[name] = {"ms": round(gms, 3),
+                              "mfma_frac_of_bf16_peak": round(gflops / (gms / 1e3) / 1e12 / 2500.0, 4)}
+        del gq, gk
     return {
         "queries": nq, "keys": nk, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
         "score_ms": round(ms, 3),
@@ -474,6 +493,7 @@ def sparse_q(torch, S, synthetic, dev):
         "exp_per_s": round(2 * hq * float((pos + 1).sum()) / (ms / 1e3), 1),
         "select_total_ms_with_masks_and_sync": round(total_ms, 3),
         "selected": int(selected.numel()),
+        "other_group_sizes": other_groups,
     }
 
 
