@@ -76,8 +76,9 @@ def _inputs(n_active, prefix, hq, hkv, d, dtype, seed):
     (torch.bfloat16, 64, 8, 8),
     (torch.float16, 128, 16, 2),
     (torch.float32, 32, 4, 2),
-    # head groups that leave a partial 4-head unit in the column pass (3, 6),
-    # one unit per tile (1) and four (16, the widest row-statistics path)
+    # column-pass units of 4 consecutive (tile, head) rows that span two
+    # tiles (3, 6) or four (1), and four 4-head units per tile (16, also the
+    # widest row-statistics path)
     (torch.bfloat16, 128, 12, 4),
     (torch.bfloat16, 64, 24, 4),
     (torch.float16, 64, 4, 4),
